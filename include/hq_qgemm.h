@@ -1,0 +1,132 @@
+/*
+ * hq_qgemm.h — C ABI of the MI355X (gfx950) weight-only quantized GEMM.
+ *
+ * Drop-in for hydrogen's Marlin-style qGEMM path. The reference surface is the
+ * C++ class hydrogen::MarlinGemmEngine (hydrogen/include/marlin_gemm.hpp:59-172,
+ * hydrogen/src/model/marlin_gemm.cu:381-758); each entry point below names the
+ * member it replaces. Differences from that surface, all required by the target
+ * operator (fp16/bf16 activations, fp16 group scales, fp32 accumulation):
+ *   - activations and outputs are fp16 or bf16 instead of fp32;
+ *   - scales are fp16 [K/group][N]; the zero point is fixed at 8 for int4, which is
+ *     the reference's bias = -8 * scale (marlin_gemm.cu:486-487), so no bias array;
+ *   - M is given per call and may be any value >= 1 (the reference's buffers fix a
+ *     maximum M and its kernels are only valid for M <= 8, marlin_gemm.cu:260);
+ *   - every call takes an explicit stream and returns a status instead of throwing
+ *     (the reference throws std::runtime_error from CUDA_CHECK, marlin_gemm.cu:19-27).
+ *
+ * Conventions. All pointers passed to hq_gemm_* and *_device calls are device
+ * pointers; hq_repack_* / hq_unpack_* without _device are host-to-host. The caller
+ * owns every buffer. Calls are thread-safe; a call returns after enqueueing its
+ * kernels on `stream` (a hipStream_t; NULL is the null stream). On error nothing is
+ * enqueued, the status is returned, and hq_last_error() describes it (per thread).
+ */
+#ifndef HQ_QGEMM_H
+#define HQ_QGEMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HQ_ABI_VERSION 1
+
+typedef enum hq_status {
+    HQ_OK = 0,
+    HQ_ERR_INVALID_ARG = 1,  /* null pointer, bad enum */
+    HQ_ERR_SHAPE = 2,        /* M, K, N, group or leading dimensions not supported */
+    HQ_ERR_ALIGNMENT = 3,    /* a pointer or leading dimension breaks the alignment rules */
+    HQ_ERR_UNSUPPORTED = 4,  /* valid request this build does not implement */
+    HQ_ERR_WORKSPACE = 5,    /* workspace missing or smaller than hq_workspace_bytes() */
+    HQ_ERR_BAD_CODE = 6,     /* ternary code 3 met while repacking */
+    HQ_ERR_DEVICE = 7,       /* HIP runtime error */
+    HQ_ERR_INTERNAL = 8
+} hq_status;
+
+typedef enum hq_dtype { HQ_DTYPE_F16 = 1, HQ_DTYPE_BF16 = 2 } hq_dtype;
+
+typedef enum hq_format {
+    HQ_FORMAT_INT4 = 1,      /* u32 [K/8][N], nibble i of word (kw, n) is k = 8*kw + i, code q in
+                                0..15, weight (q - 8) * scale (marlin_gemm.cu:495-512) */
+    HQ_FORMAT_TERNARY2 = 2   /* u32 [K/16][N], bits 2i..2i+1 of word (kw, n) hold c = t + 1 for
+                                k = 16*kw + i, t in {-1, 0, +1}, weight t * scale; c = 3 is invalid
+                                (value semantics of native_decoder.cu:81-102, 184-186) */
+} hq_format;
+
+typedef void* hq_stream; /* hipStream_t */
+
+/* One projection of a fused call: its own packed weight, scales, width and output. */
+typedef struct hq_segment {
+    const uint32_t* Wp;     /* packed (hq_repack_*) weight, device */
+    const uint16_t* scales; /* fp16 [K/group][N], device */
+    void* Y;                /* [M][ldy] output in the activation dtype, device */
+    int64_t ldy;            /* elements, >= N */
+    uint32_t N;
+} hq_segment;
+
+#define HQ_MAX_SEGMENTS 8
+
+/* ---- support ---- */
+const char* hq_version(void);
+/* Description of the last failure on the calling thread ("" if none). */
+const char* hq_last_error(void);
+const char* hq_status_string(hq_status s);
+
+/* Words of the reference linear layout: (K/8)*N for int4, (K/16)*N for ternary. */
+size_t hq_linear_words(hq_format fmt, uint32_t K, uint32_t N);
+/* Words of the gfx950 tile layout (N padded up to a multiple of 16). 0 on a bad shape. */
+size_t hq_packed_words(hq_format fmt, uint32_t K, uint32_t N);
+/* Device workspace a GEMM call of this shape needs (0 means none; pass NULL). */
+hq_status hq_workspace_bytes(hq_format fmt, uint32_t M, uint32_t K, uint32_t N, uint32_t group,
+                             size_t* bytes);
+
+/* ---- repack: replaces MarlinGemmEngine::repack_q4k_to_marlin (marlin_gemm.hpp:78-83) ---- */
+
+/* The reference's own "Marlin" layout, bit-exact with marlin_gemm.cu:446-455:
+ * dst[(kq*N + n)*4 + j] = src[(4*kq + j)*N + n], kq < K/32. Host to host, K % 32 == 0. */
+hq_status hq_repack_int4_ref(const uint32_t* src_linear, uint32_t* dst, uint32_t K, uint32_t N);
+
+/* Linear -> gfx950 tile layout (hq_packed_words words), host to host. K % 128 == 0. */
+hq_status hq_repack_int4(const uint32_t* src_linear, uint32_t* dst_packed, uint32_t K, uint32_t N);
+hq_status hq_repack_ternary2(const uint32_t* src_linear, uint32_t* dst_packed, uint32_t K, uint32_t N);
+/* Inverse of the above (padding columns dropped), host to host. */
+hq_status hq_unpack_int4(const uint32_t* packed, uint32_t* dst_linear, uint32_t K, uint32_t N);
+hq_status hq_unpack_ternary2(const uint32_t* packed, uint32_t* dst_linear, uint32_t K, uint32_t N);
+
+/* Same repacks on the device (one kernel, enqueued on `stream`). For ternary,
+ * d_bad_flag (a device uint32, may be NULL) is set to 1 if a code 3 was met; the
+ * caller zeroes it first and reads it after the stream completes. */
+hq_status hq_repack_int4_device(const uint32_t* d_src_linear, uint32_t* d_dst_packed, uint32_t K,
+                                uint32_t N, hq_stream stream);
+hq_status hq_repack_ternary2_device(const uint32_t* d_src_linear, uint32_t* d_dst_packed, uint32_t K,
+                                    uint32_t N, uint32_t* d_bad_flag, hq_stream stream);
+
+/* ---- forward: replaces MarlinGemmEngine::forward_marlin_int4 (marlin_gemm.hpp:100-107,
+ *      marlin_gemm.cu:556-601) ----
+ * Y[m, n] = sum_k X[m, k] * w(k, n), fp32 accumulation, Y rounded to the activation dtype.
+ * X: [M][ldx] fp16/bf16, 16-byte aligned, ldx % 8 == 0, ldx >= K.
+ * Wp: gfx950 packed weight, 16-byte aligned. scales: fp16 [K/group][N].
+ * Y: [M][ldy], 2-byte aligned, ldy >= N; written in full (no zero-fill needed).
+ * K % 128 == 0, group % 128 == 0, K % group == 0, M >= 1, N >= 1.
+ * Decode shapes (M <= 16) run the HBM-streaming kernel; larger M the MFMA tile kernel. */
+hq_status hq_gemm_w4a16(const void* X, hq_dtype dtype, int64_t ldx, const uint32_t* Wp,
+                        const uint16_t* scales, void* Y, int64_t ldy, uint32_t M, uint32_t K,
+                        uint32_t N, uint32_t group, void* workspace, size_t workspace_bytes,
+                        hq_stream stream);
+hq_status hq_gemm_w2a16(const void* X, hq_dtype dtype, int64_t ldx, const uint32_t* Wp,
+                        const uint16_t* scales, void* Y, int64_t ldy, uint32_t M, uint32_t K,
+                        uint32_t N, uint32_t group, void* workspace, size_t workspace_bytes,
+                        hq_stream stream);
+
+/* Fused projections sharing one activation read (QKV, gate||up): nseg segments of one
+ * format over the same X. Result equals one hq_gemm_* call per segment. Replaces the
+ * separate GEMV launches of native_decoder.cu:1113-1115, 1149-1150, 1178-1179. */
+hq_status hq_gemm_fused(const void* X, hq_dtype dtype, int64_t ldx, hq_format fmt,
+                        const hq_segment* segs, uint32_t nseg, uint32_t M, uint32_t K,
+                        uint32_t group, void* workspace, size_t workspace_bytes, hq_stream stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* HQ_QGEMM_H */

@@ -1,0 +1,320 @@
+// hq_api.cpp — the C ABI (include/hq_qgemm.h): argument validation, host repacks,
+// kernel dispatch and per-thread error strings. No exception crosses the ABI.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "hq_internal.hpp"
+#include "hq_layout.hpp"
+#include "hq_qgemm.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+hq_status fail(hq_status s, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return s;
+}
+
+hq_status ok() {
+  g_last_error.clear();
+  return HQ_OK;
+}
+
+hq_status from_hip(hipError_t e, const char* what) {
+  if (e == hipSuccess) return ok();
+  return fail(HQ_ERR_DEVICE, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool valid_fmt(int f) { return f == HQ_FORMAT_INT4 || f == HQ_FORMAT_TERNARY2; }
+bool valid_dtype(int d) { return d == HQ_DTYPE_F16 || d == HQ_DTYPE_BF16; }
+
+hq_status check_repack_shape(hq_format fmt, uint32_t K, uint32_t N) {
+  if (!valid_fmt(fmt)) return fail(HQ_ERR_INVALID_ARG, "unknown format %d", (int)fmt);
+  if (K == 0 || N == 0) return fail(HQ_ERR_SHAPE, "K=%u N=%u must be positive", K, N);
+  if (K % hq::kBlockK) return fail(HQ_ERR_SHAPE, "K=%u must be a multiple of 128", K);
+  return HQ_OK;
+}
+
+// Parallel-for over [0, n) on host threads (the repacks are memory-bound word gathers).
+template <class F>
+void parallel_for(size_t n, F f) {
+  unsigned nt = std::thread::hardware_concurrency();
+  if (nt == 0) nt = 1;
+  if (nt > 16) nt = 16;
+  if (n < (1u << 16) || nt == 1) {
+    f(0, n);
+    return;
+  }
+  std::vector<std::thread> th;
+  const size_t chunk = (n + nt - 1) / nt;
+  for (unsigned i = 0; i < nt; ++i) {
+    const size_t b = i * chunk, e = std::min(n, b + chunk);
+    if (b < e) th.emplace_back([=] { f(b, e); });
+  }
+  for (auto& t : th) t.join();
+}
+
+// Validation shared by the GEMM entry points.
+hq_status check_gemm_common(const void* X, int dtype, int64_t ldx, uint32_t M, uint32_t K,
+                            uint32_t group, void* ws, size_t ws_bytes) {
+  (void)ws;
+  (void)ws_bytes;
+  if (!X) return fail(HQ_ERR_INVALID_ARG, "X is null");
+  if (!valid_dtype(dtype)) return fail(HQ_ERR_INVALID_ARG, "unknown dtype %d", dtype);
+  if (M == 0) return fail(HQ_ERR_SHAPE, "M must be >= 1");
+  if (K == 0 || K % hq::kBlockK) return fail(HQ_ERR_SHAPE, "K=%u must be a positive multiple of 128", K);
+  if (group == 0 || group % hq::kBlockK)
+    return fail(HQ_ERR_SHAPE, "group=%u must be a positive multiple of 128", group);
+  if (K % group) return fail(HQ_ERR_SHAPE, "K=%u must be a multiple of group=%u", K, group);
+  if (ldx < (int64_t)K) return fail(HQ_ERR_SHAPE, "ldx=%lld < K=%u", (long long)ldx, K);
+  if (ldx % 8) return fail(HQ_ERR_ALIGNMENT, "ldx=%lld must be a multiple of 8 elements", (long long)ldx);
+  if (reinterpret_cast<uintptr_t>(X) % 16) return fail(HQ_ERR_ALIGNMENT, "X must be 16-byte aligned");
+  return HQ_OK;
+}
+
+hq_status check_segment(const hq_segment& s, uint32_t i) {
+  if (!s.Wp || !s.scales || !s.Y) return fail(HQ_ERR_INVALID_ARG, "segment %u: null pointer", i);
+  if (s.N == 0) return fail(HQ_ERR_SHAPE, "segment %u: N must be >= 1", i);
+  if (s.ldy < (int64_t)s.N) return fail(HQ_ERR_SHAPE, "segment %u: ldy=%lld < N=%u", i, (long long)s.ldy, s.N);
+  if (reinterpret_cast<uintptr_t>(s.Wp) % 16) return fail(HQ_ERR_ALIGNMENT, "segment %u: Wp must be 16-byte aligned", i);
+  if (reinterpret_cast<uintptr_t>(s.scales) % 2) return fail(HQ_ERR_ALIGNMENT, "segment %u: scales must be 2-byte aligned", i);
+  if (reinterpret_cast<uintptr_t>(s.Y) % 2) return fail(HQ_ERR_ALIGNMENT, "segment %u: Y must be 2-byte aligned", i);
+  return HQ_OK;
+}
+
+hq_status run_gemm(const void* X, hq_dtype dtype, int64_t ldx, hq_format fmt, const hq_segment* segs,
+                   uint32_t nseg, uint32_t M, uint32_t K, uint32_t group, void* ws, size_t ws_bytes,
+                   hq_stream stream) {
+  hq_status st = check_gemm_common(X, dtype, ldx, M, K, group, ws, ws_bytes);
+  if (st != HQ_OK) return st;
+  if (!valid_fmt(fmt)) return fail(HQ_ERR_INVALID_ARG, "unknown format %d", (int)fmt);
+  if (!segs || nseg == 0 || nseg > HQ_MAX_SEGMENTS)
+    return fail(HQ_ERR_INVALID_ARG, "need 1..%d segments, got %u", HQ_MAX_SEGMENTS, nseg);
+  hq::GemmDesc d{};
+  d.X = X;
+  d.ldx = ldx;
+  d.M = M;
+  d.K = K;
+  d.nkb = K / hq::kBlockK;
+  d.gkb = group / hq::kBlockK;
+  d.nseg = nseg;
+  for (uint32_t i = 0; i < nseg; ++i) {
+    if ((st = check_segment(segs[i], i)) != HQ_OK) return st;
+    d.seg[i].Wp = segs[i].Wp;
+    d.seg[i].S = segs[i].scales;
+    d.seg[i].Y = segs[i].Y;
+    d.seg[i].ldy = segs[i].ldy;
+    d.seg[i].N = segs[i].N;
+    d.seg[i].ntiles = hq::col_tiles(segs[i].N);
+  }
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  hipError_t e = M <= 16 ? hq::launch_decode(fmt, dtype, d, s) : hq::launch_prefill(fmt, dtype, d, s);
+  return from_hip(e, M <= 16 ? "decode launch" : "prefill launch");
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* hq_version(void) { return "nebula-hq 0.1.0 (gfx950)"; }
+
+const char* hq_last_error(void) { return g_last_error.c_str(); }
+
+const char* hq_status_string(hq_status s) {
+  switch (s) {
+    case HQ_OK: return "ok";
+    case HQ_ERR_INVALID_ARG: return "invalid argument";
+    case HQ_ERR_SHAPE: return "unsupported shape";
+    case HQ_ERR_ALIGNMENT: return "misaligned pointer or leading dimension";
+    case HQ_ERR_UNSUPPORTED: return "unsupported";
+    case HQ_ERR_WORKSPACE: return "workspace too small";
+    case HQ_ERR_BAD_CODE: return "invalid ternary code";
+    case HQ_ERR_DEVICE: return "device error";
+    case HQ_ERR_INTERNAL: return "internal error";
+  }
+  return "unknown status";
+}
+
+size_t hq_linear_words(hq_format fmt, uint32_t K, uint32_t N) {
+  if (fmt == HQ_FORMAT_INT4) return (size_t)(K / 8) * N;
+  if (fmt == HQ_FORMAT_TERNARY2) return (size_t)(K / 16) * N;
+  return 0;
+}
+
+size_t hq_packed_words(hq_format fmt, uint32_t K, uint32_t N) {
+  if (!valid_fmt(fmt) || K == 0 || N == 0 || K % hq::kBlockK) return 0;
+  return (size_t)hq::col_tiles(N) * (K / hq::kBlockK) * 64u * hq::words_per_lane(fmt);
+}
+
+hq_status hq_workspace_bytes(hq_format fmt, uint32_t M, uint32_t K, uint32_t N, uint32_t group, size_t* bytes) {
+  if (!bytes) return fail(HQ_ERR_INVALID_ARG, "bytes is null");
+  if (!valid_fmt(fmt)) return fail(HQ_ERR_INVALID_ARG, "unknown format %d", (int)fmt);
+  (void)M;
+  (void)K;
+  (void)N;
+  (void)group;
+  *bytes = 0;
+  return ok();
+}
+
+hq_status hq_repack_int4_ref(const uint32_t* src, uint32_t* dst, uint32_t K, uint32_t N) {
+  if (!src || !dst) return fail(HQ_ERR_INVALID_ARG, "null pointer");
+  if (K == 0 || N == 0 || K % 32) return fail(HQ_ERR_SHAPE, "K=%u must be a positive multiple of 32, N=%u > 0", K, N);
+  const uint32_t nkq = K / 32;
+  parallel_for(nkq, [=](size_t b, size_t e) {
+    for (size_t kq = b; kq < e; ++kq)
+      for (uint32_t n = 0; n < N; ++n) {
+        const size_t o = (kq * N + n) * 4;
+        for (uint32_t j = 0; j < 4; ++j) dst[o + j] = src[(4 * kq + j) * N + n];
+      }
+  });
+  return ok();
+}
+
+hq_status hq_repack_int4(const uint32_t* src, uint32_t* dst, uint32_t K, uint32_t N) {
+  if (!src || !dst) return fail(HQ_ERR_INVALID_ARG, "null pointer");
+  hq_status st = check_repack_shape(HQ_FORMAT_INT4, K, N);
+  if (st != HQ_OK) return st;
+  const uint32_t nkb = K / hq::kBlockK, nt = hq::col_tiles(N);
+  parallel_for((size_t)nt * nkb, [=](size_t b, size_t e) {
+    for (size_t blk = b; blk < e; ++blk) {
+      const uint32_t ct = (uint32_t)(blk / nkb), kb = (uint32_t)(blk % nkb);
+      uint32_t* o = dst + blk * 256;
+      for (uint32_t lane = 0; lane < 64; ++lane) {
+        const uint32_t n = ct * 16 + (lane & 15);
+        for (uint32_t w = 0; w < 4; ++w) {
+          const uint32_t lin = n < N ? src[(size_t)hq::int4_linear_kw(kb, lane, w) * N + n] : 0x88888888u;
+          o[lane * 4 + w] = hq::int4_linear_to_tile(lin);
+        }
+      }
+    }
+  });
+  return ok();
+}
+
+hq_status hq_unpack_int4(const uint32_t* packed, uint32_t* dst, uint32_t K, uint32_t N) {
+  if (!packed || !dst) return fail(HQ_ERR_INVALID_ARG, "null pointer");
+  hq_status st = check_repack_shape(HQ_FORMAT_INT4, K, N);
+  if (st != HQ_OK) return st;
+  const uint32_t nkb = K / hq::kBlockK, nt = hq::col_tiles(N);
+  parallel_for((size_t)nt * nkb, [=](size_t b, size_t e) {
+    for (size_t blk = b; blk < e; ++blk) {
+      const uint32_t ct = (uint32_t)(blk / nkb), kb = (uint32_t)(blk % nkb);
+      const uint32_t* p = packed + blk * 256;
+      for (uint32_t lane = 0; lane < 64; ++lane) {
+        const uint32_t n = ct * 16 + (lane & 15);
+        if (n >= N) continue;
+        for (uint32_t w = 0; w < 4; ++w)
+          dst[(size_t)hq::int4_linear_kw(kb, lane, w) * N + n] = hq::int4_tile_to_linear(p[lane * 4 + w]);
+      }
+    }
+  });
+  return ok();
+}
+
+hq_status hq_repack_ternary2(const uint32_t* src, uint32_t* dst, uint32_t K, uint32_t N) {
+  if (!src || !dst) return fail(HQ_ERR_INVALID_ARG, "null pointer");
+  hq_status st = check_repack_shape(HQ_FORMAT_TERNARY2, K, N);
+  if (st != HQ_OK) return st;
+  const uint32_t nkb = K / hq::kBlockK, nt = hq::col_tiles(N);
+  std::vector<char> bad_by_chunk(nt, 0);
+  char* badp = bad_by_chunk.data();
+  parallel_for(nt, [=](size_t b, size_t e) {
+    for (size_t ct = b; ct < e; ++ct) {
+      bool bad = false;
+      for (uint32_t kb = 0; kb < nkb; ++kb) {
+        uint32_t* o = dst + ((size_t)ct * nkb + kb) * 128;
+        for (uint32_t lane = 0; lane < 64; ++lane) {
+          const uint32_t n = (uint32_t)ct * 16 + (lane & 15), g4 = lane >> 4;
+          for (uint32_t w = 0; w < 2; ++w) {
+            uint32_t out = 0;
+            if (n < N) {
+              const size_t kw0 = (size_t)8 * kb + 4 * w + (g4 >> 1);
+              out = hq::tern_pack_word(src[kw0 * N + n], src[(kw0 + 2) * N + n], g4 & 1, &bad);
+            }
+            o[lane * 2 + w] = out;
+          }
+        }
+      }
+      badp[ct] = bad;
+    }
+  });
+  for (uint32_t i = 0; i < nt; ++i)
+    if (bad_by_chunk[i]) return fail(HQ_ERR_BAD_CODE, "ternary code 3 in column tile %u", i);
+  return ok();
+}
+
+hq_status hq_unpack_ternary2(const uint32_t* packed, uint32_t* dst, uint32_t K, uint32_t N) {
+  if (!packed || !dst) return fail(HQ_ERR_INVALID_ARG, "null pointer");
+  hq_status st = check_repack_shape(HQ_FORMAT_TERNARY2, K, N);
+  if (st != HQ_OK) return st;
+  const uint32_t nkb = K / hq::kBlockK;
+  // Each linear word (kw, n) gathers 8 codes from each of two packed words.
+  parallel_for((size_t)(K / 16), [=](size_t b, size_t e) {
+    for (size_t kw = b; kw < e; ++kw) {
+      for (uint32_t n = 0; n < N; ++n) {
+        uint32_t lin = 0;
+        for (uint32_t i = 0; i < 16; ++i) {
+          const uint32_t k = (uint32_t)kw * 16 + i;
+          const uint32_t kb = k / 128, r = k % 128, c = r / 32, g4 = (r % 32) / 8, el = r % 8;
+          const uint32_t lane = g4 * 16 + (n % 16), w = c >> 1, cw = c & 1;
+          const uint32_t word = packed[(((size_t)(n / 16) * nkb + kb) * 64 + lane) * 2 + w];
+          const uint32_t f = (word >> hq::tern_field_bit(cw, el)) & 3u;
+          lin |= hq::tern_field_to_c(f) << (2 * i);
+        }
+        dst[kw * N + n] = lin;
+      }
+    }
+  });
+  return ok();
+}
+
+hq_status hq_repack_int4_device(const uint32_t* src, uint32_t* dst, uint32_t K, uint32_t N, hq_stream stream) {
+  if (!src || !dst) return fail(HQ_ERR_INVALID_ARG, "null pointer");
+  hq_status st = check_repack_shape(HQ_FORMAT_INT4, K, N);
+  if (st != HQ_OK) return st;
+  return from_hip(hq::launch_repack_int4(src, dst, K, N, reinterpret_cast<hipStream_t>(stream)), "repack launch");
+}
+
+hq_status hq_repack_ternary2_device(const uint32_t* src, uint32_t* dst, uint32_t K, uint32_t N, uint32_t* bad,
+                                    hq_stream stream) {
+  if (!src || !dst) return fail(HQ_ERR_INVALID_ARG, "null pointer");
+  hq_status st = check_repack_shape(HQ_FORMAT_TERNARY2, K, N);
+  if (st != HQ_OK) return st;
+  return from_hip(hq::launch_repack_ternary2(src, dst, K, N, bad, reinterpret_cast<hipStream_t>(stream)),
+                  "repack launch");
+}
+
+hq_status hq_gemm_w4a16(const void* X, hq_dtype dtype, int64_t ldx, const uint32_t* Wp, const uint16_t* scales,
+                        void* Y, int64_t ldy, uint32_t M, uint32_t K, uint32_t N, uint32_t group, void* ws,
+                        size_t ws_bytes, hq_stream stream) {
+  hq_segment s{Wp, scales, Y, ldy, N};
+  return run_gemm(X, dtype, ldx, HQ_FORMAT_INT4, &s, 1, M, K, group, ws, ws_bytes, stream);
+}
+
+hq_status hq_gemm_w2a16(const void* X, hq_dtype dtype, int64_t ldx, const uint32_t* Wp, const uint16_t* scales,
+                        void* Y, int64_t ldy, uint32_t M, uint32_t K, uint32_t N, uint32_t group, void* ws,
+                        size_t ws_bytes, hq_stream stream) {
+  hq_segment s{Wp, scales, Y, ldy, N};
+  return run_gemm(X, dtype, ldx, HQ_FORMAT_TERNARY2, &s, 1, M, K, group, ws, ws_bytes, stream);
+}
+
+hq_status hq_gemm_fused(const void* X, hq_dtype dtype, int64_t ldx, hq_format fmt, const hq_segment* segs,
+                        uint32_t nseg, uint32_t M, uint32_t K, uint32_t group, void* ws, size_t ws_bytes,
+                        hq_stream stream) {
+  return run_gemm(X, dtype, ldx, fmt, segs, nseg, M, K, group, ws, ws_bytes, stream);
+}
+
+}  // extern "C"

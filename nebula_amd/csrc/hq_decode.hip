@@ -1,0 +1,240 @@
+// hq_decode.hip — memory-bound qGEMM for M <= 16 (decode), gfx950.
+//
+// Replaces kernel_marlin_gemm_int4_templated / _dynamic
+// (hydrogen/src/model/marlin_gemm.cu:130-237, 242-322). The reference gives each
+// thread one output column and does 32 x M scalar FMAs per 16-byte weight load,
+// then merges 16 fixed K-splits with fp32 atomics into a pre-zeroed Y. Here:
+//   * one wavefront streams T column tiles (16 columns each) over its K range, one
+//     fully coalesced wave load (1 KiB int4 / 512 B ternary) per tile and k-block;
+//   * weights are dequantised in registers straight into MFMA B fragments and
+//     multiplied against the activation rows (M padded to 16) with
+//     v_mfma_f32_16x16x32_{f16,bf16}: the k reduction happens inside the matrix core
+//     instead of lane-by-lane FMAs and shuffles;
+//   * the group scale multiplies the fp32 group sum once per (column, group);
+//   * WK wavefronts of a workgroup split K and are reduced through LDS in a fixed
+//     order, so the result is deterministic and Y needs no zero-fill or atomics.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdlib>
+
+#include "hq_device.hpp"
+#include "hq_internal.hpp"
+
+namespace hq {
+namespace {
+
+constexpr int kMaxWK = 8;
+
+template <int FMT>
+struct WTraits;
+template <>
+struct WTraits<HQ_FORMAT_INT4> {
+  using V = u4;
+  static constexpr uint32_t wpl = 4;
+};
+template <>
+struct WTraits<HQ_FORMAT_TERNARY2> {
+  using V = u2;
+  static constexpr uint32_t wpl = 2;
+};
+
+template <int FMT, int DT>
+__device__ __forceinline__ u4 dequant_chunk(const typename WTraits<FMT>::V& w, int c) {
+  if constexpr (FMT == HQ_FORMAT_INT4) {
+    if constexpr (DT == HQ_DTYPE_F16) return dq_int4_f16(w[c]);
+    else return dq_int4_bf16_biased(w[c]);
+  } else {
+    const uint32_t word = w[c >> 1];
+    return (c & 1) ? dq_tern2<1>(word) : dq_tern2<0>(word);
+  }
+}
+
+// Constant bf16 -1.5 in every B element: MFMA(x, this) = -1.5 * sum_k x over the chunk.
+constexpr uint32_t kBf16NegOneHalf2 = 0xBFC0BFC0u;
+
+template <int FMT, int DT, int T>
+__global__ void __launch_bounds__(64 * kMaxWK) hq_decode_kernel(const GemmDesc d, uint32_t kb_per_wave) {
+  using W = typename WTraits<FMT>::V;
+  constexpr uint32_t WPL = WTraits<FMT>::wpl;
+  constexpr bool kBiased = (FMT == HQ_FORMAT_INT4 && DT == HQ_DTYPE_BF16);
+  extern __shared__ float red[];
+
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t wave = threadIdx.x >> 6;
+  const uint32_t nwave = blockDim.x >> 6;
+  const uint32_t c16 = lane & 15u;
+  const uint32_t g4 = lane >> 4;
+
+  // Segment of this workgroup (segments are few; the scan is uniform).
+  uint32_t s = 0;
+#pragma unroll
+  for (uint32_t i = 1; i < HQ_MAX_SEGMENTS; ++i)
+    if (i < d.nseg && blockIdx.x >= d.seg[i].blk_begin) s = i;
+  const SegDesc sg = d.seg[s];
+  const uint32_t ct0 = (blockIdx.x - sg.blk_begin) * T;
+
+  const uint32_t kb0 = wave * kb_per_wave;
+  const uint32_t kb1 = min(d.nkb, kb0 + kb_per_wave);
+
+  // A operand: row c16 of X (rows >= M read as zero), k-slice g4 of each chunk.
+  const bool xrow_ok = c16 < d.M;
+  const char* xrow = reinterpret_cast<const char*>(d.X) + (size_t)c16 * (size_t)d.ldx * 2u + g4 * 16u;
+
+  const W* wbase[T];
+  bool tile_ok[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    const uint32_t ct = ct0 + t;
+    tile_ok[t] = ct < sg.ntiles;
+    wbase[t] = reinterpret_cast<const W*>(sg.Wp + ((size_t)ct * d.nkb) * 64u * WPL) + lane;
+  }
+
+  f4 acc[T], gacc[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    acc[t] = f4{0.f, 0.f, 0.f, 0.f};
+    gacc[t] = f4{0.f, 0.f, 0.f, 0.f};
+  }
+  f4 corr = f4{0.f, 0.f, 0.f, 0.f};
+
+  for (uint32_t kb = kb0; kb < kb1; ++kb) {
+    u4 a[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      a[c] = xrow_ok ? *reinterpret_cast<const u4*>(xrow + ((size_t)kb * 128u + c * 32u) * 2u)
+                     : u4{0u, 0u, 0u, 0u};
+    }
+    W wv[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      if (tile_ok[t]) wv[t] = __builtin_nontemporal_load(wbase[t] + (size_t)kb * 64u);
+    }
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      if (tile_ok[t]) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) gacc[t] = mfma16x16x32<DT>(a[c], dequant_chunk<FMT, DT>(wv[t], c), gacc[t]);
+      }
+    }
+    if constexpr (kBiased) {
+      const u4 neg = u4{kBf16NegOneHalf2, kBf16NegOneHalf2, kBf16NegOneHalf2, kBf16NegOneHalf2};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) corr = mfma16x16x32<DT>(a[c], neg, corr);
+    }
+    if ((kb + 1u) % d.gkb == 0u) {
+      const uint32_t grp = kb / d.gkb;
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        if (!tile_ok[t]) continue;
+        const uint32_t n = (ct0 + t) * 16u + c16;
+        float sc = n < sg.N ? f16_to_f32(sg.S[(size_t)grp * sg.N + n]) : 0.0f;
+        if constexpr (FMT == HQ_FORMAT_TERNARY2) {
+          // A non-finite block scale drops the block (native_decoder.cu:174); fields hold 2t.
+          sc = __builtin_isfinite(sc) ? 0.5f * sc : 0.0f;
+        }
+        if constexpr (kBiased) {
+          sc *= 16.0f;
+          gacc[t] += corr;
+        }
+        acc[t] += gacc[t] * sc;
+        gacc[t] = f4{0.f, 0.f, 0.f, 0.f};
+      }
+      corr = f4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+
+  // Output element e = (t * 4 + v) * 64 + ln: row 4 * (ln / 16) + v, column 16 * (ct0 + t) + ln % 16.
+  auto store = [&](uint32_t e, float val) {
+    const uint32_t t = e >> 8, v = (e >> 6) & 3u, ln = e & 63u;
+    const uint32_t row = 4u * (ln >> 4) + v;
+    const uint32_t n = (ct0 + t) * 16u + (ln & 15u);
+    if (row < d.M && n < sg.N && ct0 + t < sg.ntiles)
+      reinterpret_cast<uint16_t*>(sg.Y)[(size_t)row * sg.ldy + n] = f32_to_out<DT>(val);
+  };
+
+  if (nwave == 1) {
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) store((t * 4 + v) * 64 + lane, acc[t][v]);
+    return;
+  }
+  constexpr uint32_t per_wave = T * 4 * 64;
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) red[wave * per_wave + (t * 4 + v) * 64 + lane] = acc[t][v];
+  __syncthreads();
+  for (uint32_t e = threadIdx.x; e < per_wave; e += blockDim.x) {
+    float sum = 0.0f;
+    for (uint32_t w = 0; w < nwave; ++w) sum += red[w * per_wave + e];
+    store(e, sum);
+  }
+}
+
+struct DecodeConfig {
+  int T;
+  int WK;
+};
+
+int env_int(const char* name, int dflt) {
+  const char* v = std::getenv(name);
+  return v && *v ? std::atoi(v) : dflt;
+}
+
+// Tiling choice: enough wavefronts to cover 256 CUs several times over with long
+// enough streams per wavefront; T > 1 amortises the activation loads over more columns.
+DecodeConfig choose_decode(const GemmDesc& d) {
+  uint32_t tiles = 0;
+  for (uint32_t i = 0; i < d.nseg; ++i) tiles += d.seg[i].ntiles;
+  const uint32_t groups = d.nkb / d.gkb;
+  int T = tiles >= 2048 ? 2 : 1;
+  const uint32_t target_waves = 4096;
+  const uint32_t blocks = (tiles + T - 1) / T;
+  int WK = (int)std::min<uint32_t>(kMaxWK, std::max<uint32_t>(1, (target_waves + blocks - 1) / blocks));
+  WK = (int)std::min<uint32_t>((uint32_t)WK, groups);
+  const int eT = env_int("HQ_DECODE_T", 0), eWK = env_int("HQ_DECODE_WK", 0);
+  if (eT == 1 || eT == 2 || eT == 4) T = eT;
+  if (eWK >= 1 && eWK <= kMaxWK) WK = std::min<int>(eWK, (int)groups);
+  return {T, WK};
+}
+
+template <int FMT, int DT, int T>
+hipError_t launch_t(GemmDesc d, int WK, hipStream_t stream) {
+  uint32_t blk = 0;
+  for (uint32_t i = 0; i < d.nseg; ++i) {
+    d.seg[i].blk_begin = blk;
+    d.seg[i].blk_count = (d.seg[i].ntiles + T - 1) / T;
+    blk += d.seg[i].blk_count;
+  }
+  const uint32_t groups = d.nkb / d.gkb;
+  const uint32_t gpw = (groups + WK - 1) / WK;
+  const uint32_t kb_per_wave = gpw * d.gkb;
+  const size_t lds = WK > 1 ? (size_t)WK * T * 4 * 64 * sizeof(float) : 0;
+  hipLaunchKernelGGL((hq_decode_kernel<FMT, DT, T>), dim3(blk), dim3(64 * WK), lds, stream, d, kb_per_wave);
+  return hipGetLastError();
+}
+
+template <int FMT, int DT>
+hipError_t launch_fd(GemmDesc d, hipStream_t stream) {
+  const DecodeConfig cfg = choose_decode(d);
+  switch (cfg.T) {
+    case 4: return launch_t<FMT, DT, 4>(d, cfg.WK, stream);
+    case 2: return launch_t<FMT, DT, 2>(d, cfg.WK, stream);
+    default: return launch_t<FMT, DT, 1>(d, cfg.WK, stream);
+  }
+}
+
+}  // namespace
+
+hipError_t launch_decode(int fmt, int dtype, GemmDesc d, hipStream_t stream) {
+  if (fmt == HQ_FORMAT_INT4) {
+    return dtype == HQ_DTYPE_F16 ? launch_fd<HQ_FORMAT_INT4, HQ_DTYPE_F16>(d, stream)
+                                 : launch_fd<HQ_FORMAT_INT4, HQ_DTYPE_BF16>(d, stream);
+  }
+  return dtype == HQ_DTYPE_F16 ? launch_fd<HQ_FORMAT_TERNARY2, HQ_DTYPE_F16>(d, stream)
+                               : launch_fd<HQ_FORMAT_TERNARY2, HQ_DTYPE_BF16>(d, stream);
+}
+
+}  // namespace hq

@@ -1,0 +1,44 @@
+// hq_internal.hpp — descriptors shared by the C-ABI layer and the kernel launchers.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "hq_qgemm.h"
+
+namespace hq {
+
+// One projection inside a (possibly fused) launch. blk_begin is the first workgroup
+// (grid x index) that works on this segment; the launcher fills it.
+struct SegDesc {
+  const uint32_t* Wp;
+  const uint16_t* S;
+  void* Y;
+  int64_t ldy;
+  uint32_t N;
+  uint32_t ntiles;     // ceil(N / 16)
+  uint32_t blk_begin;  // first grid x index of this segment
+  uint32_t blk_count;  // grid x extent of this segment
+};
+
+struct GemmDesc {
+  const void* X;
+  int64_t ldx;
+  uint32_t M, K;
+  uint32_t nkb;  // K / 128
+  uint32_t gkb;  // group / 128
+  uint32_t nseg;
+  uint32_t pad;
+  SegDesc seg[HQ_MAX_SEGMENTS];
+};
+
+// Decode (M <= 16): HBM-streaming MFMA kernel. Validated descriptor in, status out.
+hipError_t launch_decode(int fmt, int dtype, GemmDesc d, hipStream_t stream);
+// Prefill (M > 16): MFMA tile kernel.
+hipError_t launch_prefill(int fmt, int dtype, GemmDesc d, hipStream_t stream);
+
+hipError_t launch_repack_int4(const uint32_t* src, uint32_t* dst, uint32_t K, uint32_t N,
+                              hipStream_t stream);
+hipError_t launch_repack_ternary2(const uint32_t* src, uint32_t* dst, uint32_t K, uint32_t N,
+                                  uint32_t* bad_flag, hipStream_t stream);
+
+}  // namespace hq

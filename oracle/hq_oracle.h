@@ -1,0 +1,83 @@
+/*
+ * hq_oracle.h — CPU restatement of hydrogen's weight-only quantized GEMM path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This library is the checker: tests, the smoke
+ * check and the CPU-baseline leg of the benchmark call it. Nothing in the
+ * product library (nebula_amd/) links or loads it.
+ *
+ * Every function restates one piece of the reference (paths relative to the
+ * reference repository root):
+ *   hqo_repack_ref        hydrogen/src/model/marlin_gemm.cu:432-467 (loop 446-455)
+ *   hqo_dequant_int4      hydrogen/src/model/marlin_gemm.cu:495-512 (w = q*s + b, b = -8*s, :483-488)
+ *   hqo_dequant_ternary2  hydrogen/src/model/native_decoder.cu:184-186 (w = d * t)
+ *   hqo_gemm_f32          hydrogen/src/model/marlin_gemm.cu:52-70 (fp32, k ascending, FMA)
+ *   hqo_qgemm             the two above fused row by row (bit-identical to running them in turn)
+ *   hqo_fidelity          hydrogen/src/model/marlin_gemm.cu:619-644 (max |d|, MSE in fp64)
+ *
+ * The generator (hqo_rng_*, hqo_gen_*) is this build's own specification, not
+ * the reference's: the reference seeds std::mt19937 with implementation-defined
+ * distributions (marlin_gemm.cu:470-472), which no other compiler reproduces.
+ *
+ * Numeric types cross this interface as raw IEEE bit patterns: uint16_t for
+ * fp16 and bf16, float for fp32.
+ */
+#ifndef HQ_ORACLE_H
+#define HQ_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum { HQO_F16 = 1, HQO_BF16 = 2 };
+enum { HQO_INT4 = 1, HQO_TERNARY2 = 2 };
+
+/* ---- counter-based generator: splitmix64 finaliser over (seed, stream, index) ---- */
+uint64_t hqo_rng_u64(uint64_t seed, uint64_t stream, uint64_t idx);
+/* Uniform double in (0, 1]: ((r >> 11) + 1) * 2^-53. */
+double hqo_rng_uniform(uint64_t seed, uint64_t stream, uint64_t idx);
+/* N(0, sigma) by Box-Muller on draws (2i, 2i+1); |.| when absval != 0; rounded (RNE) to dtype. */
+void hqo_gen_normal(uint64_t seed, uint64_t stream, double sigma, int absval, int dtype,
+                    uint16_t* out, size_t n);
+/* int4 codes uniform on {0..15}: u32 [K/8][N], nibble i of word (kw, n) is k = 8*kw + i. */
+void hqo_gen_int4_linear(uint64_t seed, uint64_t stream, uint32_t* out, uint32_t K, uint32_t N);
+/* Ternary t in {-1,0,+1} with P = {0.25, 0.5, 0.25}: u32 [K/16][N], bits 2i..2i+1 hold c = t + 1
+ * for k = 16*kw + i. */
+void hqo_gen_ternary2_linear(uint64_t seed, uint64_t stream, uint32_t* out, uint32_t K, uint32_t N);
+
+/* ---- IEEE conversions (round to nearest even), written from the format definitions ---- */
+uint16_t hqo_f32_to_f16(float f);
+float hqo_f16_to_f32(uint16_t h);
+uint16_t hqo_f32_to_bf16(float f);
+float hqo_bf16_to_f32(uint16_t h);
+void hqo_to_f32(const uint16_t* in, int dtype, float* out, size_t n);
+void hqo_from_f32(const float* in, int dtype, uint16_t* out, size_t n);
+
+/* ---- the reference algorithm ---- */
+/* marlin_gemm.cu:446-455: dst[(kq*N + n)*4 + j] = src[(4*kq + j)*N + n], kq < K/32, j < 4. */
+void hqo_repack_ref(const uint32_t* src_linear, uint32_t* dst, uint32_t K, uint32_t N);
+/* marlin_gemm.cu:495-512 with scale = fp16 scale widened to fp32, bias = -8 * scale:
+ * Wdq[k*N + n] = (float)q * scale + bias, evaluated without contraction. */
+void hqo_dequant_int4(const uint32_t* w_linear, const uint16_t* scales_f16, uint32_t K, uint32_t N,
+                      uint32_t group, float* wdq);
+/* native_decoder.cu:184-186: Wdq[k*N + n] = scale * (float)t, t = c - 1. Returns -1 if a code 3 is present. */
+int hqo_dequant_ternary2(const uint32_t* w_linear, const uint16_t* scales_f16, uint32_t K, uint32_t N,
+                         uint32_t group, float* wdq);
+/* marlin_gemm.cu:60-69: Y[m*N + n] = sum_k X[m*K + k] * W[k*N + n], fp32, FMA, k ascending. */
+void hqo_gemm_f32(const float* X, const float* W, float* Y, uint32_t M, uint32_t K, uint32_t N,
+                  int threads);
+/* Dequantize-then-matmul over fp16/bf16 activation bits. X is [M][ldx] (elements), Y is fp32 [M][N].
+ * Bit-identical to hqo_dequant_* followed by hqo_gemm_f32 on the widened activations.
+ * Returns -1 on an invalid ternary code, 0 otherwise. */
+int hqo_qgemm(const uint16_t* X, int xdtype, size_t ldx, int fmt, const uint32_t* w_linear,
+              const uint16_t* scales_f16, uint32_t M, uint32_t K, uint32_t N, uint32_t group,
+              float* Y, int threads);
+/* marlin_gemm.cu:619-644: max |a - b| and mean squared difference, accumulated in fp64. */
+void hqo_fidelity(const float* a, const float* b, size_t count, double* max_abs, double* mse);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

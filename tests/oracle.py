@@ -1,0 +1,181 @@
+"""ctypes binding of the CPU oracle (oracle/liboracle_hq.so) — test infrastructure only."""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent.parent
+ORACLE_DIR = ROOT / "oracle"
+ORACLE_LIB = Path(os.environ.get("HQO_LIB", ORACLE_DIR / "liboracle_hq.so"))
+
+F16, BF16 = 1, 2
+INT4, TERNARY2 = 1, 2
+
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not ORACLE_LIB.exists():
+        subprocess.run(["make", "-C", str(ORACLE_DIR), "-s"], check=True)
+    L = ctypes.CDLL(str(ORACLE_LIB))
+    u64, u32, u16, vp, sz, i32, dbl, f32 = (ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint16, ctypes.c_void_p,
+                                             ctypes.c_size_t, ctypes.c_int, ctypes.c_double, ctypes.c_float)
+    L.hqo_rng_u64.restype = u64
+    L.hqo_rng_u64.argtypes = [u64, u64, u64]
+    L.hqo_rng_uniform.restype = dbl
+    L.hqo_rng_uniform.argtypes = [u64, u64, u64]
+    L.hqo_gen_normal.argtypes = [u64, u64, dbl, i32, i32, vp, sz]
+    L.hqo_gen_int4_linear.argtypes = [u64, u64, vp, u32, u32]
+    L.hqo_gen_ternary2_linear.argtypes = [u64, u64, vp, u32, u32]
+    L.hqo_f32_to_f16.restype = u16
+    L.hqo_f32_to_f16.argtypes = [f32]
+    L.hqo_f16_to_f32.restype = f32
+    L.hqo_f16_to_f32.argtypes = [u16]
+    L.hqo_f32_to_bf16.restype = u16
+    L.hqo_f32_to_bf16.argtypes = [f32]
+    L.hqo_bf16_to_f32.restype = f32
+    L.hqo_bf16_to_f32.argtypes = [u16]
+    L.hqo_to_f32.argtypes = [vp, i32, vp, sz]
+    L.hqo_from_f32.argtypes = [vp, i32, vp, sz]
+    L.hqo_repack_ref.argtypes = [vp, vp, u32, u32]
+    L.hqo_dequant_int4.argtypes = [vp, vp, u32, u32, u32, vp]
+    L.hqo_dequant_ternary2.restype = i32
+    L.hqo_dequant_ternary2.argtypes = [vp, vp, u32, u32, u32, vp]
+    L.hqo_gemm_f32.argtypes = [vp, vp, vp, u32, u32, u32, i32]
+    L.hqo_qgemm.restype = i32
+    L.hqo_qgemm.argtypes = [vp, i32, sz, i32, vp, vp, u32, u32, u32, u32, vp, i32]
+    L.hqo_fidelity.argtypes = [vp, vp, sz, ctypes.POINTER(dbl), ctypes.POINTER(dbl)]
+    _lib = L
+    return L
+
+
+def _p(a: np.ndarray) -> int:
+    assert a.flags["C_CONTIGUOUS"], "oracle arrays must be contiguous"
+    return a.ctypes.data
+
+
+def gen_normal(seed: int, stream: int, n: int, sigma: float = 1.0, absval: bool = False, dtype: int = F16) -> np.ndarray:
+    out = np.empty(n, dtype=np.uint16)
+    lib().hqo_gen_normal(seed, stream, sigma, int(absval), dtype, _p(out), n)
+    return out
+
+
+def gen_int4(seed: int, stream: int, K: int, N: int) -> np.ndarray:
+    out = np.empty((K // 8) * N, dtype=np.uint32)
+    lib().hqo_gen_int4_linear(seed, stream, _p(out), K, N)
+    return out
+
+
+def gen_ternary(seed: int, stream: int, K: int, N: int) -> np.ndarray:
+    out = np.empty((K // 16) * N, dtype=np.uint32)
+    lib().hqo_gen_ternary2_linear(seed, stream, _p(out), K, N)
+    return out
+
+
+def to_f32(bits: np.ndarray, dtype: int) -> np.ndarray:
+    bits = np.ascontiguousarray(bits, dtype=np.uint16)
+    out = np.empty(bits.shape, dtype=np.float32)
+    lib().hqo_to_f32(_p(bits), dtype, _p(out), bits.size)
+    return out
+
+
+def from_f32(x: np.ndarray, dtype: int) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    lib().hqo_from_f32(_p(x), dtype, _p(out), x.size)
+    return out
+
+
+def repack_ref(linear: np.ndarray, K: int, N: int) -> np.ndarray:
+    src = np.ascontiguousarray(linear, dtype=np.uint32)
+    dst = np.empty(src.size, dtype=np.uint32)
+    lib().hqo_repack_ref(_p(src), _p(dst), K, N)
+    return dst
+
+
+def dequant(fmt: int, linear: np.ndarray, scales: np.ndarray, K: int, N: int, group: int) -> np.ndarray:
+    w = np.ascontiguousarray(linear, dtype=np.uint32)
+    s = np.ascontiguousarray(scales, dtype=np.uint16)
+    out = np.empty((K, N), dtype=np.float32)
+    if fmt == INT4:
+        lib().hqo_dequant_int4(_p(w), _p(s), K, N, group, _p(out))
+    else:
+        if lib().hqo_dequant_ternary2(_p(w), _p(s), K, N, group, _p(out)) != 0:
+            raise ValueError("ternary code 3 in weight")
+    return out
+
+
+def gemm_f32(X: np.ndarray, W: np.ndarray, threads: int = 8) -> np.ndarray:
+    X = np.ascontiguousarray(X, dtype=np.float32)
+    W = np.ascontiguousarray(W, dtype=np.float32)
+    M, K = X.shape
+    K2, N = W.shape
+    assert K == K2
+    Y = np.empty((M, N), dtype=np.float32)
+    lib().hqo_gemm_f32(_p(X), _p(W), _p(Y), M, K, N, threads)
+    return Y
+
+
+def qgemm(fmt: int, X_bits: np.ndarray, xdtype: int, linear: np.ndarray, scales: np.ndarray, N: int,
+          group: int = 128, threads: int = 8) -> np.ndarray:
+    """Reference dequantize-then-matmul: fp32 Y[M, N] from fp16/bf16 activation bits [M, K]."""
+    X = np.ascontiguousarray(X_bits, dtype=np.uint16)
+    M, K = X.shape
+    w = np.ascontiguousarray(linear, dtype=np.uint32)
+    s = np.ascontiguousarray(scales, dtype=np.uint16)
+    Y = np.empty((M, N), dtype=np.float32)
+    rc = lib().hqo_qgemm(_p(X), xdtype, K, fmt, _p(w), _p(s), M, K, N, group, _p(Y), threads)
+    if rc == -1:
+        raise ValueError("ternary code 3 in weight")
+    if rc != 0:
+        raise MemoryError("oracle allocation failed")
+    return Y
+
+
+def fidelity(a: np.ndarray, b: np.ndarray) -> tuple[float, float]:
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    b = np.ascontiguousarray(b, dtype=np.float32)
+    mx, mse = ctypes.c_double(), ctypes.c_double()
+    lib().hqo_fidelity(_p(a), _p(b), a.size, ctypes.byref(mx), ctypes.byref(mse))
+    return mx.value, mse.value
+
+
+# ------------------------------------------------------------ problem builder
+class Problem:
+    """Seeded synthetic inputs of one qGEMM case (the distributions of the benchmark configs)."""
+
+    def __init__(self, fmt: int, M: int, K: int, N: int, group: int = 128, xdtype: int = F16, seed: int = 42,
+                 x_sigma: float = 1.0, s_sigma: float = 0.02):
+        self.fmt, self.M, self.K, self.N, self.group, self.xdtype, self.seed = fmt, M, K, N, group, xdtype, seed
+        self.X = gen_normal(seed, 1, M * K, x_sigma, False, xdtype).reshape(M, K)
+        self.scales = gen_normal(seed, 2, (K // group) * N, s_sigma, True, F16).reshape(K // group, N)
+        self.W = gen_int4(seed, 3, K, N) if fmt == INT4 else gen_ternary(seed, 3, K, N)
+
+    def reference(self, rows=None, threads: int = 8) -> np.ndarray:
+        X = self.X if rows is None else self.X[rows]
+        return qgemm(self.fmt, X, self.xdtype, self.W, self.scales, self.N, self.group, threads)
+
+
+def normwise_error(y: np.ndarray, r: np.ndarray) -> float:
+    """max |y - r| / max |r| — the acceptance metric (tolerance 1e-2)."""
+    y = np.asarray(y, dtype=np.float64)
+    r = np.asarray(r, dtype=np.float64)
+    denom = np.max(np.abs(r))
+    return float(np.max(np.abs(y - r)) / denom) if denom > 0 else float(np.max(np.abs(y - r)))
+
+
+def elementwise_error(y: np.ndarray, r: np.ndarray, floor_frac: float = 1e-2) -> tuple[float, int]:
+    """max |y - r| / |r| over |r| >= floor_frac * rms(r), and how many elements fall below the floor."""
+    y = np.asarray(y, dtype=np.float64)
+    r = np.asarray(r, dtype=np.float64)
+    floor = floor_frac * np.sqrt(np.mean(r * r))
+    m = np.abs(r) >= floor
+    rel = np.abs(y[m] - r[m]) / np.abs(r[m]) if m.any() else np.zeros(1)
+    return float(rel.max()), int((~m).sum())

@@ -1,0 +1,195 @@
+"""CPU tests of the C ABI: the library loads, exports what include/hq_qgemm.h declares,
+rejects bad arguments before touching a device, and its host repacks are bijections
+whose reference layout is bit-exact with the oracle's restatement of
+hydrogen/src/model/marlin_gemm.cu:446-455."""
+import ctypes
+import re
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle as O
+from nebula_amd import hq
+
+ROOT = Path(__file__).resolve().parent.parent
+
+
+def header_functions():
+    text = (ROOT / "include" / "hq_qgemm.h").read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(hq_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    L = hq.lib()
+    declared = header_functions()
+    assert declared == sorted(hq.EXPORTS)
+    for name in declared:
+        assert hasattr(L, name), name
+    assert "gfx950" in hq.version()
+
+
+def test_status_strings():
+    L = hq.lib()
+    assert L.hq_status_string(0) == b"ok"
+    assert L.hq_status_string(6) == b"invalid ternary code"
+
+
+def test_sizes():
+    assert hq.linear_words(hq.FORMAT_INT4, 4096, 4096) == 512 * 4096
+    assert hq.linear_words(hq.FORMAT_TERNARY2, 5120, 27648) == 320 * 27648
+    assert hq.packed_words(hq.FORMAT_INT4, 4096, 4096) == 4096 * 4096 // 8
+    assert hq.packed_words(hq.FORMAT_INT4, 128, 17) == 2 * 256  # N padded to 32
+    assert hq.packed_words(hq.FORMAT_TERNARY2, 256, 16) == 2 * 128
+    assert hq.packed_words(hq.FORMAT_INT4, 100, 16) == 0
+    b = ctypes.c_size_t(99)
+    assert hq.lib().hq_workspace_bytes(1, 16, 4096, 4096, 128, ctypes.byref(b)) == 0 and b.value == 0
+
+
+# ---------------------------------------------------------------- validation (no device work)
+def call_gemm(X=0x1000, dtype=1, ldx=4096, Wp=0x2000, S=0x3000, Y=0x4000, ldy=4096, M=16, K=4096, N=4096, g=128,
+              fn="hq_gemm_w4a16"):
+    return getattr(hq.lib(), fn)(X, dtype, ldx, Wp, S, Y, ldy, M, K, N, g, None, 0, None)
+
+
+@pytest.mark.parametrize("kw,status", [
+    (dict(X=0), hq.HQ_ERR_INVALID_ARG),
+    (dict(Wp=0), hq.HQ_ERR_INVALID_ARG),
+    (dict(S=0), hq.HQ_ERR_INVALID_ARG),
+    (dict(Y=0), hq.HQ_ERR_INVALID_ARG),
+    (dict(dtype=3), hq.HQ_ERR_INVALID_ARG),
+    (dict(M=0), hq.HQ_ERR_SHAPE),
+    (dict(N=0), hq.HQ_ERR_SHAPE),
+    (dict(K=4000, ldx=4000), hq.HQ_ERR_SHAPE),
+    (dict(g=64), hq.HQ_ERR_SHAPE),
+    (dict(g=96), hq.HQ_ERR_SHAPE),
+    (dict(K=384, ldx=384, g=256), hq.HQ_ERR_SHAPE),
+    (dict(ldx=4000), hq.HQ_ERR_SHAPE),
+    (dict(ldy=100), hq.HQ_ERR_SHAPE),
+    (dict(ldx=4100), hq.HQ_ERR_ALIGNMENT),
+    (dict(X=0x1008), hq.HQ_ERR_ALIGNMENT),
+    (dict(Wp=0x2004), hq.HQ_ERR_ALIGNMENT),
+    (dict(S=0x3001), hq.HQ_ERR_ALIGNMENT),
+    (dict(Y=0x4001), hq.HQ_ERR_ALIGNMENT),
+])
+def test_gemm_rejects_bad_arguments(kw, status):
+    for fn in ("hq_gemm_w4a16", "hq_gemm_w2a16"):
+        assert call_gemm(fn=fn, **kw) == status
+        assert hq.lib().hq_last_error().decode()
+
+
+def test_fused_rejects_bad_segments():
+    L = hq.lib()
+    segs = (hq.Segment * 9)()
+    for i in range(9):
+        segs[i] = hq.Segment(0x2000, 0x3000, 0x4000, 64, 64)
+    assert L.hq_gemm_fused(0x1000, 1, 4096, 1, segs, 0, 16, 4096, 128, None, 0, None) == hq.HQ_ERR_INVALID_ARG
+    assert L.hq_gemm_fused(0x1000, 1, 4096, 1, segs, 9, 16, 4096, 128, None, 0, None) == hq.HQ_ERR_INVALID_ARG
+    assert L.hq_gemm_fused(0x1000, 1, 4096, 7, segs, 2, 16, 4096, 128, None, 0, None) == hq.HQ_ERR_INVALID_ARG
+    segs[1] = hq.Segment(0x2000, 0x3000, 0x4000, 10, 64)
+    assert L.hq_gemm_fused(0x1000, 1, 4096, 1, segs, 2, 16, 4096, 128, None, 0, None) == hq.HQ_ERR_SHAPE
+    assert "segment 1" in L.hq_last_error().decode()
+
+
+def test_last_error_is_per_thread():
+    import threading
+
+    assert call_gemm(M=0) == hq.HQ_ERR_SHAPE
+    seen = {}
+
+    def other():
+        seen["msg"] = hq.lib().hq_last_error().decode()
+
+    t = threading.Thread(target=other)
+    t.start()
+    t.join()
+    assert seen["msg"] == "" and hq.lib().hq_last_error().decode() != ""
+
+
+def test_device_repack_rejects_bad_shapes():
+    L = hq.lib()
+    assert L.hq_repack_int4_device(0x1000, 0x2000, 100, 16, None) == hq.HQ_ERR_SHAPE
+    assert L.hq_repack_ternary2_device(0, 0x2000, 128, 16, None, None) == hq.HQ_ERR_INVALID_ARG
+
+
+# ---------------------------------------------------------------- host repacks
+def test_repack_int4_ref_bit_exact_with_oracle():
+    for K, N in [(32, 1), (128, 17), (4096, 64), (512, 300)]:
+        src = O.gen_int4(5, 1, K, N)
+        assert np.array_equal(hq.repack_int4_ref(src, K, N), O.repack_ref(src, K, N))
+
+
+@pytest.mark.parametrize("K,N", [(128, 16), (128, 17), (256, 40), (1024, 3), (5120, 64)])
+def test_int4_tile_layout_round_trip_and_to_ref(K, N):
+    src = O.gen_int4(6, 1, K, N)
+    packed = hq.repack(hq.FORMAT_INT4, src, K, N)
+    assert packed.size == hq.packed_words(hq.FORMAT_INT4, K, N)
+    back = hq.unpack(hq.FORMAT_INT4, packed, K, N)
+    assert np.array_equal(back, src)
+    # to_ref: the tile layout maps back to the reference "Marlin" layout bit for bit
+    assert np.array_equal(hq.repack_int4_ref(back, K, N), O.repack_ref(src, K, N))
+
+
+def test_int4_tile_layout_semantics():
+    # Lane l of block (ct, kb), word c, element e: column 16*ct + l%16, k = 128*kb + 32*c + 8*(l//16) + e,
+    # nibble position {0,4,1,5,2,6,3,7}[e].
+    K, N = 256, 32
+    q = np.random.default_rng(3).integers(0, 16, size=(K, N), dtype=np.uint32)
+    lin = np.bitwise_or.reduce(q.reshape(K // 8, 8, N) << (4 * np.arange(8, dtype=np.uint32))[None, :, None], axis=1)
+    packed = hq.repack(hq.FORMAT_INT4, lin.astype(np.uint32).ravel(), K, N).reshape(N // 16, K // 128, 64, 4)
+    pos = [0, 4, 1, 5, 2, 6, 3, 7]
+    for ct in range(N // 16):
+        for kb in range(K // 128):
+            for lane in (0, 5, 17, 63):
+                for c in range(4):
+                    for e in range(8):
+                        k = 128 * kb + 32 * c + 8 * (lane // 16) + e
+                        got = (packed[ct, kb, lane, c] >> (4 * pos[e])) & 0xF
+                        assert got == q[k, 16 * ct + lane % 16]
+
+
+def test_int4_padding_columns_decode_to_zero():
+    K, N = 128, 20
+    packed = hq.repack(hq.FORMAT_INT4, O.gen_int4(1, 1, K, N), K, N).reshape(2, 1, 64, 4)
+    pad_lanes = [l for l in range(64) if 16 + l % 16 >= N]
+    assert np.all(packed[1, 0, pad_lanes, :] == 0x88888888)
+
+
+@pytest.mark.parametrize("K,N", [(128, 16), (256, 17), (512, 48), (5120, 40)])
+def test_ternary_tile_layout_round_trip(K, N):
+    src = O.gen_ternary(8, 1, K, N)
+    packed = hq.repack(hq.FORMAT_TERNARY2, src, K, N)
+    assert packed.size == hq.packed_words(hq.FORMAT_TERNARY2, K, N)
+    assert np.array_equal(hq.unpack(hq.FORMAT_TERNARY2, packed, K, N), src)
+
+
+def test_ternary_tile_layout_semantics():
+    # (word << 2a) & 0xC000C000 must give the fp16/bf16 bits of 2t for elements (2h, 2h+1)
+    # of chunk 2w + a//4 (a = 4*cw + h), lane column 16*ct + l%16.
+    K, N = 256, 16
+    t = np.random.default_rng(4).choice([-1, 0, 1], size=(K, N))
+    c = (t + 1).astype(np.uint32)
+    lin = np.bitwise_or.reduce(c.reshape(K // 16, 16, N) << (2 * np.arange(16, dtype=np.uint32))[None, :, None], axis=1)
+    packed = hq.repack(hq.FORMAT_TERNARY2, lin.astype(np.uint32).ravel(), K, N).reshape(1, K // 128, 64, 2)
+    val = {0x0000: 0, 0x4000: 2, 0xC000: -2}
+    for kb in range(K // 128):
+        for lane in range(64):
+            for w in range(2):
+                word = int(packed[0, kb, lane, w])
+                for a in range(8):
+                    v = ((word << (2 * a)) & 0xC000C000) & 0xFFFFFFFF
+                    cw, h = divmod(a, 4)
+                    chunk = 2 * w + cw
+                    for half, e in ((v & 0xFFFF, 2 * h), (v >> 16, 2 * h + 1)):
+                        k = 128 * kb + 32 * chunk + 8 * (lane // 16) + e
+                        assert val[half] == 2 * t[k, lane % 16]
+
+
+def test_ternary_repack_rejects_code_3():
+    K, N = 128, 16
+    src = O.gen_ternary(9, 1, K, N)
+    src[3] |= 3 << 10
+    with pytest.raises(hq.HQError) as ei:
+        hq.repack(hq.FORMAT_TERNARY2, src, K, N)
+    assert ei.value.status == hq.HQ_ERR_BAD_CODE

@@ -1,0 +1,188 @@
+"""GPU parity of the HIP qGEMM against the CPU oracle, called through the C ABI.
+
+Bar (north star): normwise max relative error <= 1e-2 with fp32 accumulation on both
+sides; the integer/byte work (repacks) is bit-exact. Outputs are additionally held to
+their own rounding: fp16 outputs carry <= 2^-11 relative rounding, bf16 <= 2^-8, so
+the normwise error must also stay under OUT_TOL[dtype], which a layout or scale bug
+cannot meet.
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from gpu_util import DeviceProblem, assert_parity, to_dev_u16, to_dev_u32, to_host_f32
+from nebula_amd import hq
+
+pytestmark = pytest.mark.gpu
+
+OUT_TOL = {O.F16: 2e-3, O.BF16: 8e-3}
+BAR = 1e-2
+
+
+def check(y, ref, xdtype, label):
+    err = assert_parity(y, ref, BAR, label)
+    assert err <= OUT_TOL[xdtype], f"{label}: normwise {err:.3e} above output-rounding bound {OUT_TOL[xdtype]}"
+    el, below = O.elementwise_error(to_host_f32(y), ref)
+    assert el <= BAR, f"{label}: elementwise {el:.3e} over the 1%-rms floor ({below} below)"
+    return err
+
+
+def test_config0_w4a16_m16_4096(cuda):
+    # Config 0: M=16, K=N=4096, int4 zero point 8, g=128, fp16 in/out.
+    P = O.Problem(O.INT4, 16, 4096, 4096, 128, O.F16, seed=42)
+    D = DeviceProblem(P)
+    check(D.run(), P.reference(), O.F16, "c0")
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4, 5, 8, 11, 16])
+def test_decode_m_sweep_int4_f16(cuda, M):
+    P = O.Problem(O.INT4, M, 5120, 5120, 128, O.F16, seed=100 + M)
+    check(DeviceProblem(P).run(), P.reference(), O.F16, f"int4 f16 M={M}")
+
+
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_decode_int4_bf16(cuda, M):
+    P = O.Problem(O.INT4, M, 2048, 1536, 128, O.BF16, seed=200 + M)
+    check(DeviceProblem(P).run(), P.reference(), O.BF16, f"int4 bf16 M={M}")
+
+
+@pytest.mark.parametrize("M", [1, 8])
+def test_config2_ternary_bf16(cuda, M):
+    # Config 2: ternary {-1,0,1} p={.25,.5,.25}, K=5120, N=27648, bf16 activations.
+    P = O.Problem(O.TERNARY2, M, 5120, 27648, 128, O.BF16, seed=300 + M)
+    check(DeviceProblem(P).run(), P.reference(), O.BF16, f"ternary bf16 M={M}")
+
+
+@pytest.mark.parametrize("M", [1, 16])
+def test_decode_ternary_f16(cuda, M):
+    P = O.Problem(O.TERNARY2, M, 1024, 2048, 128, O.F16, seed=310 + M)
+    check(DeviceProblem(P).run(), P.reference(), O.F16, f"ternary f16 M={M}")
+
+
+@pytest.mark.parametrize("K,N", [(5120, 27648), (27648, 5120)])
+def test_config1_large_shapes_m16(cuda, K, N):
+    P = O.Problem(O.INT4, 16, K, N, 128, O.F16, seed=400)
+    check(DeviceProblem(P).run(), P.reference(threads=16), O.F16, f"c1 {K}x{N}")
+
+
+@pytest.mark.parametrize("fmt,xdt", [(O.INT4, O.F16), (O.INT4, O.BF16), (O.TERNARY2, O.F16), (O.TERNARY2, O.BF16)])
+@pytest.mark.parametrize("N", [1, 20, 1000])
+def test_ragged_n(cuda, fmt, xdt, N):
+    P = O.Problem(fmt, 3, 384, N, 128, xdt, seed=500 + N)
+    check(DeviceProblem(P).run(), P.reference(), xdt, f"ragged N={N}")
+
+
+@pytest.mark.parametrize("group", [256, 512])
+def test_larger_groups(cuda, group):
+    P = O.Problem(O.INT4, 7, 2048, 640, group, O.F16, seed=600 + group)
+    check(DeviceProblem(P).run(), P.reference(), O.F16, f"group {group}")
+
+
+def test_golden_fixture(cuda):
+    from pathlib import Path
+
+    data = np.load(Path(__file__).resolve().parent / "golden" / "qgemm_small.npz")
+    for case in sorted({k.split("/")[0] for k in data.files}):
+        fmt, xdt = int(data[f"{case}/fmt"]), int(data[f"{case}/xdtype"])
+        X, W, S, N, g = data[f"{case}/X"], data[f"{case}/W"], data[f"{case}/scales"], int(data[f"{case}/N"]), int(
+            data[f"{case}/group"])
+        K = X.shape[1]
+        Wp = to_dev_u32(hq.repack(fmt, W, K, N))
+        y = hq.gemm(fmt, to_dev_u16(X, xdt), Wp, to_dev_u16(S), N, g)
+        check(y, data[f"{case}/Y64"], xdt, case)
+
+
+def test_zero_point_and_one_hot_exact(cuda):
+    K, N = 512, 48
+    P = O.Problem(O.INT4, 1, K, N, 128, O.F16, seed=700)
+    ks = [0, 7, 8, 127, 128, 300, 511]
+    X = np.zeros((len(ks), K), dtype=np.uint16)
+    for r, k in enumerate(ks):
+        X[r, k] = 0x3C00
+    D = DeviceProblem(P)
+    y = to_host_f32(D.run(X=to_dev_u16(X, O.F16)))
+    Wdq = O.dequant(O.INT4, P.W, P.scales.ravel(), K, N, 128)
+    expect = O.to_f32(O.from_f32(Wdq[ks], O.F16), O.F16)  # the dequantised row, rounded to fp16 once
+    assert np.array_equal(y, expect)
+    W8 = np.full((K // 8) * N, 0x88888888, dtype=np.uint32)
+    y0 = hq.gemm(O.INT4, D.X, to_dev_u32(hq.repack(O.INT4, W8, K, N)), D.S, N)
+    assert np.all(to_host_f32(y0) == 0)
+
+
+def test_ternary_nonfinite_scale_drops_group(cuda):
+    P = O.Problem(O.TERNARY2, 4, 512, 64, 128, O.BF16, seed=710)
+    P.scales[1, 5] = 0x7E00
+    P.scales[2, 9] = 0x7C00
+    check(DeviceProblem(P).run(), P.reference(), O.BF16, "nonfinite scale")
+
+
+def test_strided_operands(cuda):
+    import torch
+
+    P = O.Problem(O.INT4, 5, 1024, 200, 128, O.F16, seed=720)
+    D = DeviceProblem(P)
+    Xw = torch.zeros((5, 1024 + 64), dtype=torch.float16, device="cuda")
+    Xw[:, :1024] = D.X
+    Yw = torch.full((5, 256), 7.0, dtype=torch.float16, device="cuda")
+    hq.gemm(O.INT4, Xw[:, :1024], D.Wp, D.S, 200, out=Yw[:, :200])
+    check(Yw[:, :200], P.reference(), O.F16, "strided")
+    assert torch.all(Yw[:, 200:] == 7.0)
+
+
+@pytest.mark.parametrize("M", [17, 40])
+def test_m_above_16(cuda, M):
+    P = O.Problem(O.INT4, M, 1024, 512, 128, O.F16, seed=800 + M)
+    check(DeviceProblem(P).run(), P.reference(), O.F16, f"M={M}")
+
+
+def test_rows_independent_and_deterministic(cuda):
+    P = O.Problem(O.INT4, 16, 2048, 1024, 128, O.F16, seed=900)
+    D = DeviceProblem(P)
+    y16 = D.run()
+    y16b = D.run()
+    assert torch_equal(y16, y16b)
+    for r in (0, 7, 15):
+        y1 = D.run(X=D.X[r:r + 1].contiguous())
+        np.testing.assert_allclose(to_host_f32(y1)[0], to_host_f32(y16)[r], rtol=2e-3, atol=1e-3)
+
+
+def torch_equal(a, b):
+    import torch
+
+    return bool(torch.equal(a, b))
+
+
+@pytest.mark.parametrize("fmt,xdt,Ns", [(O.INT4, O.F16, [5120, 1024, 1024]), (O.TERNARY2, O.F16, [2048, 2048]),
+                                        (O.INT4, O.BF16, [640, 33])])
+@pytest.mark.parametrize("M", [1, 16])
+def test_fused_equals_separate(cuda, fmt, xdt, Ns, M):
+    K = 1024
+    probs = [O.Problem(fmt, M, K, n, 128, xdt, seed=1000 + i) for i, n in enumerate(Ns)]
+    for p in probs[1:]:
+        p.X = probs[0].X
+    devs = [DeviceProblem(p) for p in probs]
+    X = devs[0].X
+    outs = hq.gemm_fused(fmt, X, [(d.Wp, d.S, d.P.N) for d in devs])
+    for d, y in zip(devs, outs):
+        sep = d.run(X=X)
+        assert torch_equal(sep, y)
+        check(y, d.P.reference(), xdt, f"fused N={d.P.N}")
+
+
+@pytest.mark.parametrize("fmt", [O.INT4, O.TERNARY2])
+def test_device_repack_matches_host(cuda, fmt):
+    import torch
+
+    K, N = 1024, 300
+    W = O.gen_int4(5, 5, K, N) if fmt == O.INT4 else O.gen_ternary(5, 5, K, N)
+    flag = torch.zeros(1, dtype=torch.int32, device="cuda")
+    dev = hq.repack_device(fmt, to_dev_u32(W), K, N, bad_flag=flag)
+    torch.cuda.synchronize()
+    host = hq.repack(fmt, W, K, N)
+    assert np.array_equal(dev.cpu().numpy().view(np.uint32), host)
+    assert int(flag.item()) == 0
+    if fmt == O.TERNARY2:
+        W[7] |= 3 << 4
+        hq.repack_device(fmt, to_dev_u32(W), K, N, bad_flag=flag)
+        torch.cuda.synchronize()
+        assert int(flag.item()) == 1
