@@ -120,7 +120,8 @@ hq_status hq_gemm_w2a16(const void* X, hq_dtype dtype, int64_t ldx, const uint32
                         hq_stream stream);
 
 /* Fused projections sharing one activation read (QKV, gate||up): nseg segments of one
- * format over the same X. Result equals one hq_gemm_* call per segment. Replaces the
+ * format over the same X. Each output equals the hq_gemm_* call of its segment up to fp32
+ * summation order (the fused launch may split K differently). Replaces the
  * separate GEMV launches of native_decoder.cu:1113-1115, 1149-1150, 1178-1179. */
 hq_status hq_gemm_fused(const void* X, hq_dtype dtype, int64_t ldx, hq_format fmt,
                         const hq_segment* segs, uint32_t nseg, uint32_t M, uint32_t K,

@@ -31,30 +31,65 @@ __device__ __forceinline__ f4 mfma16x16x32(u4 a, u4 b, f4 c) {
   }
 }
 
+// Raw buffer resource (gfx9 family descriptor word 3 = 0x00020000). Loads past
+// num_records return zero without touching memory, which lets every load in a
+// pipelined loop be unconditional (no branches, so s_waitcnt stays exact).
+constexpr int kBufferFlags = 0x00020000;
+constexpr uint32_t kOutOfRange = 0x80000000u;  // a voffset past any descriptor used here
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, kBufferFlags);
+}
+
 __device__ __forceinline__ uint32_t h2_bits(h2 v) { return __builtin_bit_cast(uint32_t, v); }
 __device__ __forceinline__ h2 bits_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
+
+// Registers the compiler cannot see through. gfx9 VOP3 instructions take no literal
+// constants and read at most one SGPR, so (w & mask) | magic only becomes a single
+// v_and_or_b32 when the mask sits in an SGPR and the magic in a VGPR.
+__device__ __forceinline__ uint32_t opaque_sgpr(uint32_t v) {
+  uint32_t r;
+  asm volatile("s_mov_b32 %0, %1" : "=s"(r) : "i"(v));
+  return r;
+}
+__device__ __forceinline__ uint32_t opaque_vgpr(uint32_t v) {
+  uint32_t r;
+  asm volatile("v_mov_b32 %0, %1" : "=v"(r) : "i"(v));
+  return r;
+}
+
+// Constants of the int4 dequantisation, materialised once per kernel.
+struct DqConst {
+  uint32_t lo, hi, magic;  // nibble masks (SGPR) and exponent magic (VGPR)
+};
+__device__ __forceinline__ DqConst dq_const_f16() {
+  return {opaque_sgpr(0x000F000Fu), opaque_sgpr(0x00F000F0u), opaque_vgpr(0x64006400u)};
+}
+__device__ __forceinline__ DqConst dq_const_bf16() {
+  return {opaque_sgpr(0x00780078u), 0u, opaque_vgpr(0x3F803F80u)};
+}
 
 // int4 word (tile nibble order) -> exact fp16 (q - 8) fragment.
 // (q | 0x6400) is the fp16 1024 + q; (16q | 0x6400) is 1024 + 16q. Subtracting 1032, or
 // scaling by 1/16 and subtracting 72, leaves q - 8 exactly.
-__device__ __forceinline__ u4 dq_int4_f16(uint32_t w) {
+__device__ __forceinline__ u4 dq_int4_f16(uint32_t w, const DqConst& k) {
   const h2 c1032 = {(_Float16)-1032.0f, (_Float16)-1032.0f};
   const h2 c72 = {(_Float16)-72.0f, (_Float16)-72.0f};
   const h2 s16 = {(_Float16)0.0625f, (_Float16)0.0625f};
   const uint32_t hi = w >> 8;
-  h2 v0 = bits_h2((w & 0x000F000Fu) | 0x64006400u) + c1032;
-  h2 v1 = __builtin_elementwise_fma(bits_h2((w & 0x00F000F0u) | 0x64006400u), s16, c72);
-  h2 v2 = bits_h2((hi & 0x000F000Fu) | 0x64006400u) + c1032;
-  h2 v3 = __builtin_elementwise_fma(bits_h2((hi & 0x00F000F0u) | 0x64006400u), s16, c72);
+  h2 v0 = bits_h2((w & k.lo) | k.magic) + c1032;
+  h2 v1 = __builtin_elementwise_fma(bits_h2((w & k.hi) | k.magic), s16, c72);
+  h2 v2 = bits_h2((hi & k.lo) | k.magic) + c1032;
+  h2 v3 = __builtin_elementwise_fma(bits_h2((hi & k.hi) | k.magic), s16, c72);
   return u4{h2_bits(v0), h2_bits(v1), h2_bits(v2), h2_bits(v3)};
 }
 
 // int4 word -> bf16 fragment of (16 + q) / 16 = 0x3F80 | q << 3 (exact). gfx950 has no
 // packed bf16 add, so the offset is removed after the MFMA: the caller accumulates
 // -1.5 * sum(x) over the same k range and the group sum is 16 * (acc + corr).
-__device__ __forceinline__ u4 dq_int4_bf16_biased(uint32_t w) {
-  return u4{((w << 3) & 0x00780078u) | 0x3F803F80u, ((w >> 1) & 0x00780078u) | 0x3F803F80u,
-            ((w >> 5) & 0x00780078u) | 0x3F803F80u, ((w >> 9) & 0x00780078u) | 0x3F803F80u};
+__device__ __forceinline__ u4 dq_int4_bf16_biased(uint32_t w, const DqConst& k) {
+  return u4{((w << 3) & k.lo) | k.magic, ((w >> 1) & k.lo) | k.magic, ((w >> 5) & k.lo) | k.magic,
+            ((w >> 9) & k.lo) | k.magic};
 }
 
 // Ternary word -> fragment of chunk CW (0 or 1): elements 2t in fp16 and in bf16

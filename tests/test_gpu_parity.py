@@ -164,8 +164,9 @@ def test_fused_equals_separate(cuda, fmt, xdt, Ns, M):
     X = devs[0].X
     outs = hq.gemm_fused(fmt, X, [(d.Wp, d.S, d.P.N) for d in devs])
     for d, y in zip(devs, outs):
-        sep = d.run(X=X)
-        assert torch_equal(sep, y)
+        # Same values up to fp32 summation order (the fused launch may split K differently).
+        sep = to_host_f32(d.run(X=X))
+        assert O.normwise_error(to_host_f32(y), sep) <= OUT_TOL[xdt]
         check(y, d.P.reference(), xdt, f"fused N={d.P.N}")
 
 
