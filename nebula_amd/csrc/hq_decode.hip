@@ -116,8 +116,8 @@ __global__ void __launch_bounds__(64 * max_wk(T)) hq_decode_kernel(const GemmDes
 #pragma unroll
     for (int t = 0; t < T; ++t) {
       const uint32_t wo = ok ? (kb * 64u + lane) * WPL * 4u : kOutOfRange;
-      if constexpr (WPL == 4) wr[slot][t] = __builtin_amdgcn_raw_buffer_load_b128(wrs[t], wo, 0, 0);
-      else wr[slot][t] = __builtin_amdgcn_raw_buffer_load_b64(wrs[t], wo, 0, 0);
+      if constexpr (WPL == 4) wr[slot][t] = __builtin_amdgcn_raw_buffer_load_b128(wrs[t], wo, 0, kStreamAux);
+      else wr[slot][t] = __builtin_amdgcn_raw_buffer_load_b64(wrs[t], wo, 0, kStreamAux);
       sr[slot][t] = __builtin_amdgcn_raw_buffer_load_b16(srs, grp * srow + soff[t], 0, 0);
     }
     const uint32_t base = ok ? xoff + kb * 256u : kOutOfRange;
@@ -220,18 +220,15 @@ int env_int(const char* name, int dflt) {
   return v && *v ? std::atoi(v) : dflt;
 }
 
-// Tiling choice. Wide tiles (T=4) amortise the activation fragments over 64 columns
-// when N offers enough tiles; narrow ones keep every CU busy for small N. WK splits K
-// inside the workgroup until there are ~12 wavefronts per CU.
+// Tiling choice (measured on MI355X over the 27B-class decode shapes): wide tiles (T=4)
+// amortise the activation fragments over 64 columns when N offers >= 1024 tiles, T=2
+// for mid-size N, T=1 below; four wavefronts per workgroup split K.
 DecodeConfig choose_decode(const GemmDesc& d) {
   uint32_t tiles = 0;
   for (uint32_t i = 0; i < d.nseg; ++i) tiles += d.seg[i].ntiles;
   const uint32_t groups = d.nkb / d.gkb;
-  int T = tiles >= 1024 ? 4 : (tiles >= 512 ? 2 : 1);
-  const uint32_t target_waves = 256u * 12u;
-  uint32_t blocks = 0;
-  for (uint32_t i = 0; i < d.nseg; ++i) blocks += (d.seg[i].ntiles + T - 1) / T;
-  int WK = (int)std::min<uint32_t>(max_wk(T), std::max<uint32_t>(1, (target_waves + blocks - 1) / blocks));
+  int T = tiles >= 1024 ? 4 : (tiles >= 300 ? 2 : 1);
+  int WK = 4;
   const int eT = env_int("HQ_DECODE_T", 0), eWK = env_int("HQ_DECODE_WK", 0);
   if (eT == 1 || eT == 2 || eT == 4) T = eT;
   if (eWK >= 1) WK = eWK;

@@ -36,6 +36,8 @@ __device__ __forceinline__ f4 mfma16x16x32(u4 a, u4 b, f4 c) {
 // pipelined loop be unconditional (no branches, so s_waitcnt stays exact).
 constexpr int kBufferFlags = 0x00020000;
 constexpr uint32_t kOutOfRange = 0x80000000u;  // a voffset past any descriptor used here
+// Cache policy of the decode weight stream: non-temporal (each byte is read once).
+constexpr int kStreamAux = 2;
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, kBufferFlags);
@@ -48,6 +50,9 @@ typedef __attribute__((address_space(3))) void* lds_ptr_t;
 __device__ __forceinline__ void buffer_to_lds16(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voff) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds, 16, voff, 0, 0, 0);
 }
+
+// s_waitcnt immediate (gfx9 encoding) waiting for vmcnt <= n only (n < 64).
+constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x70 | 0xF00; }
 
 __device__ __forceinline__ uint32_t h2_bits(h2 v) { return __builtin_bit_cast(uint32_t, v); }
 __device__ __forceinline__ h2 bits_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }

@@ -3,10 +3,12 @@
 // The reference has no prefill GEMM (hydrogen's decoder feeds prompt tokens one at a
 // time, native_decoder.cu:1297); this is the MFMA path the target operator asks for.
 //
-// Workgroup tile: (16 * RT) rows x 256 columns, K stepped one 128-deep k-block at a time.
-// Four wavefronts each own all rows and 64 columns (4 column tiles), so every weight
-// fragment is dequantised exactly once per workgroup, with its group scale folded in,
-// and reused by RT MFMAs. Activation tiles are staged in LDS, double-buffered, with the
+// Workgroup tile: (16 * RT * WM) rows x 256 columns, K stepped one 128-deep k-block at a
+// time. 4 * WM wavefronts: WM along M, 4 along N; each owns 16 * RT rows and 64 columns
+// (4 column tiles, 16 * RT * 4 fp32 accumulators). A weight fragment is dequantised with
+// its group scale folded in by the WM wavefronts sharing its columns and reused by RT
+// MFMAs each; WM = 2 gives two waves per SIMD so one's dequantisation hides under the
+// other's MFMAs. Activation tiles are staged in LDS, double-buffered, with the
 // gfx950 buffer->LDS path (buffer_load_dwordx4 ... lds), in a layout whose 16-byte units
 // are XOR-swizzled by row so the ds_read_b128 fragment reads are bank-conflict free.
 // Weights go straight from HBM into registers in the tile layout (hq_layout.hpp), which
@@ -23,7 +25,6 @@
 namespace hq {
 namespace {
 
-constexpr int kWaves = 4;
 constexpr int kTilesPerWave = 4;  // 64 columns per wavefront, 256 per workgroup
 
 // Dequantised B fragment with the group scale applied. s2 holds the fp16 scale twice.
@@ -78,9 +79,9 @@ __device__ __forceinline__ u4 dq_scaled(const u4& w, int c, uint32_t s_f16, cons
   }
 }
 
-template <int FMT, int DT, int RT>
-__global__ void __launch_bounds__(64 * kWaves) hq_prefill_kernel(const GemmDesc d, uint32_t mtiles, uint32_t total_wg) {
-  constexpr uint32_t BM = 16u * RT;
+template <int FMT, int DT, int RT, int WM>
+__global__ void __launch_bounds__(256 * WM) hq_prefill_kernel(const GemmDesc d, uint32_t mtiles, uint32_t total_wg) {
+  constexpr uint32_t BM = 16u * RT * WM;
   constexpr uint32_t kStageBytes = BM * 256u;  // BM rows x 128 fp16
   extern __shared__ __attribute__((aligned(16))) char smem[];
 
@@ -101,15 +102,17 @@ __global__ void __launch_bounds__(64 * kWaves) hq_prefill_kernel(const GemmDesc 
   const uint32_t local = lid - sg.blk_begin;
   const uint32_t mt = local / nblk, nt = local % nblk;
   const uint32_t m0 = mt * BM;
-  const uint32_t ct0 = nt * 16u + wave * kTilesPerWave;
+  const uint32_t wm = wave / 4u, wn = wave % 4u;
+  const uint32_t ct0 = nt * 16u + wn * kTilesPerWave;
+  const uint32_t wrow0 = wm * 16u * RT;  // first workgroup row of this wavefront
 
   // Activation rows [m0, m0 + BM) of X; rows >= M read as zero.
   const uint32_t rows = min(BM, d.M - m0);
   const __amdgpu_buffer_rsrc_t xr =
       make_rsrc(reinterpret_cast<const char*>(d.X) + (size_t)m0 * (size_t)d.ldx * 2u, rows * (uint32_t)d.ldx * 2u);
-  // This lane's part of the wave's RT load instructions per k-block: instruction i fills
-  // LDS rows 4q..4q+3, q = wave * RT + i; lane -> row 4q + g4, 16-byte slot c16 holding
-  // unit c16 ^ (row & 15).
+  // This lane's part of the wave's RT load instructions per k-block (BM / 4 in all): instruction
+  // i fills LDS rows 4q..4q+3, q = wave * RT + i; lane -> row 4q + g4, 16-byte slot c16
+  // holding unit c16 ^ (row & 15).
   uint32_t aoff[RT];
 #pragma unroll
   for (int i = 0; i < RT; ++i) {
@@ -137,19 +140,22 @@ __global__ void __launch_bounds__(64 * kWaves) hq_prefill_kernel(const GemmDesc 
     soff[t] = min(ct * 16u + c16, sg.N - 1u) * 2u;
   }
   const __amdgpu_buffer_rsrc_t srs = make_rsrc(sg.S, (d.nkb / d.gkb) * sg.N * 2u);
-  u4 wnext[kTilesPerWave];
-  uint32_t snext[kTilesPerWave];
-  auto load_b = [&](uint32_t kb) {
-    const uint32_t grp = kb / d.gkb;
+  // Weights and scales: a register ring of 3 k-blocks, two ahead of the one computed.
+  // Loads past the last k-block read zero (empty range) instead of branching.
+  u4 wr[3][kTilesPerWave];
+  uint32_t sr[3][kTilesPerWave];
+  auto load_b = [&](int slot, uint32_t kb) {
+    const bool ok = kb < d.nkb;
+    const uint32_t grp = min(kb, d.nkb - 1u) / d.gkb;
 #pragma unroll
     for (int t = 0; t < kTilesPerWave; ++t) {
       if constexpr (FMT == HQ_FORMAT_INT4) {
-        wnext[t] = __builtin_amdgcn_raw_buffer_load_b128(wrs[t], (kb * 64u + lane) * 16u, 0, 0);
+        wr[slot][t] = __builtin_amdgcn_raw_buffer_load_b128(wrs[t], ok ? (kb * 64u + lane) * 16u : kOutOfRange, 0, 0);
       } else {
-        const u2 v = __builtin_amdgcn_raw_buffer_load_b64(wrs[t], (kb * 64u + lane) * 8u, 0, 0);
-        wnext[t] = u4{v[0], v[1], 0u, 0u};
+        const u2 v = __builtin_amdgcn_raw_buffer_load_b64(wrs[t], ok ? (kb * 64u + lane) * 8u : kOutOfRange, 0, 0);
+        wr[slot][t] = u4{v[0], v[1], 0u, 0u};
       }
-      snext[t] = __builtin_amdgcn_raw_buffer_load_b16(srs, grp * sg.N * 2u + soff[t], 0, 0);
+      sr[slot][t] = __builtin_amdgcn_raw_buffer_load_b16(srs, grp * sg.N * 2u + soff[t], 0, 0);
     }
   };
 
@@ -165,40 +171,42 @@ __global__ void __launch_bounds__(64 * kWaves) hq_prefill_kernel(const GemmDesc 
 #pragma unroll
   for (int c = 0; c < 4; ++c) ldsoff[c] = c16 * 256u + (((4u * c + g4) ^ c16) * 16u);
 
-  load_a(0, 0);
-  load_b(0);
   const uint32_t nkb = d.nkb;
-  for (uint32_t kb = 0; kb < nkb; ++kb) {
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's LDS fills and register loads have landed
-    __syncthreads();                // ... and every wave's; the other stage is no longer read
-    u4 wcur[kTilesPerWave];
-    uint32_t scur[kTilesPerWave];
+  // One k-block. Issue order per step: A(kb + 1) to LDS, then B(kb + 2) to registers, so
+  // at the top of the next step vmcnt(2 * kTilesPerWave) leaves only B(kb + 2) in flight.
+  auto step = [&](uint32_t kb, int slot) {
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kTilesPerWave));  // A(kb), B(kb) landed for this wave
+    __syncthreads();                                            // ... for every wave; stage (kb+1)&1 is free
+    load_a((kb + 1) & 1u, kb + 1);
+    load_b((slot + 2) % 3, kb + 2);
+    if (kb < nkb) {  // uniform; no loads inside
+      const char* sbase = smem + (kb & 1u) * kStageBytes;
 #pragma unroll
-    for (int t = 0; t < kTilesPerWave; ++t) {
-      wcur[t] = wnext[t];
-      scur[t] = snext[t];
-    }
-    if (kb + 1 < nkb) {
-      load_a((kb + 1) & 1u, kb + 1);
-      load_b(kb + 1);
-    }
-    const char* sbase = smem + (kb & 1u) * kStageBytes;
+      for (int c = 0; c < 4; ++c) {
+        u4 b[kTilesPerWave];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      u4 b[kTilesPerWave];
+        for (int t = 0; t < kTilesPerWave; ++t) b[t] = dq_scaled<FMT, DT>(wr[slot][t], c, sr[slot][t], dqk);
 #pragma unroll
-      for (int t = 0; t < kTilesPerWave; ++t) b[t] = dq_scaled<FMT, DT>(wcur[t], c, scur[t], dqk);
+        for (int r = 0; r < RT; ++r) {
+          const u4 a = *reinterpret_cast<const u4*>(sbase + (wrow0 + 16u * r) * 256u + ldsoff[c]);
 #pragma unroll
-      for (int r = 0; r < RT; ++r) {
-        const u4 a = *reinterpret_cast<const u4*>(sbase + r * 4096u + ldsoff[c]);
-#pragma unroll
-        for (int t = 0; t < kTilesPerWave; ++t) acc[r][t] = mfma16x16x32<DT>(a, b[t], acc[r][t]);
+          for (int t = 0; t < kTilesPerWave; ++t) acc[r][t] = mfma16x16x32<DT>(a, b[t], acc[r][t]);
+        }
+        // Keep each chunk's fragments from being hoisted into the previous chunk.
+        __builtin_amdgcn_sched_barrier(0);
       }
-      // Keep each chunk's fragments from being hoisted into the previous chunk (register
-      // pressure: the accumulators already fill the AGPRs).
-      __builtin_amdgcn_sched_barrier(0);
     }
+  };
+
+  load_a(0, 0);
+  load_b(0, 0);
+  load_b(1, 1);
+  for (uint32_t kb = 0; kb < nkb; kb += 3) {
+    step(kb, 0);
+    step(kb + 1, 1);
+    step(kb + 2, 2);
   }
+  __builtin_amdgcn_s_waitcnt(0);  // drain the out-of-range prefetches before the stores
 
   // Epilogue: tile (r, t), lane -> column 16 (ct0 + t) + c16, rows 16 r + 4 g4 + v. Rows past M
   // fall outside the descriptor; columns past N get an out-of-range offset.
@@ -213,16 +221,16 @@ __global__ void __launch_bounds__(64 * kWaves) hq_prefill_kernel(const GemmDesc 
     for (int r = 0; r < RT; ++r)
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
-        const uint32_t row = 16u * r + 4u * g4 + v;
+        const uint32_t row = wrow0 + 16u * r + 4u * g4 + v;
         __builtin_amdgcn_raw_buffer_store_b16(f32_to_out<DT>(acc[r][t][v] * post), yr,
                                               cbase == kOutOfRange ? kOutOfRange : cbase + row * (uint32_t)sg.ldy * 2u, 0, 0);
       }
   }
 }
 
-template <int FMT, int DT, int RT>
+template <int FMT, int DT, int RT, int WM>
 hipError_t launch_rt(GemmDesc d, hipStream_t stream) {
-  constexpr uint32_t BM = 16u * RT;
+  constexpr uint32_t BM = 16u * RT * WM;
   const uint32_t mtiles = (d.M + BM - 1) / BM;
   uint32_t blk = 0;
   for (uint32_t i = 0; i < d.nseg; ++i) {
@@ -233,18 +241,18 @@ hipError_t launch_rt(GemmDesc d, hipStream_t stream) {
   const size_t lds = 2u * BM * 256u;
   // More than the default 64 KiB of dynamic LDS needs an opt-in per kernel (idempotent).
   static const hipError_t attr =
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&hq_prefill_kernel<FMT, DT, RT>),
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&hq_prefill_kernel<FMT, DT, RT, WM>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (attr != hipSuccess) return attr;
-  hipLaunchKernelGGL((hq_prefill_kernel<FMT, DT, RT>), dim3(blk), dim3(64 * kWaves), lds, stream, d, mtiles, blk);
+  hipLaunchKernelGGL((hq_prefill_kernel<FMT, DT, RT, WM>), dim3(blk), dim3(256 * WM), lds, stream, d, mtiles, blk);
   return hipGetLastError();
 }
 
 template <int FMT, int DT>
 hipError_t launch_fd(GemmDesc d, hipStream_t stream) {
-  if (d.M <= 64) return launch_rt<FMT, DT, 4>(d, stream);
-  if (d.M <= 128) return launch_rt<FMT, DT, 8>(d, stream);
-  return launch_rt<FMT, DT, 16>(d, stream);
+  if (d.M <= 64) return launch_rt<FMT, DT, 4, 1>(d, stream);
+  if (d.M <= 128) return launch_rt<FMT, DT, 8, 1>(d, stream);
+  return launch_rt<FMT, DT, 8, 2>(d, stream);
 }
 
 }  // namespace
