@@ -77,7 +77,16 @@ const char* hq_status_string(hq_status s);
 size_t hq_linear_words(hq_format fmt, uint32_t K, uint32_t N);
 /* Words of the gfx950 tile layout (N padded up to a multiple of 16). 0 on a bad shape. */
 size_t hq_packed_words(hq_format fmt, uint32_t K, uint32_t N);
-/* Device workspace a GEMM call of this shape needs (0 means none; pass NULL). */
+/* Device workspace a GEMM call of this shape needs on the current device (0: none).
+ * Decode shapes (M <= 16) whose work is split across workgroups along K need one: a
+ * 256-byte aligned buffer, zero-filled by the caller before its first use (every call
+ * leaves it zero-filled again). Calls sharing one workspace must not overlap in time
+ * (same stream, or ordered by events). For hq_gemm_fused pass N = sum of the segments'
+ * N plus 16 per segment after the first. Passing NULL instead makes the library use a
+ * buffer of its own per (device, stream), allocated on first need outside stream
+ * capture; a call that would need to allocate it during capture fails with
+ * HQ_ERR_WORKSPACE. The reference has no workspace: it allocates inside
+ * MarlinGemmEngine (marlin_gemm.cu:381-416). */
 hq_status hq_workspace_bytes(hq_format fmt, uint32_t M, uint32_t K, uint32_t N, uint32_t group,
                              size_t* bytes);
 
@@ -109,7 +118,9 @@ hq_status hq_repack_ternary2_device(const uint32_t* d_src_linear, uint32_t* d_ds
  * Wp: gfx950 packed weight, 16-byte aligned. scales: fp16 [K/group][N].
  * Y: [M][ldy], 2-byte aligned, ldy >= N; written in full (no zero-fill needed).
  * K % 128 == 0, group % 128 == 0, K % group == 0, M >= 1, N >= 1.
- * Decode shapes (M <= 16) run the HBM-streaming kernel; larger M the MFMA tile kernel. */
+ * workspace / workspace_bytes: see hq_workspace_bytes (NULL, 0 is always accepted).
+ * Decode shapes (M <= 16) run the HBM-streaming kernel; larger M the MFMA tile kernel.
+ * Results are deterministic: repeated calls with the same shapes give identical bits. */
 hq_status hq_gemm_w4a16(const void* X, hq_dtype dtype, int64_t ldx, const uint32_t* Wp,
                         const uint16_t* scales, void* Y, int64_t ldy, uint32_t M, uint32_t K,
                         uint32_t N, uint32_t group, void* workspace, size_t workspace_bytes,

@@ -2,11 +2,15 @@
 // kernel dispatch and per-thread error strings. No exception crosses the ABI.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <map>
+#include <mutex>
 #include <string>
 #include <thread>
+#include <utility>
 #include <vector>
 
 #include "hq_internal.hpp"
@@ -66,11 +70,56 @@ void parallel_for(size_t n, F f) {
   for (auto& t : th) t.join();
 }
 
+// Library-owned decode workspace, one per (device, stream), used when the caller passes
+// none. It is zero-filled when allocated (the kernels leave its counters at zero), grows
+// when a larger shape needs it, and is never allocated while the stream is capturing.
+// Buffers that were outgrown stay allocated until the process ends: a launch still in
+// flight may use them.
+struct InternalWorkspace {
+  std::mutex mu;
+  std::map<std::pair<int, hipStream_t>, std::pair<void*, size_t>> live;
+  std::vector<void*> retired;
+};
+InternalWorkspace& internal_ws() {
+  static InternalWorkspace* w = new InternalWorkspace();  // never destroyed: see above
+  return *w;
+}
+
+hq_status get_internal_ws(hipStream_t stream, size_t need, void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(HQ_ERR_DEVICE, "hipGetDevice: %s", hipGetErrorString(e));
+  InternalWorkspace& w = internal_ws();
+  std::lock_guard<std::mutex> lock(w.mu);
+  auto& slot = w.live[{dev, stream}];
+  if (slot.second >= need) {
+    *out = slot.first;
+    return HQ_OK;
+  }
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  e = hipStreamIsCapturing(stream, &cap);
+  if (e != hipSuccess) return fail(HQ_ERR_DEVICE, "hipStreamIsCapturing: %s", hipGetErrorString(e));
+  if (cap != hipStreamCaptureStatusNone)
+    return fail(HQ_ERR_WORKSPACE,
+                "this decode shape needs %zu workspace bytes; pass a workspace (hq_workspace_bytes) or run "
+                "the shape once before capturing the stream",
+                need);
+  const size_t bytes = std::max(need, (size_t)1 << 20);
+  void* p = nullptr;
+  if ((e = hipMalloc(&p, bytes)) != hipSuccess) return fail(HQ_ERR_DEVICE, "hipMalloc(%zu): %s", bytes, hipGetErrorString(e));
+  if ((e = hipMemsetAsync(p, 0, bytes, stream)) != hipSuccess) {
+    (void)hipFree(p);
+    return fail(HQ_ERR_DEVICE, "hipMemsetAsync: %s", hipGetErrorString(e));
+  }
+  if (slot.first) w.retired.push_back(slot.first);
+  slot = {p, bytes};
+  *out = p;
+  return HQ_OK;
+}
+
 // Validation shared by the GEMM entry points.
 hq_status check_gemm_common(const void* X, int dtype, int64_t ldx, uint32_t M, uint32_t K,
-                            uint32_t group, void* ws, size_t ws_bytes) {
-  (void)ws;
-  (void)ws_bytes;
+                            uint32_t group) {
   if (!X) return fail(HQ_ERR_INVALID_ARG, "X is null");
   if (!valid_dtype(dtype)) return fail(HQ_ERR_INVALID_ARG, "unknown dtype %d", dtype);
   if (M == 0) return fail(HQ_ERR_SHAPE, "M must be >= 1");
@@ -97,7 +146,7 @@ hq_status check_segment(const hq_segment& s, uint32_t i) {
 hq_status run_gemm(const void* X, hq_dtype dtype, int64_t ldx, hq_format fmt, const hq_segment* segs,
                    uint32_t nseg, uint32_t M, uint32_t K, uint32_t group, void* ws, size_t ws_bytes,
                    hq_stream stream) {
-  hq_status st = check_gemm_common(X, dtype, ldx, M, K, group, ws, ws_bytes);
+  hq_status st = check_gemm_common(X, dtype, ldx, M, K, group);
   if (st != HQ_OK) return st;
   if (!valid_fmt(fmt)) return fail(HQ_ERR_INVALID_ARG, "unknown format %d", (int)fmt);
   if (!segs || nseg == 0 || nseg > HQ_MAX_SEGMENTS)
@@ -120,8 +169,22 @@ hq_status run_gemm(const void* X, hq_dtype dtype, int64_t ldx, hq_format fmt, co
     d.seg[i].ntiles = hq::col_tiles(segs[i].N);
   }
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  hipError_t e = M <= 16 ? hq::launch_decode(fmt, dtype, d, s) : hq::launch_prefill(fmt, dtype, d, s);
-  return from_hip(e, M <= 16 ? "decode launch" : "prefill launch");
+  if (M > 16) return from_hip(hq::launch_prefill(fmt, dtype, d, s), "prefill launch");
+  const hq::DecodeConfig c = hq::choose_decode(fmt, d);
+  const size_t need = hq::decode_workspace_bytes(d, c);
+  void* w = nullptr;
+  if (need > 0) {
+    if (ws) {
+      if (ws_bytes < need)
+        return fail(HQ_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu this call needs", ws_bytes, need);
+      if (reinterpret_cast<uintptr_t>(ws) % 256)
+        return fail(HQ_ERR_ALIGNMENT, "workspace must be 256-byte aligned");
+      w = ws;
+    } else if ((st = get_internal_ws(s, need, &w)) != HQ_OK) {
+      return st;
+    }
+  }
+  return from_hip(hq::launch_decode(fmt, dtype, d, c, w, s), "decode launch");
 }
 
 }  // namespace
@@ -161,11 +224,19 @@ size_t hq_packed_words(hq_format fmt, uint32_t K, uint32_t N) {
 hq_status hq_workspace_bytes(hq_format fmt, uint32_t M, uint32_t K, uint32_t N, uint32_t group, size_t* bytes) {
   if (!bytes) return fail(HQ_ERR_INVALID_ARG, "bytes is null");
   if (!valid_fmt(fmt)) return fail(HQ_ERR_INVALID_ARG, "unknown format %d", (int)fmt);
-  (void)M;
-  (void)K;
-  (void)N;
-  (void)group;
+  if (M == 0 || N == 0 || K == 0 || K % hq::kBlockK || group == 0 || group % hq::kBlockK || K % group)
+    return fail(HQ_ERR_SHAPE, "bad shape M=%u K=%u N=%u group=%u", M, K, N, group);
   *bytes = 0;
+  if (M > 16) return ok();
+  hq::GemmDesc d{};
+  d.M = M;
+  d.K = K;
+  d.nkb = K / hq::kBlockK;
+  d.gkb = group / hq::kBlockK;
+  d.nseg = 1;
+  d.seg[0].N = N;
+  d.seg[0].ntiles = hq::col_tiles(N);
+  *bytes = hq::decode_workspace_bytes(d, hq::choose_decode(fmt, d));
   return ok();
 }
 

@@ -4,24 +4,29 @@
 // (hydrogen/src/model/marlin_gemm.cu:130-237, 242-322). The reference gives each
 // thread one output column and does 32 x M scalar FMAs per 16-byte weight load,
 // then merges 16 fixed K-splits with fp32 atomics into a pre-zeroed Y. Here:
-//   * one wavefront streams T column tiles (16 columns each) over its K range, one
-//     fully coalesced wave load (1 KiB int4 / 512 B ternary) per tile and k-block,
-//     with U k-blocks of weights, scales and activations in flight in a register ring
-//     (HBM latency is ~2 us, so bytes in flight, not wave count, set the bandwidth);
+//   * the work is cut into units of (slab of T column tiles) x (128-deep k-block) and
+//     every workgroup streams an equal contiguous range of units (hq_plan.hpp), so all
+//     CUs finish together whatever N and K are; slabs cut by a range boundary are
+//     completed by a last-arriver fix-up through the workspace, in workgroup order;
+//   * inside a workgroup the WK wavefronts take the units of each slab in turn
+//     (unit j -> wavefront j mod WK), each with U k-blocks of weights, scales and
+//     activations in flight in a register ring, and meet only once, at the end, to sum
+//     their per-slab results through LDS in wavefront order;
 //   * weights are dequantised in registers straight into MFMA B fragments and
 //     multiplied against the activation rows (M padded to 16) with
-//     v_mfma_f32_16x16x32_{f16,bf16}: the k reduction happens inside the matrix core
-//     instead of lane-by-lane FMAs and shuffles;
-//   * the group scale multiplies the fp32 group sum once per (column, group);
-//   * WK wavefronts of a workgroup split K and are reduced through LDS in a fixed
-//     order, so the result is deterministic and Y needs no zero-fill or atomics.
+//     v_mfma_f32_16x16x32_{f16,bf16}. int4 uses the biased form (magic + q, one
+//     v_and_or_b32 per fragment word) and removes the bias with one extra MFMA per
+//     chunk whose result seeds every tile's accumulator;
+//   * the group scale multiplies the fp32 k-block sum once per (column, k-block).
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
 #include <cstdlib>
+#include <mutex>
 
 #include "hq_device.hpp"
 #include "hq_internal.hpp"
+#include "hq_plan.hpp"
 
 namespace hq {
 namespace {
@@ -39,238 +44,489 @@ struct WTraits<HQ_FORMAT_TERNARY2> {
   static constexpr uint32_t wpl = 2;
 };
 
-template <int FMT, int DT>
-__device__ __forceinline__ u4 dequant_chunk(const typename WTraits<FMT>::V& w, int c, const DqConst& k) {
-  if constexpr (FMT == HQ_FORMAT_INT4) {
-    if constexpr (DT == HQ_DTYPE_F16) return dq_int4_f16(w[c], k);
-    else return dq_int4_bf16_biased(w[c], k);
-  } else {
-    const uint32_t word = w[c >> 1];
-    return (c & 1) ? dq_tern2<1>(word) : dq_tern2<0>(word);
-  }
-}
-
-// Constant bf16 -1.5 in every B element: MFMA(x, this) = -1.5 * sum_k x over the chunk.
-constexpr uint32_t kBf16NegOneHalf2 = 0xBFC0BFC0u;
-
-// Largest workgroup (in wavefronts) per tile width: the deep register rings of T >= 2 need
-// more than the 128 VGPRs a 16-wave workgroup leaves each lane.
+// Largest workgroup (in wavefronts) per slab width: the register rings of T >= 2 leave
+// room for two wavefronts per SIMD, those of T = 1 for four.
 constexpr int max_wk(int T) { return T >= 2 ? 8 : 16; }
 
+struct Piece {
+  uint32_t g, ka, kz;  // slab and its k-block range [ka, kz) inside this workgroup
+};
+
 template <int FMT, int DT, int T, int U>
-__global__ void __launch_bounds__(64 * max_wk(T)) hq_decode_kernel(const GemmDesc d, uint32_t kb_per_wave) {
+__global__ void __launch_bounds__(64 * max_wk(T)) hq_decode_kernel(const GemmDesc d, const DecodePlan pl) {
   using W = typename WTraits<FMT>::V;
   constexpr uint32_t WPL = WTraits<FMT>::wpl;
-  constexpr bool kBiased = (FMT == HQ_FORMAT_INT4 && DT == HQ_DTYPE_BF16);
-  extern __shared__ float red[];
+  constexpr uint32_t kLaneBytes = WPL * 4u;
+  constexpr uint32_t kBlockBytes = 64u * kLaneBytes;  // one tile x one k-block
+  constexpr uint32_t kCols = 16u * T;                 // output columns of a slab
+  constexpr bool kInt4 = FMT == HQ_FORMAT_INT4;
+  extern __shared__ float red[];  // [np_max][WK][M * kCols]
+  __shared__ uint32_t sh_last[2];
 
   const uint32_t lane = threadIdx.x & 63u;
-  // Wave index through readfirstlane so the compiler keeps all k-block arithmetic scalar.
+  // Wave index through readfirstlane so all unit bookkeeping stays scalar.
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const uint32_t nwave = blockDim.x >> 6;
+  const uint32_t WK = pl.WK;
   const uint32_t c16 = lane & 15u;
   const uint32_t g4 = lane >> 4;
+  const uint32_t nkb = d.nkb;
+  const uint32_t b = blockIdx.x;
+  const uint32_t M = d.M;
+  const uint32_t SL = M * kCols;  // floats of one piece's partial tile
 
-  // Segment of this workgroup (segments are few; the scan is uniform).
-  uint32_t s = 0;
+  const uint32_t u0 = plan_begin(pl.utot, pl.P, b);
+  const uint32_t u1 = plan_begin(pl.utot, pl.P, b + 1);
+  const uint32_t gfirst = u0 / nkb, glast = (u1 - 1u) / nkb;
+  const uint32_t np = glast - gfirst + 1u;
+  auto piece = [&](uint32_t i) {
+    Piece p;
+    p.g = plan_piece_slab(gfirst, glast, i);
+    p.ka = p.g == gfirst ? u0 - p.g * nkb : 0u;
+    p.kz = p.g == glast ? u1 - p.g * nkb : nkb;
+    return p;
+  };
+  // k-blocks [s, e) step st of wavefront w inside piece p: interleaved (w, w + WK, ...) or
+  // one contiguous run per wavefront.
+  const uint32_t kstep = pl.contig ? 1u : WK;
+  auto span_begin = [&](const Piece& p, uint32_t w) {
+    return pl.contig ? p.ka + (w * (p.kz - p.ka)) / WK : p.ka + w;
+  };
+  auto span_end = [&](const Piece& p, uint32_t w) {
+    return pl.contig ? p.ka + ((w + 1u) * (p.kz - p.ka)) / WK : p.kz;
+  };
+
+  // Fixed per-lane offsets. Tile t of a slab lies t * nkb blocks after tile 0, so the
+  // slab descriptor (sized to its valid tiles) turns missing tiles into zero reads.
+  uint32_t wvo[T];
 #pragma unroll
-  for (uint32_t i = 1; i < HQ_MAX_SEGMENTS; ++i)
-    if (i < d.nseg && blockIdx.x >= d.seg[i].blk_begin) s = i;
-  const SegDesc sg = d.seg[s];
-  const uint32_t ct0 = (blockIdx.x - sg.blk_begin) * T;
+  for (int t = 0; t < T; ++t) wvo[t] = lane * kLaneBytes + (uint32_t)t * nkb * kBlockBytes;
+  // A operand: row c16 of X, k-slice g4 of each chunk; rows >= M read as zero (activation
+  // and scale loads past the wavefront's units re-read cached data and are discarded).
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(d.X, M * (uint32_t)d.ldx * 2u);
+  const uint32_t xo = c16 * (uint32_t)d.ldx * 2u + g4 * 16u;
 
-  const uint32_t kb0 = wave * kb_per_wave;
-  const uint32_t kb1 = min(d.nkb, kb0 + kb_per_wave);
-
-  // A operand: row c16 of X, k-slice g4 of each chunk. Rows >= M fall outside the
-  // descriptor and read as zero.
-  const __amdgpu_buffer_rsrc_t xr = make_rsrc(d.X, d.M * (uint32_t)d.ldx * 2u);
-  const uint32_t xoff = c16 * (uint32_t)d.ldx * 2u + g4 * 16u;
-
-  // One descriptor per column tile; tiles past the segment get an empty descriptor.
-  __amdgpu_buffer_rsrc_t wrs[T];
-  uint32_t soff[T];
-  const uint32_t tile_bytes = d.nkb * 64u * WPL * 4u;
+  // Load-side iterator: piece lp, k-block lkb of this wavefront, with the buffer
+  // extents of the piece's slab (zero once the wavefront's units are exhausted, which
+  // turns the remaining ring loads into zero reads without memory traffic).
+  uint32_t lp = 0, lkb = 0, lkz = 0;
+  const uint32_t* lw_base = d.seg[0].Wp;
+  const uint16_t* ls_base = d.seg[0].S;
+  uint32_t lw_num = 0, ls_num = 0, lsrow = 0;
+  // Scales: load j of a unit gives lane l column 64 j + l % (16 T) of the slab (one load
+  // per four tiles); the flush gathers tile t's scale for column c16 from lane
+  // 16 (t % 4) + c16 of load t / 4.
+  constexpr int kSL = (T + 3) / 4;
+  uint32_t svo[kSL];
 #pragma unroll
-  for (int t = 0; t < T; ++t) {
-    const uint32_t ct = ct0 + t;
-    const bool ok = ct < sg.ntiles;
-    wrs[t] = make_rsrc(sg.Wp + (size_t)(ok ? ct : 0u) * d.nkb * 64u * WPL, ok ? tile_bytes : 0u);
-    // Padding columns read column N-1's scale; their outputs are never stored.
-    soff[t] = min(ct * 16u + c16, sg.N - 1u) * 2u;
-  }
-  const __amdgpu_buffer_rsrc_t srs = make_rsrc(sg.S, (d.nkb / d.gkb) * sg.N * 2u);
-  const uint32_t srow = sg.N * 2u;
+  for (int j = 0; j < kSL; ++j) svo[j] = 0;
 
-  // Register ring: slot u holds k-block kb0 + u (mod U) of weights, scales and activations,
-  // issued together. vmcnt retires loads in issue order, so anything fetched later than
-  // the weights it is used with would drain the whole ring; one issue point per k-block
-  // keeps U - 1 k-blocks in flight. Loads past the wave's range read zero.
+  // Segment of slab g; a plain loop so the segment table is read on demand, not held.
+  auto seg_of = [&](uint32_t g) {
+    uint32_t s = 0;
+    for (uint32_t i = 1; i < d.nseg; ++i)
+      if (g >= d.seg[i].blk_begin) s = i;
+    return __builtin_amdgcn_readfirstlane(s);
+  };
+  auto open_piece = [&](uint32_t i) {  // set the load extents for piece i (< np)
+    const Piece p = piece(i);
+    const uint32_t s = seg_of(p.g);
+    const uint32_t ct0 = (p.g - d.seg[s].blk_begin) * T;
+    const uint32_t N = d.seg[s].N;
+    const uint32_t nv = min((uint32_t)T, d.seg[s].ntiles - ct0);
+    lw_base = d.seg[s].Wp + (size_t)ct0 * nkb * 64u * WPL;
+    lw_num = __builtin_amdgcn_readfirstlane(nv * nkb * kBlockBytes);
+    ls_base = d.seg[s].S;
+    ls_num = __builtin_amdgcn_readfirstlane((nkb / d.gkb) * N * 2u);
+    lsrow = __builtin_amdgcn_readfirstlane(N * 2u);
+#pragma unroll
+    for (int j = 0; j < kSL; ++j) svo[j] = min(ct0 * 16u + 64u * j + lane % kCols, N - 1u) * 2u;
+    lkb = span_begin(p, wave);
+    lkz = span_end(p, wave);
+  };
+  // Move to the next piece in which this wavefront has units (or past the last one).
+  auto next_load_piece = [&]() {
+    while (lp < np) {
+      open_piece(lp);
+      if (lkb < lkz) return;
+      ++lp;
+    }
+    lw_num = 0;
+    lkb = 0;
+  };
+  auto advance_load = [&]() {
+    if (lp >= np) return;
+    lkb += kstep;
+    if (lkb >= lkz) {
+      ++lp;
+      next_load_piece();
+    }
+  };
+
+  // Register ring: slot u holds one unit's weights, scales and activations, issued
+  // together. vmcnt retires loads in issue order, so anything fetched later than the
+  // weights it is used with would drain the whole ring; one issue point per unit keeps
+  // U - 1 units in flight. Loads past the wavefront's units read zero.
   W wr[U][T];
-  uint16_t sr[U][T];
+  uint32_t sr[U][kSL];
   u4 ar[U][4];
-  auto load = [&](int slot, uint32_t kb) {
-    const bool ok = kb < kb1;
-    // Scales past the range re-read the last group (2 bytes, cached) instead of branching.
-    const uint32_t grp = min(kb, kb1 - 1u) / d.gkb;
+  auto load = [&](int slot) {
+    const __amdgpu_buffer_rsrc_t lw = make_rsrc(lw_base, lw_num);
+    const __amdgpu_buffer_rsrc_t ls = make_rsrc(ls_base, ls_num);
+    const __amdgpu_buffer_rsrc_t lx = xr;
+    const uint32_t kbo = __builtin_amdgcn_readfirstlane(lkb * kBlockBytes);
+    const uint32_t so = __builtin_amdgcn_readfirstlane(plan_group_of_kb(lkb, pl.gmul) * lsrow);
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-      const uint32_t wo = ok ? (kb * 64u + lane) * WPL * 4u : kOutOfRange;
-      if constexpr (WPL == 4) wr[slot][t] = __builtin_amdgcn_raw_buffer_load_b128(wrs[t], wo, 0, kStreamAux);
-      else wr[slot][t] = __builtin_amdgcn_raw_buffer_load_b64(wrs[t], wo, 0, kStreamAux);
-      sr[slot][t] = __builtin_amdgcn_raw_buffer_load_b16(srs, grp * srow + soff[t], 0, 0);
+      if constexpr (WPL == 4) wr[slot][t] = __builtin_amdgcn_raw_buffer_load_b128(lw, wvo[t], kbo, kStreamAux);
+      else wr[slot][t] = __builtin_amdgcn_raw_buffer_load_b64(lw, wvo[t], kbo, kStreamAux);
     }
-    const uint32_t base = ok ? xoff + kb * 256u : kOutOfRange;
 #pragma unroll
-    for (int c = 0; c < 4; ++c) ar[slot][c] = __builtin_amdgcn_raw_buffer_load_b128(xr, base, c * 64u, 0);
+    for (int j = 0; j < kSL; ++j) sr[slot][j] = __builtin_amdgcn_raw_buffer_load_b16(ls, svo[j], so, 0);
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+      ar[slot][c] = __builtin_amdgcn_raw_buffer_load_b128(lx, xo + c * 64u, __builtin_amdgcn_readfirstlane(lkb * 256u), 0);
   };
 
-  const DqConst dqk = DT == HQ_DTYPE_F16 ? dq_const_f16() : dq_const_bf16();
-  f4 acc[T], gacc[T];
-#pragma unroll
-  for (int t = 0; t < T; ++t) {
-    acc[t] = f4{0.f, 0.f, 0.f, 0.f};
-    gacc[t] = f4{0.f, 0.f, 0.f, 0.f};
-  }
-  f4 corr = f4{0.f, 0.f, 0.f, 0.f};
-
-  // Issue the prologue in slot order (no reordering across the barriers): the loop
-  // header's wait count is the worst case over both paths into it, so the preheader
-  // must leave slot 0 as the oldest load, as the loop latch does.
-#pragma unroll
-  for (int u = 0; u < U; ++u) {
-    load(u, kb0 + u);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-
-  for (uint32_t kb = kb0; kb < kb1; kb += U) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const uint32_t k = kb + u;
-      if (k < kb1) {  // uniform; no loads inside, so waitcnt stays exact across it
-#pragma unroll
-        for (int t = 0; t < T; ++t) {
-#pragma unroll
-          for (int c = 0; c < 4; ++c)
-            gacc[t] = mfma16x16x32<DT>(ar[u][c], dequant_chunk<FMT, DT>(wr[u][t], c, dqk), gacc[t]);
-        }
-        if constexpr (kBiased) {
-          const u4 neg = u4{kBf16NegOneHalf2, kBf16NegOneHalf2, kBf16NegOneHalf2, kBf16NegOneHalf2};
-#pragma unroll
-          for (int c = 0; c < 4; ++c) corr = mfma16x16x32<DT>(ar[u][c], neg, corr);
-        }
-        if ((k + 1u) % d.gkb == 0u) {
-#pragma unroll
-          for (int t = 0; t < T; ++t) {
-            float sc = f16_to_f32(sr[u][t]);
-            if constexpr (FMT == HQ_FORMAT_TERNARY2) {
-              // A non-finite block scale drops the block (native_decoder.cu:174); fields hold 2t.
-              sc = __builtin_isfinite(sc) ? 0.5f * sc : 0.0f;
-            }
-            if constexpr (kBiased) {
-              sc *= 16.0f;
-              gacc[t] += corr;
-            }
-            acc[t] += gacc[t] * sc;
-            gacc[t] = f4{0.f, 0.f, 0.f, 0.f};
-          }
-          corr = f4{0.f, 0.f, 0.f, 0.f};
-        }
-      }
-      load(u, k + U);
+  // Compute-side iterator over the same sequence.
+  uint32_t cp = 0, ckb = 0, ckz = 0;
+  auto next_compute_piece = [&]() {
+    while (cp < np) {
+      const Piece p = piece(cp);
+      ckb = span_begin(p, wave);
+      ckz = span_end(p, wave);
+      if (ckb < ckz) return;
+      ++cp;
     }
-  }
-
-  // Output element e = (t * 4 + v) * 64 + ln: row 4 * (ln / 16) + v, column 16 * (ct0 + t) + ln % 16.
-  auto store = [&](uint32_t e, float val) {
-    const uint32_t t = e >> 8, v = (e >> 6) & 3u, ln = e & 63u;
-    const uint32_t row = 4u * (ln >> 4) + v;
-    const uint32_t n = (ct0 + t) * 16u + (ln & 15u);
-    if (row < d.M && n < sg.N && ct0 + t < sg.ntiles)
-      reinterpret_cast<uint16_t*>(sg.Y)[(size_t)row * sg.ldy + n] = f32_to_out<DT>(val);
   };
 
-  if (nwave == 1) {
+  f4 acc[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
+
+  // Park the current piece's sums (rows < M only) in this wavefront's LDS slot.
+  auto park = [&](uint32_t p) {
+    float* dst = red + (p * WK + wave) * SL;
 #pragma unroll
     for (int t = 0; t < T; ++t)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) store((t * 4 + v) * 64 + lane, acc[t][v]);
-    return;
+      for (int v = 0; v < 4; ++v) {
+        const uint32_t row = 4u * g4 + v;
+        if (row < M) dst[row * kCols + t * 16u + c16] = acc[t][v];
+        acc[t][v] = 0.0f;
+      }
+  };
+
+  const DqBiasConst dqb = DT == HQ_DTYPE_F16 ? dq_bias_const_f16() : dq_bias_const_bf16();
+  const u4 corr_b = int4_corr_fragment<DT>();
+
+  auto compute = [&](int u) {
+    // Scale of tile t for this lane's column, gathered first so the LDS-crossbar
+    // latency overlaps the MFMAs.
+    uint32_t sbits[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+      sbits[t] = T == 1 ? sr[u][0]
+                        : (uint32_t)__builtin_amdgcn_ds_bpermute((int)((16u * (t % 4) + c16) * 4u), (int)sr[u][t / 4]);
+    f4 seed = f4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (kInt4) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) seed = mfma16x16x32<DT>(ar[u][c], corr_b, seed);
+    }
+    // Chunk-outer order: the T accumulation chains are independent and interleave.
+    f4 g[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) g[t] = seed;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        u4 bf;
+        if constexpr (kInt4) {
+          bf = dq_int4_biased<DT>(wr[u][t][c], dqb);
+        } else {
+          const uint32_t word = wr[u][t][c >> 1];
+          bf = (c & 1) ? dq_tern2<1>(word) : dq_tern2<0>(word);
+        }
+        g[t] = mfma16x16x32<DT>(ar[u][c], bf, g[t]);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      float sc = f16_to_f32((uint16_t)sbits[t]);
+      if constexpr (!kInt4) {
+        // A non-finite block scale drops the block (native_decoder.cu:174); fields hold 2t.
+        sc = __builtin_isfinite(sc) ? 0.5f * sc : 0.0f;
+      }
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[t][v] = __builtin_fmaf(g[t][v], sc, acc[t][v]);
+    }
+  };
+
+  // Prologue: position both iterators and fill the ring in slot order (no reordering
+  // across the barriers: the loop header's wait count assumes slot 0 is the oldest load).
+  next_load_piece();
+  next_compute_piece();
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    load(u);
+    advance_load();
+    __builtin_amdgcn_sched_barrier(0);
   }
-  constexpr uint32_t per_wave = T * 4 * 64;
+
+  while (cp < np) {
 #pragma unroll
-  for (int t = 0; t < T; ++t)
-#pragma unroll
-    for (int v = 0; v < 4; ++v) red[wave * per_wave + (t * 4 + v) * 64 + lane] = acc[t][v];
+    for (int u = 0; u < U; ++u) {
+      if (cp < np) {  // uniform; no loads inside, so waitcnt stays exact across it
+        compute(u);
+        ckb += kstep;
+        if (ckb >= ckz) {
+          park(cp);
+          ++cp;
+          next_compute_piece();
+        }
+      }
+      load(u);
+      advance_load();
+    }
+  }
+
+  // Sum each piece over the wavefronts that worked on it, in wavefront order.
   __syncthreads();
-  for (uint32_t e = threadIdx.x; e < per_wave; e += blockDim.x) {
-    float sum = 0.0f;
-    for (uint32_t w = 0; w < nwave; ++w) sum += red[w * per_wave + e];
-    store(e, sum);
+  const uint32_t nthr = WK * 64u;
+  bool partial_any = false;
+  for (uint32_t i = 0; i < np; ++i) {
+    const Piece p = piece(i);
+    const SegDesc& sg = d.seg[seg_of(p.g)];
+    const uint32_t col0 = (p.g - sg.blk_begin) * kCols;
+
+    const bool full = p.ka == 0u && p.kz == nkb;
+    float* slot = full ? nullptr : pl.part + ((size_t)b * 2u + i) * SL;
+    partial_any |= !full;
+    for (uint32_t o = threadIdx.x; o < SL; o += nthr) {
+      float s = 0.0f;
+      for (uint32_t w = 0; w < WK; ++w)
+        if (span_begin(p, w) < span_end(p, w)) s += red[(i * WK + w) * SL + o];  // wavefronts with units
+      if (full) {
+        const uint32_t row = o / kCols, n = col0 + o % kCols;
+        if (n < sg.N) reinterpret_cast<uint16_t*>(sg.Y)[(size_t)row * sg.ldy + n] = f32_to_out<DT>(s);
+      } else {
+        // Agent-scope store (global_store sc1): coherent across XCDs once complete.
+        __hip_atomic_store(slot + o, s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+  }
+  if (!partial_any) return;  // uniform: depends only on the range
+
+  // Fix-up of partial pieces (pieces 0 and 1 only): publish, count arrivals, and let the
+  // last contributor of each slab sum all contributors' partials in workgroup order.
+  // The partials are agent-coherent stores; waiting for their completion before the
+  // barrier orders them before the arrival count without an L2 write-back, and the last
+  // contributor reads them with agent-coherent loads after seeing the count.
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  __syncthreads();
+  if (threadIdx.x < 2u) {
+    const uint32_t i = threadIdx.x;
+    uint32_t last = 0;
+    if (i < np) {
+      const Piece p = piece(i);
+      if (!(p.ka == 0u && p.kz == nkb)) {
+        const uint32_t bf = plan_wg_of_unit(pl.utot, pl.P, p.g * nkb);
+        const uint32_t bl = plan_wg_of_unit(pl.utot, pl.P, (p.g + 1u) * nkb - 1u);
+        const uint32_t old = __hip_atomic_fetch_add(pl.cnt + p.g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old == bl - bf) {
+          last = 1u;
+          __hip_atomic_store(pl.cnt + p.g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+    }
+    sh_last[i] = last;
+  }
+  __syncthreads();
+  const uint32_t last0 = sh_last[0], last1 = sh_last[1];
+  if (!(last0 | last1)) return;
+  for (uint32_t i = 0; i < 2u; ++i) {
+    if (!(i == 0 ? last0 : last1)) continue;
+    const Piece p = piece(i);
+    const SegDesc& sg = d.seg[seg_of(p.g)];
+    const uint32_t col0 = (p.g - sg.blk_begin) * kCols;
+    const uint32_t bf = plan_wg_of_unit(pl.utot, pl.P, p.g * nkb);
+    const uint32_t bl = plan_wg_of_unit(pl.utot, pl.P, (p.g + 1u) * nkb - 1u);
+    for (uint32_t o = threadIdx.x; o < SL; o += nthr) {
+      float s = 0.0f;
+      for (uint32_t c = bf; c <= bl; ++c) {
+        const uint32_t cslot = plan_begin(pl.utot, pl.P, c) / nkb == p.g ? 0u : 1u;
+        s += __hip_atomic_load(pl.part + ((size_t)c * 2u + cslot) * SL + o, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+      }
+      const uint32_t row = o / kCols, n = col0 + o % kCols;
+      if (n < sg.N) reinterpret_cast<uint16_t*>(sg.Y)[(size_t)row * sg.ldy + n] = f32_to_out<DT>(s);
+    }
   }
 }
-
-struct DecodeConfig {
-  int T;
-  int WK;
-};
 
 int env_int(const char* name, int dflt) {
   const char* v = std::getenv(name);
   return v && *v ? std::atoi(v) : dflt;
 }
 
-// Tiling choice (measured on MI355X over the 27B-class decode shapes): wide tiles (T=4)
-// amortise the activation fragments over 64 columns when N offers >= 1024 tiles, T=2
-// for mid-size N, T=1 below; four wavefronts per workgroup split K.
-DecodeConfig choose_decode(const GemmDesc& d) {
-  uint32_t tiles = 0;
-  for (uint32_t i = 0; i < d.nseg; ++i) tiles += d.seg[i].ntiles;
-  const uint32_t groups = d.nkb / d.gkb;
-  int T = tiles >= 1024 ? 4 : (tiles >= 300 ? 2 : 1);
-  int WK = 4;
-  const int eT = env_int("HQ_DECODE_T", 0), eWK = env_int("HQ_DECODE_WK", 0);
-  if (eT == 1 || eT == 2 || eT == 4) T = eT;
-  if (eWK >= 1) WK = eWK;
-  WK = std::max(1, std::min<int>(std::min<int>(WK, max_wk(T)), (int)groups));
-  return {T, WK};
+int cu_count() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  static std::mutex mu;
+  static int cached[64] = {0};
+  std::lock_guard<std::mutex> lock(mu);
+  if (dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+// Counter area at the start of every workspace, the same for all shapes so that one
+// workspace can serve calls of different shapes (the counters stay zero between calls;
+// the partial area after them does not).
+constexpr uint32_t kMaxCounters = 16384;
+constexpr size_t kCounterBytes = kMaxCounters * 4u;
+
+uint32_t total_slabs(const GemmDesc& d, int T) {
+  uint32_t g = 0;
+  for (uint32_t i = 0; i < d.nseg; ++i) g += (d.seg[i].ntiles + T - 1) / T;
+  return g;
+}
+
+// Dynamic LDS budget of one workgroup (160 KiB per CU, less the kernel's static LDS).
+constexpr size_t kLdsLimit = 160u * 1024u - 1024u;
+
+size_t lds_bytes(const GemmDesc& d, const DecodeConfig& c, uint32_t np_max) {
+  return (size_t)np_max * c.WK * d.M * 16u * c.T * sizeof(float);
 }
 
 template <int FMT, int DT, int T, int U>
-hipError_t launch_t(GemmDesc d, int WK, hipStream_t stream) {
+hipError_t launch_t(GemmDesc d, const DecodeConfig& c, void* ws, hipStream_t stream) {
+  DecodePlan pl{};
   uint32_t blk = 0;
   for (uint32_t i = 0; i < d.nseg; ++i) {
     d.seg[i].blk_begin = blk;
     d.seg[i].blk_count = (d.seg[i].ntiles + T - 1) / T;
     blk += d.seg[i].blk_count;
   }
-  const uint32_t groups = d.nkb / d.gkb;
-  const uint32_t gpw = (groups + WK - 1) / WK;
-  const uint32_t kb_per_wave = gpw * d.gkb;
-  const size_t lds = WK > 1 ? (size_t)WK * T * 4 * 64 * sizeof(float) : 0;
-  hipLaunchKernelGGL((hq_decode_kernel<FMT, DT, T, U>), dim3(blk), dim3(64 * WK), lds, stream, d, kb_per_wave);
+  pl.G = blk;
+  pl.utot = blk * d.nkb;
+  pl.P = (uint32_t)c.SK;
+  pl.WK = (uint32_t)c.WK;
+  pl.np_max = plan_np_max(pl.utot, pl.P, d.nkb);
+  pl.gmul = plan_gmul(d.gkb);
+  pl.contig = (uint32_t)c.contig;
+  if (plan_has_partial(pl.G, pl.P)) {
+    if (!ws) return hipErrorInvalidValue;
+    pl.cnt = static_cast<uint32_t*>(ws);
+    pl.part = reinterpret_cast<float*>(static_cast<char*>(ws) + kCounterBytes);
+  }
+  const size_t lds = lds_bytes(d, c, pl.np_max);
+  if (lds > kLdsLimit) return hipErrorInvalidConfiguration;
+  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&hq_decode_kernel<FMT, DT, T, U>),
+                                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsLimit);
+  if (attr != hipSuccess) return attr;
+  hipLaunchKernelGGL((hq_decode_kernel<FMT, DT, T, U>), dim3(pl.P), dim3(64 * c.WK), lds, stream, d, pl);
   return hipGetLastError();
 }
 
 template <int FMT, int DT>
-hipError_t launch_fd(GemmDesc d, hipStream_t stream) {
-  const DecodeConfig cfg = choose_decode(d);
-  switch (cfg.T) {
-    case 4: return launch_t<FMT, DT, 4, 4>(d, cfg.WK, stream);
-    case 2: return launch_t<FMT, DT, 2, 4>(d, cfg.WK, stream);
-    default: return launch_t<FMT, DT, 1, 4>(d, cfg.WK, stream);
+hipError_t launch_fd(const GemmDesc& d, const DecodeConfig& c, void* ws, hipStream_t stream) {
+  switch (c.T) {
+    case 8: return launch_t<FMT, DT, 8, 3>(d, c, ws, stream);
+    case 4: return launch_t<FMT, DT, 4, 4>(d, c, ws, stream);
+    case 2: return launch_t<FMT, DT, 2, 4>(d, c, ws, stream);
+    default: return launch_t<FMT, DT, 1, 4>(d, c, ws, stream);
   }
 }
 
 }  // namespace
 
-hipError_t launch_decode(int fmt, int dtype, GemmDesc d, hipStream_t stream) {
-  if (fmt == HQ_FORMAT_INT4) {
-    return dtype == HQ_DTYPE_F16 ? launch_fd<HQ_FORMAT_INT4, HQ_DTYPE_F16>(d, stream)
-                                 : launch_fd<HQ_FORMAT_INT4, HQ_DTYPE_BF16>(d, stream);
+// Tiling choice (measured on MI355X over the 27B-class decode shapes, see the tuning
+// notes of the decode kernel): the memory pipeline prefers few wavefronts per CU, each
+// with many bytes in flight, and whole slabs per workgroup (a cut slab costs a
+// fix-up round trip at the end):
+//   1. the widest slab (8, 4 or 2 tiles) whose slab count fills >= 80% of the CUs, one
+//      slab per workgroup;
+//   2. otherwise, for large weights (>= 24 MiB), 4-tile slabs each cut into
+//      floor(CUs / slabs) k-ranges (stream-K fix-up);
+//   3. otherwise (small weights, latency-bound) the widest slab giving >= 150 slabs
+//      (else 2-tile, else 1-tile slabs), uncut.
+// Four wavefronts per workgroup (two for M > 8 on small weights). Narrow outputs with
+// fewer than 16 tiles use 1-tile slabs. HQ_DECODE_T / _WK / _P / _CONTIG override.
+DecodeConfig choose_decode(int fmt, const GemmDesc& d) {
+  uint32_t tiles = 0;
+  for (uint32_t i = 0; i < d.nseg; ++i) tiles += d.seg[i].ntiles;
+  const uint32_t cus = (uint32_t)cu_count();
+  const double bytes = (double)tiles * 16.0 * d.K * (fmt == HQ_FORMAT_INT4 ? 0.5 : 0.25);
+  const bool large = bytes >= 24.0 * 1024 * 1024;
+  int T = 0, WK = 4;
+  long P = 0;
+  for (int t : {8, 4, 2}) {
+    const uint32_t g = total_slabs(d, t);
+    if (g * 5 >= cus * 4) {
+      T = t;
+      P = g;
+      break;
+    }
   }
-  return dtype == HQ_DTYPE_F16 ? launch_fd<HQ_FORMAT_TERNARY2, HQ_DTYPE_F16>(d, stream)
-                               : launch_fd<HQ_FORMAT_TERNARY2, HQ_DTYPE_BF16>(d, stream);
+  if (T == 0 && large) {
+    T = 4;
+    const uint32_t g = total_slabs(d, 4);
+    P = (long)g * std::max<uint32_t>(1, cus / std::max<uint32_t>(1, g));
+  }
+  if (T == 0) {
+    T = tiles >= 16 ? 2 : 1;
+    for (int t : {8, 4}) {
+      if (total_slabs(d, t) >= 150) {
+        T = t;
+        break;
+      }
+    }
+    P = total_slabs(d, T);
+    if (d.M > 8) WK = 2;
+  }
+  bool contig = true;
+  const int eT = env_int("HQ_DECODE_T", 0);
+  if (eT == 1 || eT == 2 || eT == 4 || eT == 8) {
+    T = eT;
+    P = total_slabs(d, T);
+  }
+  const int eWK = env_int("HQ_DECODE_WK", 0);
+  if (eWK >= 1) WK = eWK;
+  WK = std::min(WK, max_wk(T));
+  const int eP = env_int("HQ_DECODE_P", 0);
+  if (eP >= 1) P = eP;
+  const char* ec = std::getenv("HQ_DECODE_CONTIG");
+  if (ec && *ec) contig = std::atoi(ec) != 0;
+  const uint32_t utot = total_slabs(d, T) * d.nkb;
+  // More slabs than counters: use a grid that never cuts a slab.
+  if (total_slabs(d, T) > kMaxCounters) P = total_slabs(d, T);
+  P = std::max(1L, std::min<long>(P, utot));
+  DecodeConfig c{T, WK, (int)P, contig};
+  // Grow the grid (fewer slabs per workgroup) until the per-piece LDS slots fit; with one
+  // unit per workgroup a piece needs M * 16 * T floats per wavefront, which always fits.
+  while ((uint32_t)c.SK < utot && lds_bytes(d, c, plan_np_max(utot, (uint32_t)c.SK, d.nkb)) > kLdsLimit)
+    c.SK = (int)std::min<long>(utot, (long)c.SK * 4 / 3 + 1);
+  return c;
+}
+
+size_t decode_workspace_bytes(const GemmDesc& d, const DecodeConfig& c) {
+  const uint32_t G = total_slabs(d, c.T);
+  if (!plan_has_partial(G, (uint32_t)c.SK)) return 0;
+  return kCounterBytes + (size_t)c.SK * 2u * d.M * 16u * c.T * sizeof(float);
+}
+
+hipError_t launch_decode(int fmt, int dtype, GemmDesc d, const DecodeConfig& c, void* ws, hipStream_t stream) {
+  if (fmt == HQ_FORMAT_INT4) {
+    return dtype == HQ_DTYPE_F16 ? launch_fd<HQ_FORMAT_INT4, HQ_DTYPE_F16>(d, c, ws, stream)
+                                 : launch_fd<HQ_FORMAT_INT4, HQ_DTYPE_BF16>(d, c, ws, stream);
+  }
+  return dtype == HQ_DTYPE_F16 ? launch_fd<HQ_FORMAT_TERNARY2, HQ_DTYPE_F16>(d, c, ws, stream)
+                               : launch_fd<HQ_FORMAT_TERNARY2, HQ_DTYPE_BF16>(d, c, ws, stream);
 }
 
 }  // namespace hq

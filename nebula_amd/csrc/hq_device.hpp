@@ -105,6 +105,48 @@ __device__ __forceinline__ u4 dq_int4_bf16_biased(uint32_t w, const DqConst& k) 
             ((w >> 9) & k.lo) | k.magic};
 }
 
+// Biased int4 dequantisation (decode path): each nibble q is OR-ed into the mantissa of a
+// power of two chosen so that its unit in the last place is 1, giving the exact value
+// magic + q with one v_and_or_b32 per 32-bit word of the fragment:
+//   fp16: nibble at bits 0..3 -> 1024 + q (0x6400), bits 4..7 -> 64 + q (0x5400);
+//   bf16: nibble at bits 0..3 -> 128 + q (0x4300), bits 3..6 -> 16 + q (0x4180).
+// The bias magic + 8 is removed after the MFMA: the caller seeds each tile's accumulator
+// with MFMA(x, kInt4Corr*), i.e. -sum_k x_k (magic_k + 8) over the same chunk, so the
+// result is sum_k x_k (q_k - 8) with exact products and fp32 accumulation.
+struct DqBiasConst {
+  uint32_t m_lo, m_hi;  // nibble masks (SGPR)
+  uint32_t v_lo, v_hi;  // magics (VGPR)
+};
+__device__ __forceinline__ DqBiasConst dq_bias_const_f16() {
+  return {opaque_sgpr(0x000F000Fu), opaque_sgpr(0x00F000F0u), opaque_vgpr(0x64006400u), opaque_vgpr(0x54005400u)};
+}
+__device__ __forceinline__ DqBiasConst dq_bias_const_bf16() {
+  return {opaque_sgpr(0x000F000Fu), opaque_sgpr(0x00780078u), opaque_vgpr(0x43004300u), opaque_vgpr(0x41804180u)};
+}
+// Correction fragments (every chunk alike): -(1024 + 8), -(64 + 8) in fp16; -(128 + 8),
+// -(16 + 8) in bf16, matching the magic of each fragment word.
+constexpr uint32_t kInt4CorrF16Lo = 0xE408E408u, kInt4CorrF16Hi = 0xD480D480u;
+constexpr uint32_t kInt4CorrBf16Lo = 0xC308C308u, kInt4CorrBf16Hi = 0xC1C0C1C0u;
+
+template <int DT>
+__device__ __forceinline__ u4 int4_corr_fragment() {
+  if constexpr (DT == HQ_DTYPE_F16) return u4{kInt4CorrF16Lo, kInt4CorrF16Hi, kInt4CorrF16Lo, kInt4CorrF16Hi};
+  else return u4{kInt4CorrBf16Lo, kInt4CorrBf16Hi, kInt4CorrBf16Lo, kInt4CorrBf16Hi};
+}
+
+// int4 word (tile nibble order: elements (0,1) at nibbles (0,4), (2,3) at (1,5), (4,5) at
+// (2,6), (6,7) at (3,7)) -> biased fragment.
+template <int DT>
+__device__ __forceinline__ u4 dq_int4_biased(uint32_t w, const DqBiasConst& k) {
+  if constexpr (DT == HQ_DTYPE_F16) {
+    const uint32_t h = w >> 8;
+    return u4{(w & k.m_lo) | k.v_lo, (w & k.m_hi) | k.v_hi, (h & k.m_lo) | k.v_lo, (h & k.m_hi) | k.v_hi};
+  } else {
+    return u4{(w & k.m_lo) | k.v_lo, ((w >> 1) & k.m_hi) | k.v_hi, ((w >> 8) & k.m_lo) | k.v_lo,
+              ((w >> 9) & k.m_hi) | k.v_hi};
+  }
+}
+
 // Ternary word -> fragment of chunk CW (0 or 1): elements 2t in fp16 and in bf16
 // (the 2-bit field is the sign bit and the top exponent bit of +-2.0).
 template <int CW>

@@ -31,8 +31,22 @@ struct GemmDesc {
   SegDesc seg[HQ_MAX_SEGMENTS];
 };
 
+// Decode tiling: T column tiles per wavefront, WK wavefronts splitting K inside a
+// workgroup (LDS reduction), SK workgroups splitting K across the grid (workspace fixup).
+struct DecodeConfig {
+  int T;
+  int WK;
+  int SK;      // workgroups (stream-K grid size)
+  bool contig; // wavefronts take contiguous k runs of a piece (else interleaved)
+};
+DecodeConfig choose_decode(int fmt, const GemmDesc& d);
+// Workspace bytes a decode launch with this config needs (0 when SK == 1). The first
+// 256 bytes-aligned part holds one uint32 counter per column group; these must be zero
+// before the first launch and are left zero by every launch.
+size_t decode_workspace_bytes(const GemmDesc& d, const DecodeConfig& c);
+
 // Decode (M <= 16): HBM-streaming MFMA kernel. Validated descriptor in, status out.
-hipError_t launch_decode(int fmt, int dtype, GemmDesc d, hipStream_t stream);
+hipError_t launch_decode(int fmt, int dtype, GemmDesc d, const DecodeConfig& c, void* ws, hipStream_t stream);
 // Prefill (M > 16): MFMA tile kernel.
 hipError_t launch_prefill(int fmt, int dtype, GemmDesc d, hipStream_t stream);
 

@@ -1,0 +1,70 @@
+// hq_plan.hpp — work decomposition of the decode kernel, shared by host and device code.
+//
+// The output columns of all segments are cut into "slabs" of T column tiles (16 columns
+// each); a unit of work is one slab times one 128-deep k-block, and units are numbered
+// slab-major: u = g * nkb + kb. The grid has P workgroups and workgroup b owns the
+// contiguous unit range [begin(b), begin(b + 1)), begin(b) = floor(b * utot / P), so
+// every workgroup streams the same number of weight bytes (+-1 unit) whatever N and K
+// are. A slab whose k range is cut by a range boundary ("partial piece") is finished by
+// a fix-up: every contributing workgroup writes its fp32 partial tile to the workspace,
+// and the last one to arrive (per-slab counter) sums the partials in workgroup order and
+// stores the output, so the result does not depend on arrival order.
+//
+// Inside a workgroup, pieces are numbered: 0 = the slab of the first unit, 1 = the slab
+// of the last unit (when different), 2.. = the slabs in between (always whole). Only
+// pieces 0 and 1 can be partial; their partials go to workspace slots 0 and 1 of the
+// workgroup.
+#pragma once
+#include <stdint.h>
+
+#include "hq_layout.hpp"
+
+namespace hq {
+
+struct DecodePlan {
+  uint32_t G;     // slabs over all segments
+  uint32_t utot;  // G * nkb
+  uint32_t P;     // workgroups
+  uint32_t WK;    // wavefronts per workgroup
+  uint32_t np_max;  // largest number of pieces of one workgroup
+  uint32_t gmul;    // ceil(2^32 / gkb) for the k-block -> scale-group division (0 when gkb == 1)
+  uint32_t contig;  // 1: wavefront w takes k-blocks [ka + w*len/WK, ka + (w+1)*len/WK) of a piece;
+                    // 0: k-blocks ka + w, ka + w + WK, ...
+  float* part;      // [P][2][M * 16 * T] partial tiles (null when no piece is partial)
+  uint32_t* cnt;    // [G] arrival counters, zero between launches
+};
+
+HQ_HD uint32_t plan_begin(uint32_t utot, uint32_t P, uint32_t b) { return (uint32_t)((uint64_t)b * utot / P); }
+
+// Workgroup whose range holds unit u: the largest b with begin(b) <= u.
+HQ_HD uint32_t plan_wg_of_unit(uint32_t utot, uint32_t P, uint32_t u) {
+  return (uint32_t)(((uint64_t)(u + 1) * P - 1) / utot);
+}
+
+// Largest piece count of any workgroup: a range of at most ceil(utot / P) units touches
+// at most floor((L - 1) / nkb) + 2 slabs.
+HQ_HD uint32_t plan_np_max(uint32_t utot, uint32_t P, uint32_t nkb) {
+  if (utot % P == 0 && (utot / P) % nkb == 0) return utot / P / nkb;  // ranges aligned to slabs
+  const uint32_t L = (utot + P - 1) / P;
+  const uint32_t n = (L - 1) / nkb + 2;
+  const uint32_t g = utot / nkb;
+  return n < g ? n : g;
+}
+
+// Slab of piece i of a workgroup whose slabs run from gfirst to glast.
+HQ_HD uint32_t plan_piece_slab(uint32_t gfirst, uint32_t glast, uint32_t i) {
+  return i == 0 ? gfirst : (i == 1 ? glast : gfirst + i - 1);
+}
+
+// Whether some workgroup range boundary falls inside a slab.
+HQ_HD bool plan_has_partial(uint32_t G, uint32_t P) { return G % P != 0; }
+
+// k-block -> scale group with the multiplier of DecodePlan::gmul (exact for kb * gkb < 2^32).
+HQ_HD uint32_t plan_group_of_kb(uint32_t kb, uint32_t gmul) {
+  return gmul == 0 ? kb : (uint32_t)(((uint64_t)kb * gmul) >> 32);
+}
+HQ_HD uint32_t plan_gmul(uint32_t gkb) {
+  return gkb == 1 ? 0u : (uint32_t)((((uint64_t)1 << 32) + gkb - 1) / gkb);
+}
+
+}  // namespace hq

@@ -180,20 +180,38 @@ def repack_device(fmt: int, linear, K: int, N: int, stream=None, bad_flag=None):
     return out
 
 
-def gemm(fmt: int, X, Wp, scales, N: int, group: int = 128, out=None, stream=None):
-    """Y[M, N] = X[M, K] @ dequant(Wp) with fp32 accumulation (Y in X's dtype)."""
+def workspace_bytes(fmt: int, M: int, K: int, N: int, group: int = 128) -> int:
+    """Bytes of the decode fix-up workspace for this shape on the current device (0: none)."""
+    b = ctypes.c_size_t(0)
+    check(lib().hq_workspace_bytes(fmt, M, K, N, group, ctypes.byref(b)))
+    return int(b.value)
+
+
+def _ws(workspace):
+    """(pointer, bytes) of a caller workspace tensor (zero-filled before first use), or (None, 0)."""
+    if workspace is None:
+        return None, 0
+    return workspace.data_ptr(), workspace.numel() * workspace.element_size()
+
+
+def gemm(fmt: int, X, Wp, scales, N: int, group: int = 128, out=None, stream=None, workspace=None):
+    """Y[M, N] = X[M, K] @ dequant(Wp) with fp32 accumulation (Y in X's dtype).
+
+    workspace: optional device tensor of at least workspace_bytes() bytes, zero-filled
+    before its first use; by default the library's own per-stream buffer is used."""
     import torch
 
     M, K = X.shape
     if out is None:
         out = torch.empty((M, N), dtype=X.dtype, device=X.device)
     f = lib().hq_gemm_w4a16 if fmt == FORMAT_INT4 else lib().hq_gemm_w2a16
+    wp, wb = _ws(workspace)
     check(f(X.data_ptr(), _dt(X), X.stride(0), Wp.data_ptr(), scales.data_ptr(), out.data_ptr(), out.stride(0),
-            M, K, N, group, None, 0, _stream_ptr(stream)))
+            M, K, N, group, wp, wb, _stream_ptr(stream)))
     return out
 
 
-def gemm_fused(fmt: int, X, segments: Sequence[tuple], group: int = 128, outs=None, stream=None):
+def gemm_fused(fmt: int, X, segments: Sequence[tuple], group: int = 128, outs=None, stream=None, workspace=None):
     """segments: (Wp, scales, N) per projection; returns one output per segment."""
     import torch
 
@@ -203,6 +221,7 @@ def gemm_fused(fmt: int, X, segments: Sequence[tuple], group: int = 128, outs=No
     arr = (Segment * len(segments))()
     for i, ((wp, sc, n), y) in enumerate(zip(segments, outs)):
         arr[i] = Segment(wp.data_ptr(), sc.data_ptr(), y.data_ptr(), y.stride(0), n)
-    check(lib().hq_gemm_fused(X.data_ptr(), _dt(X), X.stride(0), fmt, arr, len(segments), M, K, group, None, 0,
+    wp, wb = _ws(workspace)
+    check(lib().hq_gemm_fused(X.data_ptr(), _dt(X), X.stride(0), fmt, arr, len(segments), M, K, group, wp, wb,
                               _stream_ptr(stream)))
     return outs

@@ -43,8 +43,39 @@ def test_sizes():
     assert hq.packed_words(hq.FORMAT_INT4, 128, 17) == 2 * 256  # N padded to 32
     assert hq.packed_words(hq.FORMAT_TERNARY2, 256, 16) == 2 * 128
     assert hq.packed_words(hq.FORMAT_INT4, 100, 16) == 0
+
+
+def workspace_bytes(fmt, M, K, N, group=128):
     b = ctypes.c_size_t(99)
-    assert hq.lib().hq_workspace_bytes(1, 16, 4096, 4096, 128, ctypes.byref(b)) == 0 and b.value == 0
+    st = hq.lib().hq_workspace_bytes(fmt, M, K, N, group, ctypes.byref(b))
+    return st, b.value
+
+
+def test_workspace_bytes():
+    # Large decode shapes with few column tiles cut their slabs along K and need a fix-up
+    # workspace: a fixed counter area plus fp32 partial tiles that scale with M.
+    st, b16 = workspace_bytes(hq.FORMAT_INT4, 16, 27648, 5120)
+    st1, b1 = workspace_bytes(hq.FORMAT_INT4, 1, 27648, 5120)
+    assert st == st1 == hq.HQ_OK
+    assert b16 > b1 > 0 and b16 % 256 == 0 and b1 % 256 == 0
+    assert (b16 - 65536) == 16 * (b1 - 65536)  # fixed 64 KiB counter area, then M-row partial tiles
+    # Prefill shapes need none.
+    assert workspace_bytes(hq.FORMAT_INT4, 17, 4096, 4096) == (hq.HQ_OK, 0)
+    assert workspace_bytes(hq.FORMAT_TERNARY2, 2048, 5120, 27648) == (hq.HQ_OK, 0)
+    # Bad shapes are reported, not sized.
+    assert workspace_bytes(hq.FORMAT_INT4, 16, 4000, 4096)[0] == hq.HQ_ERR_SHAPE
+    assert workspace_bytes(hq.FORMAT_INT4, 16, 4096, 4096, group=64)[0] == hq.HQ_ERR_SHAPE
+    assert workspace_bytes(hq.FORMAT_INT4, 0, 4096, 4096)[0] == hq.HQ_ERR_SHAPE
+    assert workspace_bytes(7, 16, 4096, 4096)[0] == hq.HQ_ERR_INVALID_ARG
+
+
+def test_workspace_checked_before_launch():
+    L = hq.lib()
+    _, need = workspace_bytes(hq.FORMAT_INT4, 16, 27648, 5120)
+    args = (0x1000, 1, 27648, 0x2000, 0x3000, 0x4000, 5120, 16, 27648, 5120, 128)
+    assert L.hq_gemm_w4a16(*args, 0x10000, need - 1, None) == hq.HQ_ERR_WORKSPACE
+    assert b"smaller" in L.hq_last_error()
+    assert L.hq_gemm_w4a16(*args, 0x10010, need, None) == hq.HQ_ERR_ALIGNMENT
 
 
 # ---------------------------------------------------------------- validation (no device work)

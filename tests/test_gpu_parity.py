@@ -121,9 +121,17 @@ def test_zero_point_and_one_hot_exact(cuda):
     Wdq = O.dequant(O.INT4, P.W, P.scales.ravel(), K, N, 128)
     expect = O.to_f32(O.from_f32(Wdq[ks], O.F16), O.F16)  # the dequantised row, rounded to fp16 once
     assert np.array_equal(y, expect)
+    # All weights at the zero point. The decode kernel dequantises int4 to magic + q (magic
+    # 1024 or 64 per fragment word) and removes magic + 8 with a correction MFMA, so q = 8
+    # leaves only the fp32 rounding of per-k-block sums of at most 1032 |x| (8 dependent
+    # MFMAs, each rounding at most twice): |y| <= 16 * 2^-24 * 1032 * sum_kb (sum|x|) s.
     W8 = np.full((K // 8) * N, 0x88888888, dtype=np.uint32)
-    y0 = hq.gemm(O.INT4, D.X, to_dev_u32(hq.repack(O.INT4, W8, K, N)), D.S, N)
-    assert np.all(to_host_f32(y0) == 0)
+    y0 = to_host_f32(hq.gemm(O.INT4, D.X, to_dev_u32(hq.repack(O.INT4, W8, K, N)), D.S, N))
+    xsum = np.abs(O.to_f32(P.X, O.F16).astype(np.float64)).reshape(P.M, K // 128, 128).sum(-1)
+    s = O.to_f32(P.scales, O.F16).astype(np.float64).reshape(K // 128, N)
+    bound = 16 * 2.0**-24 * 1032 * xsum @ np.abs(s)
+    assert np.all(np.abs(y0) <= bound), np.abs(y0).max()
+    assert np.abs(y0).max() < 1e-3
 
 
 def test_ternary_nonfinite_scale_drops_group(cuda):
@@ -228,3 +236,90 @@ def test_device_repack_matches_host(cuda, fmt):
         hq.repack_device(fmt, to_dev_u32(W), K, N, bad_flag=flag)
         torch.cuda.synchronize()
         assert int(flag.item()) == 1
+
+
+# ---------------------------------------------------------------- decode work decomposition
+class decode_env:
+    """Force the decode decomposition (slab width T, wavefronts WK, workgroups P) for a block."""
+
+    def __init__(self, **kv):
+        self.kv = {f"HQ_DECODE_{k}": str(v) for k, v in kv.items()}
+
+    def __enter__(self):
+        import os
+
+        self.old = {k: os.environ.get(k) for k in self.kv}
+        os.environ.update(self.kv)
+
+    def __exit__(self, *exc):
+        import os
+
+        for k, v in self.old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
+
+
+# (T, WK, P): one workgroup for everything, grids that cut every slab several times (with
+# wavefronts left without units in short pieces), and grids aligned to the slabs.
+DECOMP = [(4, 8, 1), (4, 8, 7), (4, 3, 64), (4, 8, 256), (4, 1, 997), (2, 8, 30), (2, 5, 513), (1, 16, 63),
+          (1, 3, 300), (4, 8, 16), (8, 8, 8), (8, 4, 3), (8, 2, 100)]
+
+
+@pytest.mark.parametrize("contig", [0, 1])
+@pytest.mark.parametrize("T,WK,Pg", DECOMP)
+@pytest.mark.parametrize("M", [1, 7, 16])
+def test_decode_decompositions_int4(cuda, T, WK, Pg, M, contig):
+    # K = 2048 (16 k-blocks), N = 1000 (63 tiles, ragged): 16 slabs of 4 tiles. contig
+    # selects contiguous per-wavefront k runs instead of interleaved k-blocks.
+    P = O.Problem(O.INT4, M, 2048, 1000, 128, O.F16, seed=2000 + M)
+    D = DeviceProblem(P)
+    with decode_env(T=T, WK=WK, P=Pg, CONTIG=contig):
+        y = D.run()
+    check(y, P.reference(), O.F16, f"T={T} WK={WK} P={Pg} M={M} contig={contig}", P)
+
+
+@pytest.mark.parametrize("fmt,xdt", [(O.INT4, O.BF16), (O.TERNARY2, O.F16), (O.TERNARY2, O.BF16)])
+@pytest.mark.parametrize("T,WK,Pg,contig", [(4, 8, 5, 0), (2, 4, 77, 1), (1, 16, 200, 0), (4, 3, 40, 1), (8, 8, 6, 1),
+                                             (8, 3, 50, 0)])
+def test_decode_decompositions_formats(cuda, fmt, xdt, T, WK, Pg, contig):
+    P = O.Problem(fmt, 9, 1536, 700, 256, xdt, seed=2100)
+    D = DeviceProblem(P)
+    with decode_env(T=T, WK=WK, P=Pg, CONTIG=contig):
+        y = D.run()
+    check(y, P.reference(), xdt, f"fmt={fmt} T={T} WK={WK} P={Pg}", P)
+
+
+@pytest.mark.parametrize("Pg", [3, 50, 333])
+def test_decode_fused_decompositions(cuda, Pg):
+    # Ranges that start in one segment and end in the next.
+    Ns, K, M = [600, 130, 1000], 1024, 5
+    probs = [O.Problem(O.INT4, M, K, n, 128, O.F16, seed=2200 + i) for i, n in enumerate(Ns)]
+    for p in probs[1:]:
+        p.X = probs[0].X
+    devs = [DeviceProblem(p) for p in probs]
+    with decode_env(P=Pg):
+        outs = hq.gemm_fused(O.INT4, devs[0].X, [(d.Wp, d.S, d.P.N) for d in devs])
+    for d, y in zip(devs, outs):
+        check(y, d.P.reference(), O.F16, f"fused P={Pg} N={d.P.N}", d.P)
+
+
+def test_decode_caller_workspace_reused(cuda):
+    import torch
+
+    K, N = 27648, 5120
+    P16 = O.Problem(O.INT4, 16, K, N, 128, O.F16, seed=2300)
+    D = DeviceProblem(P16)
+    need = hq.workspace_bytes(O.INT4, 16, K, N)
+    assert need > 0
+    ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
+    y_int = D.run()
+    y_ws = hq.gemm(O.INT4, D.X, D.Wp, D.S, N, workspace=ws)
+    assert torch_equal(y_ws, y_int)  # same decomposition, fixed summation order
+    # Second call on the same workspace with fewer rows: counters were left at zero.
+    y_ws4 = hq.gemm(O.INT4, D.X[:4].contiguous(), D.Wp, D.S, N, workspace=ws)
+    assert torch_equal(y_ws4, D.run(X=D.X[:4].contiguous()))
+    check(y_ws, P16.reference(), O.F16, "caller workspace")
+    torch.cuda.synchronize()
+    assert int(ws[:4 * ((N + 15) // 16)].view(torch.int32).abs().sum().item()) == 0
