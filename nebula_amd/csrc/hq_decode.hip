@@ -290,38 +290,53 @@ __global__ void __launch_bounds__(64 * max_wk(T)) hq_decode_kernel(const GemmDes
     }
   }
 
-  // Sum each piece over the wavefronts that worked on it, in wavefront order.
+  // Epilogue. Each piece's tile is summed over the wavefronts that worked on it, in
+  // wavefront order, four consecutive columns per thread (16-byte LDS reads).
   __syncthreads();
   const uint32_t nthr = WK * 64u;
+  const uint32_t SL4 = SL / 4u;  // SL is a multiple of 16
+  // The workspace partials as a buffer, accessed 16 bytes at a time with the sc1 cache
+  // policy: agent-coherent (visible across XCDs once the store has completed).
+  constexpr int kCoherent = 16;
+  const __amdgpu_buffer_rsrc_t partr = make_rsrc(pl.part, pl.part ? pl.P * 2u * SL * 4u : 0u);
+  auto store4 = [&](const SegDesc& sg, uint32_t col0, uint32_t o4, f4 v) {
+    const uint32_t o = 4u * o4, row = o / kCols, n = col0 + o % kCols;
+    uint16_t* y = reinterpret_cast<uint16_t*>(sg.Y) + (size_t)row * sg.ldy + n;
+    if (n + 3u < sg.N && (reinterpret_cast<uintptr_t>(y) & 7u) == 0) {
+      const u2 packed = {(uint32_t)f32_to_out<DT>(v[0]) | ((uint32_t)f32_to_out<DT>(v[1]) << 16),
+                         (uint32_t)f32_to_out<DT>(v[2]) | ((uint32_t)f32_to_out<DT>(v[3]) << 16)};
+      *reinterpret_cast<u2*>(y) = packed;
+    } else {
+#pragma unroll
+      for (uint32_t e = 0; e < 4u; ++e)
+        if (n + e < sg.N) y[e] = f32_to_out<DT>(v[e]);
+    }
+  };
   bool partial_any = false;
   for (uint32_t i = 0; i < np; ++i) {
     const Piece p = piece(i);
     const SegDesc& sg = d.seg[seg_of(p.g)];
     const uint32_t col0 = (p.g - sg.blk_begin) * kCols;
-
     const bool full = p.ka == 0u && p.kz == nkb;
-    float* slot = full ? nullptr : pl.part + ((size_t)b * 2u + i) * SL;
     partial_any |= !full;
-    for (uint32_t o = threadIdx.x; o < SL; o += nthr) {
-      float s = 0.0f;
+    uint32_t wmask = 0;  // wavefronts with units in this piece
+    for (uint32_t w = 0; w < WK; ++w)
+      if (span_begin(p, w) < span_end(p, w)) wmask |= 1u << w;
+    for (uint32_t o4 = threadIdx.x; o4 < SL4; o4 += nthr) {
+      f4 v = f4{0.f, 0.f, 0.f, 0.f};
       for (uint32_t w = 0; w < WK; ++w)
-        if (span_begin(p, w) < span_end(p, w)) s += red[(i * WK + w) * SL + o];  // wavefronts with units
-      if (full) {
-        const uint32_t row = o / kCols, n = col0 + o % kCols;
-        if (n < sg.N) reinterpret_cast<uint16_t*>(sg.Y)[(size_t)row * sg.ldy + n] = f32_to_out<DT>(s);
-      } else {
-        // Agent-scope store (global_store sc1): coherent across XCDs once complete.
-        __hip_atomic_store(slot + o, s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      }
+        if ((wmask >> w) & 1u) v += *reinterpret_cast<const f4*>(red + (i * WK + w) * SL + 4u * o4);
+      if (full) store4(sg, col0, o4, v);
+      else __builtin_amdgcn_raw_buffer_store_b128(v, partr, (((b * 2u + i) * SL) + 4u * o4) * 4u, 0, kCoherent);
     }
   }
   if (!partial_any) return;  // uniform: depends only on the range
 
   // Fix-up of partial pieces (pieces 0 and 1 only): publish, count arrivals, and let the
   // last contributor of each slab sum all contributors' partials in workgroup order.
-  // The partials are agent-coherent stores; waiting for their completion before the
-  // barrier orders them before the arrival count without an L2 write-back, and the last
-  // contributor reads them with agent-coherent loads after seeing the count.
+  // Waiting for the coherent partial stores to complete before the barrier orders them
+  // before the arrival count without an L2 write-back; the last contributor reads them
+  // with coherent loads after seeing the count.
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
   __syncthreads();
   if (threadIdx.x < 2u) {
@@ -344,6 +359,7 @@ __global__ void __launch_bounds__(64 * max_wk(T)) hq_decode_kernel(const GemmDes
   __syncthreads();
   const uint32_t last0 = sh_last[0], last1 = sh_last[1];
   if (!(last0 | last1)) return;
+  constexpr uint32_t kMaxIt = (16u * kCols / 4u + 63u) / 64u;  // float4 per thread, WK >= 1
   for (uint32_t i = 0; i < 2u; ++i) {
     if (!(i == 0 ? last0 : last1)) continue;
     const Piece p = piece(i);
@@ -351,15 +367,22 @@ __global__ void __launch_bounds__(64 * max_wk(T)) hq_decode_kernel(const GemmDes
     const uint32_t col0 = (p.g - sg.blk_begin) * kCols;
     const uint32_t bf = plan_wg_of_unit(pl.utot, pl.P, p.g * nkb);
     const uint32_t bl = plan_wg_of_unit(pl.utot, pl.P, (p.g + 1u) * nkb - 1u);
-    for (uint32_t o = threadIdx.x; o < SL; o += nthr) {
-      float s = 0.0f;
-      for (uint32_t c = bf; c <= bl; ++c) {
-        const uint32_t cslot = plan_begin(pl.utot, pl.P, c) / nkb == p.g ? 0u : 1u;
-        s += __hip_atomic_load(pl.part + ((size_t)c * 2u + cslot) * SL + o, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
+    f4 v[kMaxIt];
+#pragma unroll
+    for (uint32_t j = 0; j < kMaxIt; ++j) v[j] = f4{0.f, 0.f, 0.f, 0.f};
+    for (uint32_t c = bf; c <= bl; ++c) {  // contributors in workgroup order
+      const uint32_t cslot = plan_begin(pl.utot, pl.P, c) / nkb == p.g ? 0u : 1u;
+      const uint32_t base = (c * 2u + cslot) * SL * 4u;
+#pragma unroll
+      for (uint32_t j = 0; j < kMaxIt; ++j) {
+        const uint32_t o4 = threadIdx.x + j * nthr;
+        if (o4 < SL4) v[j] += __builtin_amdgcn_raw_buffer_load_b128(partr, base + 16u * o4, 0, kCoherent);
       }
-      const uint32_t row = o / kCols, n = col0 + o % kCols;
-      if (n < sg.N) reinterpret_cast<uint16_t*>(sg.Y)[(size_t)row * sg.ldy + n] = f32_to_out<DT>(s);
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < kMaxIt; ++j) {
+      const uint32_t o4 = threadIdx.x + j * nthr;
+      if (o4 < SL4) store4(sg, col0, o4, v[j]);
     }
   }
 }
