@@ -74,9 +74,9 @@ __global__ void __launch_bounds__(64 * max_wk(T)) hq_decode_kernel(const GemmDes
   const uint32_t M = d.M;
   const uint32_t SL = M * kCols;  // floats of one piece's partial tile
 
-  const uint32_t u0 = plan_begin(pl.utot, pl.P, b);
-  const uint32_t u1 = plan_begin(pl.utot, pl.P, b + 1);
-  const uint32_t gfirst = u0 / nkb, glast = (u1 - 1u) / nkb;
+  const uint32_t u0 = plan_begin(pl.L, pl.rem, b);
+  const uint32_t u1 = plan_begin(pl.L, pl.rem, b + 1);
+  const uint32_t gfirst = plan_div(u0, nkb, pl.nkb_m), glast = plan_div(u1 - 1u, nkb, pl.nkb_m);
   const uint32_t np = glast - gfirst + 1u;
   auto piece = [&](uint32_t i) {
     Piece p;
@@ -127,12 +127,19 @@ __global__ void __launch_bounds__(64 * max_wk(T)) hq_decode_kernel(const GemmDes
       if (g >= d.seg[i].blk_begin) s = i;
     return __builtin_amdgcn_readfirstlane(s);
   };
+  // Column tiles [ct0, ct0 + nv) of slab g: a segment's slabs split its tiles as evenly
+  // as integers allow (the first slab_r slabs hold slab_w + 1 tiles, the rest slab_w).
+  auto slab_tiles = [&](const SegDesc& sg, uint32_t g, uint32_t& ct0, uint32_t& nv) {
+    const uint32_t l = g - sg.blk_begin;
+    ct0 = l * sg.slab_w + min(l, sg.slab_r);
+    nv = sg.slab_w + (l < sg.slab_r ? 1u : 0u);
+  };
   auto open_piece = [&](uint32_t i) {  // set the load extents for piece i (< np)
     const Piece p = piece(i);
     const uint32_t s = seg_of(p.g);
-    const uint32_t ct0 = (p.g - d.seg[s].blk_begin) * T;
+    uint32_t ct0, nv;
+    slab_tiles(d.seg[s], p.g, ct0, nv);
     const uint32_t N = d.seg[s].N;
-    const uint32_t nv = min((uint32_t)T, d.seg[s].ntiles - ct0);
     lw_base = d.seg[s].Wp + (size_t)ct0 * nkb * 64u * WPL;
     lw_num = __builtin_amdgcn_readfirstlane(nv * nkb * kBlockBytes);
     ls_base = d.seg[s].S;
@@ -299,8 +306,11 @@ __global__ void __launch_bounds__(64 * max_wk(T)) hq_decode_kernel(const GemmDes
   // policy: agent-coherent (visible across XCDs once the store has completed).
   constexpr int kCoherent = 16;
   const __amdgpu_buffer_rsrc_t partr = make_rsrc(pl.part, pl.part ? pl.P * 2u * SL * 4u : 0u);
-  auto store4 = [&](const SegDesc& sg, uint32_t col0, uint32_t o4, f4 v) {
-    const uint32_t o = 4u * o4, row = o / kCols, n = col0 + o % kCols;
+  // Stores four consecutive outputs of a slab tile; only the slab's own columns
+  // (local column < ncols) that exist (< N) are written.
+  auto store4 = [&](const SegDesc& sg, uint32_t col0, uint32_t ncols, uint32_t o4, f4 v) {
+    const uint32_t o = 4u * o4, row = o / kCols, lc = o % kCols, n = col0 + lc;
+    if (lc >= ncols) return;  // ncols is a multiple of 16, so lc + 3 < ncols too
     uint16_t* y = reinterpret_cast<uint16_t*>(sg.Y) + (size_t)row * sg.ldy + n;
     if (n + 3u < sg.N && (reinterpret_cast<uintptr_t>(y) & 7u) == 0) {
       const u2 packed = {(uint32_t)f32_to_out<DT>(v[0]) | ((uint32_t)f32_to_out<DT>(v[1]) << 16),
@@ -316,7 +326,9 @@ __global__ void __launch_bounds__(64 * max_wk(T)) hq_decode_kernel(const GemmDes
   for (uint32_t i = 0; i < np; ++i) {
     const Piece p = piece(i);
     const SegDesc& sg = d.seg[seg_of(p.g)];
-    const uint32_t col0 = (p.g - sg.blk_begin) * kCols;
+    uint32_t ct0, nv;
+    slab_tiles(sg, p.g, ct0, nv);
+    const uint32_t col0 = ct0 * 16u, ncols = nv * 16u;
     const bool full = p.ka == 0u && p.kz == nkb;
     partial_any |= !full;
     uint32_t wmask = 0;  // wavefronts with units in this piece
@@ -326,7 +338,7 @@ __global__ void __launch_bounds__(64 * max_wk(T)) hq_decode_kernel(const GemmDes
       f4 v = f4{0.f, 0.f, 0.f, 0.f};
       for (uint32_t w = 0; w < WK; ++w)
         if ((wmask >> w) & 1u) v += *reinterpret_cast<const f4*>(red + (i * WK + w) * SL + 4u * o4);
-      if (full) store4(sg, col0, o4, v);
+      if (full) store4(sg, col0, ncols, o4, v);
       else __builtin_amdgcn_raw_buffer_store_b128(v, partr, (((b * 2u + i) * SL) + 4u * o4) * 4u, 0, kCoherent);
     }
   }
@@ -345,8 +357,8 @@ __global__ void __launch_bounds__(64 * max_wk(T)) hq_decode_kernel(const GemmDes
     if (i < np) {
       const Piece p = piece(i);
       if (!(p.ka == 0u && p.kz == nkb)) {
-        const uint32_t bf = plan_wg_of_unit(pl.utot, pl.P, p.g * nkb);
-        const uint32_t bl = plan_wg_of_unit(pl.utot, pl.P, (p.g + 1u) * nkb - 1u);
+        const uint32_t bf = plan_wg_of_unit(pl.L, pl.rem, p.g * nkb);
+        const uint32_t bl = plan_wg_of_unit(pl.L, pl.rem, (p.g + 1u) * nkb - 1u);
         const uint32_t old = __hip_atomic_fetch_add(pl.cnt + p.g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         if (old == bl - bf) {
           last = 1u;
@@ -364,14 +376,16 @@ __global__ void __launch_bounds__(64 * max_wk(T)) hq_decode_kernel(const GemmDes
     if (!(i == 0 ? last0 : last1)) continue;
     const Piece p = piece(i);
     const SegDesc& sg = d.seg[seg_of(p.g)];
-    const uint32_t col0 = (p.g - sg.blk_begin) * kCols;
-    const uint32_t bf = plan_wg_of_unit(pl.utot, pl.P, p.g * nkb);
-    const uint32_t bl = plan_wg_of_unit(pl.utot, pl.P, (p.g + 1u) * nkb - 1u);
+    uint32_t ct0, nv;
+    slab_tiles(sg, p.g, ct0, nv);
+    const uint32_t col0 = ct0 * 16u, ncols = nv * 16u;
+    const uint32_t bf = plan_wg_of_unit(pl.L, pl.rem, p.g * nkb);
+    const uint32_t bl = plan_wg_of_unit(pl.L, pl.rem, (p.g + 1u) * nkb - 1u);
     f4 v[kMaxIt];
 #pragma unroll
     for (uint32_t j = 0; j < kMaxIt; ++j) v[j] = f4{0.f, 0.f, 0.f, 0.f};
     for (uint32_t c = bf; c <= bl; ++c) {  // contributors in workgroup order
-      const uint32_t cslot = plan_begin(pl.utot, pl.P, c) / nkb == p.g ? 0u : 1u;
+      const uint32_t cslot = plan_div(plan_begin(pl.L, pl.rem, c), nkb, pl.nkb_m) == p.g ? 0u : 1u;
       const uint32_t base = (c * 2u + cslot) * SL * 4u;
 #pragma unroll
       for (uint32_t j = 0; j < kMaxIt; ++j) {
@@ -382,7 +396,7 @@ __global__ void __launch_bounds__(64 * max_wk(T)) hq_decode_kernel(const GemmDes
 #pragma unroll
     for (uint32_t j = 0; j < kMaxIt; ++j) {
       const uint32_t o4 = threadIdx.x + j * nthr;
-      if (o4 < SL4) store4(sg, col0, o4, v[j]);
+      if (o4 < SL4) store4(sg, col0, ncols, o4, v[j]);
     }
   }
 }
@@ -413,10 +427,29 @@ int cu_count() {
 constexpr uint32_t kMaxCounters = 16384;
 constexpr size_t kCounterBytes = kMaxCounters * 4u;
 
-uint32_t total_slabs(const GemmDesc& d, int T) {
+// Slabs per segment for slab width T and a target total Gt (0: the fewest, ceil(nt / T)):
+// each segment gets at least ceil(nt / T) slabs and about its share of Gt. Sets
+// blk_begin / blk_count and returns the total.
+uint32_t assign_slabs(GemmDesc& d, int T, uint32_t Gt) {
+  uint32_t tiles = 0;
+  for (uint32_t i = 0; i < d.nseg; ++i) tiles += d.seg[i].ntiles;
   uint32_t g = 0;
-  for (uint32_t i = 0; i < d.nseg; ++i) g += (d.seg[i].ntiles + T - 1) / T;
+  for (uint32_t i = 0; i < d.nseg; ++i) {
+    const uint32_t nt = d.seg[i].ntiles;
+    uint32_t ns = (nt + T - 1) / T;
+    if (Gt) ns = std::max<uint32_t>(ns, (uint32_t)(((uint64_t)Gt * nt + tiles - 1) / tiles));
+    ns = std::min(ns, nt);
+    d.seg[i].blk_begin = g;
+    d.seg[i].blk_count = ns;
+    d.seg[i].slab_w = nt / ns;
+    d.seg[i].slab_r = nt % ns;
+    g += ns;
+  }
   return g;
+}
+uint32_t total_slabs(const GemmDesc& d, int T, uint32_t Gt = 0) {
+  GemmDesc c = d;
+  return assign_slabs(c, T, Gt);
 }
 
 // Dynamic LDS budget of one workgroup (160 KiB per CU, less the kernel's static LDS).
@@ -429,16 +462,15 @@ size_t lds_bytes(const GemmDesc& d, const DecodeConfig& c, uint32_t np_max) {
 template <int FMT, int DT, int T, int U>
 hipError_t launch_t(GemmDesc d, const DecodeConfig& c, void* ws, hipStream_t stream) {
   DecodePlan pl{};
-  uint32_t blk = 0;
-  for (uint32_t i = 0; i < d.nseg; ++i) {
-    d.seg[i].blk_begin = blk;
-    d.seg[i].blk_count = (d.seg[i].ntiles + T - 1) / T;
-    blk += d.seg[i].blk_count;
-  }
+  const uint32_t blk = assign_slabs(d, T, c.G);
   pl.G = blk;
   pl.utot = blk * d.nkb;
   pl.P = (uint32_t)c.SK;
   pl.WK = (uint32_t)c.WK;
+  pl.L = pl.utot / pl.P;
+  pl.rem = pl.utot % pl.P;
+  pl.nkb_m = plan_div_magic(d.nkb);
+  pl.wk_m = plan_div_magic(pl.WK);
   pl.np_max = plan_np_max(pl.utot, pl.P, d.nkb);
   pl.gmul = plan_gmul(d.gkb);
   pl.contig = (uint32_t)c.contig;
@@ -468,18 +500,20 @@ hipError_t launch_fd(const GemmDesc& d, const DecodeConfig& c, void* ws, hipStre
 
 }  // namespace
 
-// Tiling choice (measured on MI355X over the 27B-class decode shapes, see the tuning
-// notes of the decode kernel): the memory pipeline prefers few wavefronts per CU, each
-// with many bytes in flight, and whole slabs per workgroup (a cut slab costs a
-// fix-up round trip at the end):
-//   1. the widest slab (8, 4 or 2 tiles) whose slab count fills >= 80% of the CUs, one
-//      slab per workgroup;
-//   2. otherwise, for large weights (>= 24 MiB), 4-tile slabs each cut into
+// Tiling choice (measured on MI355X over the 27B-class decode shapes). The memory
+// pipeline wants every CU streaming the same number of bytes with few wavefronts per CU,
+// and whole slabs per workgroup (a cut slab costs a fix-up round trip at the end):
+//   1. balanced slabs: when the tiles split over k * CUs workgroups (k the smallest
+//      count giving <= 8 tiles each) with the widest workgroup at most 20% above the
+//      mean, one slab of ~tiles / (k * CUs) tiles per workgroup (slab width 2, 4 or 8);
+//   2. otherwise the widest slab (8, 4 or 2 tiles) whose slab count fills >= 80% of
+//      the CUs, one slab per workgroup;
+//   3. otherwise, for large weights (>= 24 MiB), 4-tile slabs each cut into
 //      floor(CUs / slabs) k-ranges (stream-K fix-up);
-//   3. otherwise (small weights, latency-bound) the widest slab giving >= 150 slabs
-//      (else 2-tile, else 1-tile slabs), uncut.
-// Four wavefronts per workgroup (two for M > 8 on small weights). Narrow outputs with
-// fewer than 16 tiles use 1-tile slabs. HQ_DECODE_T / _WK / _P / _CONTIG override.
+//   4. otherwise (small weights, latency-bound) the widest slab giving >= 150 slabs
+//      (else 2-tile, else 1-tile slabs), uncut, with two wavefronts per workgroup for
+//      M > 8.
+// Four wavefronts per workgroup otherwise. HQ_DECODE_T / _WK / _P / _CONTIG / _G override.
 DecodeConfig choose_decode(int fmt, const GemmDesc& d) {
   uint32_t tiles = 0;
   for (uint32_t i = 0; i < d.nseg; ++i) tiles += d.seg[i].ntiles;
@@ -488,12 +522,25 @@ DecodeConfig choose_decode(int fmt, const GemmDesc& d) {
   const bool large = bytes >= 24.0 * 1024 * 1024;
   int T = 0, WK = 4;
   long P = 0;
-  for (int t : {8, 4, 2}) {
-    const uint32_t g = total_slabs(d, t);
-    if (g * 5 >= cus * 4) {
-      T = t;
-      P = g;
-      break;
+  uint32_t G = 0;
+  if (tiles >= cus) {
+    const uint32_t k = (tiles + 8u * cus - 1u) / (8u * cus);
+    const uint32_t g = k * cus;
+    const uint32_t wmax = (tiles + g - 1u) / g;
+    if ((double)wmax * g <= 1.2 * tiles && wmax >= 2) {
+      T = wmax <= 2 ? 2 : (wmax <= 4 ? 4 : 8);
+      G = g;
+      P = total_slabs(d, T, G);
+    }
+  }
+  if (T == 0) {
+    for (int t : {8, 4, 2}) {
+      const uint32_t g = total_slabs(d, t);
+      if (g * 5 >= cus * 4) {
+        T = t;
+        P = g;
+        break;
+      }
     }
   }
   if (T == 0 && large) {
@@ -516,7 +563,13 @@ DecodeConfig choose_decode(int fmt, const GemmDesc& d) {
   const int eT = env_int("HQ_DECODE_T", 0);
   if (eT == 1 || eT == 2 || eT == 4 || eT == 8) {
     T = eT;
+    G = 0;
     P = total_slabs(d, T);
+  }
+  const int eG = env_int("HQ_DECODE_G", 0);
+  if (eG >= 1) {
+    G = (uint32_t)eG;
+    P = total_slabs(d, T, G);
   }
   const int eWK = env_int("HQ_DECODE_WK", 0);
   if (eWK >= 1) WK = eWK;
@@ -525,11 +578,16 @@ DecodeConfig choose_decode(int fmt, const GemmDesc& d) {
   if (eP >= 1) P = eP;
   const char* ec = std::getenv("HQ_DECODE_CONTIG");
   if (ec && *ec) contig = std::atoi(ec) != 0;
-  const uint32_t utot = total_slabs(d, T) * d.nkb;
+  uint32_t slabs = total_slabs(d, T, G);
   // More slabs than counters: use a grid that never cuts a slab.
-  if (total_slabs(d, T) > kMaxCounters) P = total_slabs(d, T);
+  if (slabs > kMaxCounters) {
+    G = 0;
+    slabs = total_slabs(d, T);
+    P = slabs;
+  }
+  const uint32_t utot = slabs * d.nkb;
   P = std::max(1L, std::min<long>(P, utot));
-  DecodeConfig c{T, WK, (int)P, contig};
+  DecodeConfig c{T, WK, (int)P, contig, G};
   // Grow the grid (fewer slabs per workgroup) until the per-piece LDS slots fit; with one
   // unit per workgroup a piece needs M * 16 * T floats per wavefront, which always fits.
   while ((uint32_t)c.SK < utot && lds_bytes(d, c, plan_np_max(utot, (uint32_t)c.SK, d.nkb)) > kLdsLimit)
@@ -538,7 +596,7 @@ DecodeConfig choose_decode(int fmt, const GemmDesc& d) {
 }
 
 size_t decode_workspace_bytes(const GemmDesc& d, const DecodeConfig& c) {
-  const uint32_t G = total_slabs(d, c.T);
+  const uint32_t G = total_slabs(d, c.T, c.G);
   if (!plan_has_partial(G, (uint32_t)c.SK)) return 0;
   return kCounterBytes + (size_t)c.SK * 2u * d.M * 16u * c.T * sizeof(float);
 }

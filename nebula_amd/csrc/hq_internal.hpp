@@ -16,8 +16,10 @@ struct SegDesc {
   int64_t ldy;
   uint32_t N;
   uint32_t ntiles;     // ceil(N / 16)
-  uint32_t blk_begin;  // first grid x index of this segment
-  uint32_t blk_count;  // grid x extent of this segment
+  uint32_t blk_begin;  // first slab of this segment (decode) / first grid x index (prefill)
+  uint32_t blk_count;  // slabs of this segment (decode) / grid x extent (prefill)
+  uint32_t slab_w;     // decode: tiles per slab (the first slab_r slabs hold one more)
+  uint32_t slab_r;
 };
 
 struct GemmDesc {
@@ -38,6 +40,7 @@ struct DecodeConfig {
   int WK;
   int SK;      // workgroups (stream-K grid size)
   bool contig; // wavefronts take contiguous k runs of a piece (else interleaved)
+  uint32_t G = 0;  // target slab count (0: ceil(tiles / T)); slabs then hold <= T tiles
 };
 DecodeConfig choose_decode(int fmt, const GemmDesc& d);
 // Workspace bytes a decode launch with this config needs (0 when SK == 1). The first

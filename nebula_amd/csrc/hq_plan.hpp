@@ -3,9 +3,10 @@
 // The output columns of all segments are cut into "slabs" of T column tiles (16 columns
 // each); a unit of work is one slab times one 128-deep k-block, and units are numbered
 // slab-major: u = g * nkb + kb. The grid has P workgroups and workgroup b owns the
-// contiguous unit range [begin(b), begin(b + 1)), begin(b) = floor(b * utot / P), so
-// every workgroup streams the same number of weight bytes (+-1 unit) whatever N and K
-// are. A slab whose k range is cut by a range boundary ("partial piece") is finished by
+// contiguous unit range [begin(b), begin(b + 1)) with begin(b) = b * L + min(b, rem),
+// L = utot / P, rem = utot % P (the first rem workgroups take one unit more), so every
+// workgroup streams the same number of weight bytes (+-1 unit) whatever N and K are;
+// the kernel computes its range without a division. A slab whose k range is cut by a range boundary ("partial piece") is finished by
 // a fix-up: every contributing workgroup writes its fp32 partial tile to the workspace,
 // and the last one to arrive (per-slab counter) sums the partials in workgroup order and
 // stores the output, so the result does not depend on arrival order.
@@ -26,6 +27,10 @@ struct DecodePlan {
   uint32_t utot;  // G * nkb
   uint32_t P;     // workgroups
   uint32_t WK;    // wavefronts per workgroup
+  uint32_t L;     // utot / P
+  uint32_t rem;   // utot % P
+  uint32_t nkb_m; // plan_div_magic(nkb)
+  uint32_t wk_m;  // plan_div_magic(WK)
   uint32_t np_max;  // largest number of pieces of one workgroup
   uint32_t gmul;    // ceil(2^32 / gkb) for the k-block -> scale-group division (0 when gkb == 1)
   uint32_t contig;  // 1: wavefront w takes k-blocks [ka + w*len/WK, ka + (w+1)*len/WK) of a piece;
@@ -34,15 +39,16 @@ struct DecodePlan {
   uint32_t* cnt;    // [G] arrival counters, zero between launches
 };
 
-HQ_HD uint32_t plan_begin(uint32_t utot, uint32_t P, uint32_t b) { return (uint32_t)((uint64_t)b * utot / P); }
+HQ_HD uint32_t plan_begin(uint32_t L, uint32_t rem, uint32_t b) { return b * L + (b < rem ? b : rem); }
 
 // Workgroup whose range holds unit u: the largest b with begin(b) <= u.
-HQ_HD uint32_t plan_wg_of_unit(uint32_t utot, uint32_t P, uint32_t u) {
-  return (uint32_t)(((uint64_t)(u + 1) * P - 1) / utot);
+HQ_HD uint32_t plan_wg_of_unit(uint32_t L, uint32_t rem, uint32_t u) {
+  const uint32_t head = rem * (L + 1u);  // units of the workgroups with L + 1 units
+  return u < head ? u / (L + 1u) : rem + (u - head) / L;
 }
 
-// Largest piece count of any workgroup: a range of at most ceil(utot / P) units touches
-// at most floor((L - 1) / nkb) + 2 slabs.
+// Largest piece count of any workgroup: a range of at most L + (rem > 0) units touches
+// at most floor((Lmax - 1) / nkb) + 2 slabs.
 HQ_HD uint32_t plan_np_max(uint32_t utot, uint32_t P, uint32_t nkb) {
   if (utot % P == 0 && (utot / P) % nkb == 0) return utot / P / nkb;  // ranges aligned to slabs
   const uint32_t L = (utot + P - 1) / P;
@@ -54,6 +60,14 @@ HQ_HD uint32_t plan_np_max(uint32_t utot, uint32_t P, uint32_t nkb) {
 // Slab of piece i of a workgroup whose slabs run from gfirst to glast.
 HQ_HD uint32_t plan_piece_slab(uint32_t gfirst, uint32_t glast, uint32_t i) {
   return i == 0 ? gfirst : (i == 1 ? glast : gfirst + i - 1);
+}
+
+// Exact u / d for any 32-bit u without a divide instruction: m = floor((2^32 - 1) / d)
+// makes mulhi(u, m) at most one below the quotient, and one step corrects it.
+HQ_HD uint32_t plan_div_magic(uint32_t d) { return (uint32_t)(0xFFFFFFFFu / d); }
+HQ_HD uint32_t plan_div(uint32_t u, uint32_t d, uint32_t m) {
+  const uint32_t q = (uint32_t)(((uint64_t)u * m) >> 32);  // q * d <= u
+  return u - q * d >= d ? q + 1u : q;
 }
 
 // Whether some workgroup range boundary falls inside a slab.

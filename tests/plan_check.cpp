@@ -29,14 +29,16 @@ static int fail(const char* what, uint32_t G, uint32_t nkb, uint32_t P, uint32_t
 static int check(uint32_t G, uint32_t nkb, uint32_t P, uint32_t WK) {
   const uint32_t utot = G * nkb;
   if (P > utot) return 0;
+  const uint32_t L = utot / P, rem = utot % P;
   std::vector<int> seen(utot, 0);
   std::map<uint32_t, std::set<uint32_t>> writers;        // slab -> workgroups with a partial piece
   std::map<std::pair<uint32_t, uint32_t>, uint32_t> slot_of;  // (wg, slab) -> slot written
   const uint32_t npmax = plan_np_max(utot, P, nkb);
   for (uint32_t b = 0; b < P; ++b) {
-    const uint32_t u0 = plan_begin(utot, P, b), u1 = plan_begin(utot, P, b + 1);
+    const uint32_t u0 = plan_begin(L, rem, b), u1 = plan_begin(L, rem, b + 1);
     if (u1 <= u0) return fail("empty range", G, nkb, P, WK);
-    if (plan_wg_of_unit(utot, P, u0) != b || plan_wg_of_unit(utot, P, u1 - 1) != b)
+    if (u1 - u0 > L + 1 || u1 - u0 < L) return fail("unbalanced range", G, nkb, P, WK);
+    if (plan_wg_of_unit(L, rem, u0) != b || plan_wg_of_unit(L, rem, u1 - 1) != b)
       return fail("wg_of_unit", G, nkb, P, WK);
     const uint32_t gfirst = u0 / nkb, glast = (u1 - 1) / nkb, np = glast - gfirst + 1;
     if (np > npmax) return fail("np_max", G, nkb, P, WK);
@@ -70,16 +72,17 @@ static int check(uint32_t G, uint32_t nkb, uint32_t P, uint32_t WK) {
     }
     if (slabs.size() != np) return fail("slab count", G, nkb, P, WK);
   }
+  if (plan_begin(L, rem, P) != utot) return fail("ranges do not end at utot", G, nkb, P, WK);
   for (uint32_t u = 0; u < utot; ++u)
     if (seen[u] != 1) return fail("coverage", G, nkb, P, WK);
   for (auto& kv : writers) {
     const uint32_t g = kv.first;
-    const uint32_t bf = plan_wg_of_unit(utot, P, g * nkb), bl = plan_wg_of_unit(utot, P, (g + 1) * nkb - 1);
+    const uint32_t bf = plan_wg_of_unit(L, rem, g * nkb), bl = plan_wg_of_unit(L, rem, (g + 1) * nkb - 1);
     std::set<uint32_t> expect;
     for (uint32_t c = bf; c <= bl; ++c) expect.insert(c);
     if (expect != kv.second || bl == bf) return fail("contributors", G, nkb, P, WK);
     for (uint32_t c = bf; c <= bl; ++c) {
-      const uint32_t reader_slot = plan_begin(utot, P, c) / nkb == g ? 0u : 1u;
+      const uint32_t reader_slot = plan_begin(L, rem, c) / nkb == g ? 0u : 1u;
       if (slot_of[{c, g}] != reader_slot) return fail("slot", G, nkb, P, WK);
     }
   }
@@ -99,6 +102,27 @@ int main() {
           if (check(G, nkb, P, WK)) return 1;
           ++cases;
         }
+  {
+    const uint32_t ds[] = {1, 2, 3, 5, 7, 8, 16, 40, 216, 1000, 65535, 65536, 0x7FFFFFFFu, 0xFFFFFFFFu};
+    const uint32_t us[] = {0, 1, 2, 3, 39, 40, 41, 215, 216, 217, 65535, 65536, 0x7FFFFFFEu, 0x7FFFFFFFu, 0x80000000u,
+                           0xFFFFFFFEu, 0xFFFFFFFFu};
+    for (uint32_t d : ds) {
+      const uint32_t m = plan_div_magic(d);
+      for (uint32_t u : us)
+        for (int64_t du = -2; du <= 2; ++du) {
+          const uint32_t x = (uint32_t)((int64_t)u + du);
+          if (plan_div(x, d, m) != x / d) {
+            std::printf("FAIL div u=%u d=%u\n", x, d);
+            return 1;
+          }
+        }
+      for (uint32_t x = 0; x < 200000; ++x)
+        if (plan_div(x, d, m) != x / d) {
+          std::printf("FAIL div u=%u d=%u\n", x, d);
+          return 1;
+        }
+    }
+  }
   for (uint32_t gkb = 1; gkb <= 40; ++gkb) {
     const uint32_t gmul = plan_gmul(gkb);
     for (uint32_t kb = 0; kb < 100000; ++kb)

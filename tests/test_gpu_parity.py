@@ -323,3 +323,29 @@ def test_decode_caller_workspace_reused(cuda):
     check(y_ws, P16.reference(), O.F16, "caller workspace")
     torch.cuda.synchronize()
     assert int(ws[:4 * ((N + 15) // 16)].view(torch.int32).abs().sum().item()) == 0
+
+
+# Variable-width slabs: G slabs split each segment's tiles as evenly as integers allow
+# (63 tiles here), with whole slabs per workgroup (P = G) or cut slabs (P != G).
+@pytest.mark.parametrize("T,G,WK,Pg", [(8, 10, 4, 10), (8, 9, 3, 7), (8, 10, 4, 23), (4, 20, 2, 20), (4, 17, 4, 40),
+                                       (2, 40, 4, 40), (2, 35, 1, 12)])
+@pytest.mark.parametrize("M", [1, 16])
+def test_decode_variable_slabs(cuda, T, G, WK, Pg, M):
+    P = O.Problem(O.INT4, M, 2048, 1000, 128, O.F16, seed=2400 + M)
+    D = DeviceProblem(P)
+    with decode_env(T=T, G=G, WK=WK, P=Pg):
+        y = D.run()
+    check(y, P.reference(), O.F16, f"T={T} G={G} WK={WK} P={Pg} M={M}", P)
+
+
+@pytest.mark.parametrize("G,Pg", [(12, 12), (12, 29)])
+def test_decode_variable_slabs_fused(cuda, G, Pg):
+    Ns, K, M = [600, 130, 1000], 1024, 3
+    probs = [O.Problem(O.TERNARY2, M, K, n, 128, O.BF16, seed=2500 + i) for i, n in enumerate(Ns)]
+    for p in probs[1:]:
+        p.X = probs[0].X
+    devs = [DeviceProblem(p) for p in probs]
+    with decode_env(T=8, G=G, P=Pg):
+        outs = hq.gemm_fused(O.TERNARY2, devs[0].X, [(d.Wp, d.S, d.P.N) for d in devs])
+    for d, y in zip(devs, outs):
+        check(y, d.P.reference(), O.BF16, f"fused variable slabs G={G} P={Pg} N={d.P.N}", d.P)
