@@ -18,6 +18,8 @@ CSRC = PKG / "csrc"
 BUILD = PKG / "_build"
 LIBDIR = PKG / "lib"
 LIB = LIBDIR / "libnebula_hq.so"
+BINDIR = PKG / "bin"
+BENCH_TOOL = BINDIR / "hq_bench_qgemm"
 ORACLE_DIR = ROOT / "oracle"
 
 SOURCES = ["hq_api.cpp", "hq_decode.hip", "hq_prefill.hip", "hq_repack.hip"]
@@ -82,6 +84,16 @@ def build_library(verbose: bool = False) -> Path:
     return LIB
 
 
+def build_tools() -> Path:
+    """The BENCH-compatible benchmark executable (links the library through its C ABI)."""
+    BINDIR.mkdir(exist_ok=True)
+    tmp = BENCH_TOOL.with_suffix(".tmp")
+    _run([HIPCC, "-x", "hip", *COMMON_FLAGS, str(PKG / "tools" / "hq_bench_qgemm.cpp"), "-o", str(tmp),
+          f"-L{LIBDIR}", "-lnebula_hq", "-Wl,-rpath,$ORIGIN/../lib"])
+    os.replace(tmp, BENCH_TOOL)
+    return BENCH_TOOL
+
+
 def build_oracle() -> Path:
     _run(["make", "-C", str(ORACLE_DIR), "-s"])
     return ORACLE_DIR / "liboracle_hq.so"
@@ -89,6 +101,7 @@ def build_oracle() -> Path:
 
 def build(verbose: bool = False) -> None:
     build_library(verbose)
+    build_tools()
     build_oracle()
 
 

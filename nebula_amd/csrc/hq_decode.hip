@@ -503,11 +503,11 @@ hipError_t launch_fd(const GemmDesc& d, const DecodeConfig& c, void* ws, hipStre
 // Tiling choice (measured on MI355X over the 27B-class decode shapes). The memory
 // pipeline wants every CU streaming the same number of bytes with few wavefronts per CU,
 // and whole slabs per workgroup (a cut slab costs a fix-up round trip at the end):
-//   1. balanced slabs: when the tiles split over k * CUs workgroups (k the smallest
-//      count giving <= 8 tiles each) with the widest workgroup at most 20% above the
-//      mean, one slab of ~tiles / (k * CUs) tiles per workgroup (slab width 2, 4 or 8);
-//   2. otherwise the widest slab (8, 4 or 2 tiles) whose slab count fills >= 80% of
-//      the CUs, one slab per workgroup;
+//   1. the widest uniform slab (8, 4 or 2 tiles) whose slab count keeps the last round of
+//      workgroups >= 80% full (g / (CUs * ceil(g / CUs)) >= 0.8), one slab per workgroup;
+//   2. otherwise balanced variable-width slabs: the tiles split over k * CUs workgroups (k
+//      the smallest count giving <= 8 tiles each) when the widest holds at most 20% more
+//      than the mean, one slab per workgroup (slab width 2, 4 or 8);
 //   3. otherwise, for large weights (>= 24 MiB), 4-tile slabs each cut into
 //      floor(CUs / slabs) k-ranges (stream-K fix-up);
 //   4. otherwise (small weights, latency-bound) the widest slab giving >= 150 slabs
@@ -523,7 +523,16 @@ DecodeConfig choose_decode(int fmt, const GemmDesc& d) {
   int T = 0, WK = 4;
   long P = 0;
   uint32_t G = 0;
-  if (tiles >= cus) {
+  for (int t : {8, 4, 2}) {
+    const uint32_t g = total_slabs(d, t);
+    const uint32_t rounds = (g + cus - 1) / cus;
+    if (g * 5 >= rounds * cus * 4) {
+      T = t;
+      P = g;
+      break;
+    }
+  }
+  if (T == 0 && tiles >= cus) {
     const uint32_t k = (tiles + 8u * cus - 1u) / (8u * cus);
     const uint32_t g = k * cus;
     const uint32_t wmax = (tiles + g - 1u) / g;
@@ -531,16 +540,6 @@ DecodeConfig choose_decode(int fmt, const GemmDesc& d) {
       T = wmax <= 2 ? 2 : (wmax <= 4 ? 4 : 8);
       G = g;
       P = total_slabs(d, T, G);
-    }
-  }
-  if (T == 0) {
-    for (int t : {8, 4, 2}) {
-      const uint32_t g = total_slabs(d, t);
-      if (g * 5 >= cus * 4) {
-        T = t;
-        P = g;
-        break;
-      }
     }
   }
   if (T == 0 && large) {
