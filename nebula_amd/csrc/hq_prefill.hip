@@ -18,6 +18,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdlib>
 
 #include "hq_device.hpp"
 #include "hq_internal.hpp"
@@ -179,6 +180,9 @@ __global__ void __launch_bounds__(256 * WM) hq_prefill_kernel(const GemmDesc d, 
     __syncthreads();                                            // ... for every wave; stage (kb+1)&1 is free
     load_a((kb + 1) & 1u, kb + 1);
     load_b((slot + 2) % 3, kb + 2);
+    // Keep this step's loads ahead of its compute: vmcnt retires in issue order, so a load
+    // sunk below the first use of this step's weights would be waited for with them.
+    __builtin_amdgcn_sched_barrier(0);
     if (kb < nkb) {  // uniform; no loads inside
       const char* sbase = smem + (kb & 1u) * kStageBytes;
 #pragma unroll
@@ -192,15 +196,17 @@ __global__ void __launch_bounds__(256 * WM) hq_prefill_kernel(const GemmDesc d, 
 #pragma unroll
           for (int t = 0; t < kTilesPerWave; ++t) acc[r][t] = mfma16x16x32<DT>(a, b[t], acc[r][t]);
         }
-        // Keep each chunk's fragments from being hoisted into the previous chunk.
-        __builtin_amdgcn_sched_barrier(0);
       }
     }
   };
 
+  // Prologue in ring order (no reordering across the barriers): the loop header's wait
+  // counts assume slot 1 holds the youngest loads, as at the loop latch.
   load_a(0, 0);
   load_b(0, 0);
+  __builtin_amdgcn_sched_barrier(0);
   load_b(1, 1);
+  __builtin_amdgcn_sched_barrier(0);
   for (uint32_t kb = 0; kb < nkb; kb += 3) {
     step(kb, 0);
     step(kb + 1, 1);
@@ -248,8 +254,16 @@ hipError_t launch_rt(GemmDesc d, hipStream_t stream) {
   return hipGetLastError();
 }
 
+int env_int(const char* name, int dflt) {
+  const char* v = std::getenv(name);
+  return v && *v ? std::atoi(v) : dflt;
+}
+
 template <int FMT, int DT>
 hipError_t launch_fd(GemmDesc d, hipStream_t stream) {
+  const int eWM = env_int("HQ_PREFILL_WM", 0);  // tuning override: workgroup height 128 (1) or 256 (2) rows
+  if (eWM == 1) return launch_rt<FMT, DT, 8, 1>(d, stream);
+  if (eWM == 2) return launch_rt<FMT, DT, 8, 2>(d, stream);
   if (d.M <= 64) return launch_rt<FMT, DT, 4, 1>(d, stream);
   if (d.M <= 128) return launch_rt<FMT, DT, 8, 1>(d, stream);
   return launch_rt<FMT, DT, 8, 2>(d, stream);
