@@ -70,7 +70,7 @@ void parallel_for(size_t n, F f) {
   for (auto& t : th) t.join();
 }
 
-// Library-owned decode workspace, one per (device, stream), used when the caller passes
+// Library-owned workspace, one per (device, stream), used when the caller passes
 // none. It is zero-filled when allocated (the kernels leave its counters at zero), grows
 // when a larger shape needs it, and is never allocated while the stream is capturing.
 // Buffers that were outgrown stay allocated until the process ends: a launch still in
@@ -101,7 +101,7 @@ hq_status get_internal_ws(hipStream_t stream, size_t need, void** out) {
   if (e != hipSuccess) return fail(HQ_ERR_DEVICE, "hipStreamIsCapturing: %s", hipGetErrorString(e));
   if (cap != hipStreamCaptureStatusNone)
     return fail(HQ_ERR_WORKSPACE,
-                "this decode shape needs %zu workspace bytes; pass a workspace (hq_workspace_bytes) or run "
+                "this shape needs %zu workspace bytes; pass a workspace (hq_workspace_bytes) or run "
                 "the shape once before capturing the stream",
                 need);
   const size_t bytes = std::max(need, (size_t)1 << 20);
@@ -166,12 +166,21 @@ hq_status run_gemm(const void* X, hq_dtype dtype, int64_t ldx, hq_format fmt, co
     d.seg[i].Y = segs[i].Y;
     d.seg[i].ldy = segs[i].ldy;
     d.seg[i].N = segs[i].N;
+    d.seg[i].lds = segs[i].N;
     d.seg[i].ntiles = hq::col_tiles(segs[i].N);
   }
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (M > 16) return from_hip(hq::launch_prefill(fmt, dtype, d, s), "prefill launch");
-  const hq::DecodeConfig c = hq::choose_decode(fmt, d);
-  const size_t need = hq::decode_workspace_bytes(d, c);
+  const bool prefill = M > 16;
+  hq::DecodeConfig c{};
+  hq::PrefillConfig pc{};
+  size_t need = 0;
+  if (prefill) {
+    pc = hq::choose_prefill(fmt, d);
+    need = hq::prefill_workspace_bytes(d, pc);
+  } else {
+    c = hq::choose_decode(fmt, d);
+    need = hq::decode_workspace_bytes(d, c);
+  }
   void* w = nullptr;
   if (need > 0) {
     if (ws) {
@@ -184,6 +193,7 @@ hq_status run_gemm(const void* X, hq_dtype dtype, int64_t ldx, hq_format fmt, co
       return st;
     }
   }
+  if (prefill) return from_hip(hq::launch_prefill(fmt, dtype, pc, w, s), "prefill launch");
   return from_hip(hq::launch_decode(fmt, dtype, d, c, w, s), "decode launch");
 }
 
@@ -227,7 +237,10 @@ hq_status hq_workspace_bytes(hq_format fmt, uint32_t M, uint32_t K, uint32_t N, 
   if (M == 0 || N == 0 || K == 0 || K % hq::kBlockK || group == 0 || group % hq::kBlockK || K % group)
     return fail(HQ_ERR_SHAPE, "bad shape M=%u K=%u N=%u group=%u", M, K, N, group);
   *bytes = 0;
-  if (M > 16) return ok();
+  if (M > 16) {
+    *bytes = hq::prefill_workspace_bound(fmt, M, K / hq::kBlockK);
+    return ok();
+  }
   hq::GemmDesc d{};
   d.M = M;
   d.K = K;
@@ -235,6 +248,7 @@ hq_status hq_workspace_bytes(hq_format fmt, uint32_t M, uint32_t K, uint32_t N, 
   d.gkb = group / hq::kBlockK;
   d.nseg = 1;
   d.seg[0].N = N;
+  d.seg[0].lds = N;
   d.seg[0].ntiles = hq::col_tiles(N);
   *bytes = hq::decode_workspace_bytes(d, hq::choose_decode(fmt, d));
   return ok();

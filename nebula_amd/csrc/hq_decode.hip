@@ -139,12 +139,12 @@ __global__ void __launch_bounds__(64 * max_wk(T)) hq_decode_kernel(const GemmDes
     const uint32_t s = seg_of(p.g);
     uint32_t ct0, nv;
     slab_tiles(d.seg[s], p.g, ct0, nv);
-    const uint32_t N = d.seg[s].N;
+    const uint32_t N = d.seg[s].N, lds = d.seg[s].lds;
     lw_base = d.seg[s].Wp + (size_t)ct0 * nkb * 64u * WPL;
     lw_num = __builtin_amdgcn_readfirstlane(nv * nkb * kBlockBytes);
     ls_base = d.seg[s].S;
-    ls_num = __builtin_amdgcn_readfirstlane((nkb / d.gkb) * N * 2u);
-    lsrow = __builtin_amdgcn_readfirstlane(N * 2u);
+    ls_num = __builtin_amdgcn_readfirstlane(((nkb / d.gkb - 1u) * lds + N) * 2u);
+    lsrow = __builtin_amdgcn_readfirstlane(lds * 2u);
 #pragma unroll
     for (int j = 0; j < kSL; ++j) svo[j] = min(ct0 * 16u + 64u * j + lane % kCols, N - 1u) * 2u;
     lkb = span_begin(p, wave);
@@ -406,6 +406,8 @@ int env_int(const char* name, int dflt) {
   return v && *v ? std::atoi(v) : dflt;
 }
 
+}  // namespace
+
 int cu_count() {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) return 256;
@@ -421,11 +423,7 @@ int cu_count() {
   return cached[dev];
 }
 
-// Counter area at the start of every workspace, the same for all shapes so that one
-// workspace can serve calls of different shapes (the counters stay zero between calls;
-// the partial area after them does not).
-constexpr uint32_t kMaxCounters = 16384;
-constexpr size_t kCounterBytes = kMaxCounters * 4u;
+namespace {
 
 // Slabs per segment for slab width T and a target total Gt (0: the fewest, ceil(nt / T)):
 // each segment gets at least ceil(nt / T) slabs and about its share of Gt. Sets

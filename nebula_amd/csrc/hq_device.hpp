@@ -47,8 +47,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, ui
 // writes lds + 16 * i; lds must be wave-uniform. Kept out of kernel templates: clang's host
 // pass rejects this builtin and would otherwise silently drop the kernel's host stub.
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
-__device__ __forceinline__ void buffer_to_lds16(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voff) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds, 16, voff, 0, 0, 0);
+// The range check covers voff; keep soff (wave-uniform) in range.
+__device__ __forceinline__ void buffer_to_lds16(__amdgpu_buffer_rsrc_t r, void* lds, uint32_t voff, uint32_t soff = 0) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_ptr_t)lds, 16, voff, soff, 0, 0);
 }
 
 // s_waitcnt immediate (gfx9 encoding) waiting for vmcnt <= n only (n < 64).

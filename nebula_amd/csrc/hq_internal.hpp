@@ -15,6 +15,7 @@ struct SegDesc {
   void* Y;
   int64_t ldy;
   uint32_t N;
+  uint32_t lds;        // scale row stride in elements (N unless the segment is a column range)
   uint32_t ntiles;     // ceil(N / 16)
   uint32_t blk_begin;  // first slab of this segment (decode) / first grid x index (prefill)
   uint32_t blk_count;  // slabs of this segment (decode) / grid x extent (prefill)
@@ -50,8 +51,42 @@ size_t decode_workspace_bytes(const GemmDesc& d, const DecodeConfig& c);
 
 // Decode (M <= 16): HBM-streaming MFMA kernel. Validated descriptor in, status out.
 hipError_t launch_decode(int fmt, int dtype, GemmDesc d, const DecodeConfig& c, void* ws, hipStream_t stream);
+
+// One prefill launch: (16 * RT * WM)-row x 256-column tiles over the columns of d; psk
+// stream-K workgroups share the last tiles - dp tiles along K, dp workgroups own one tile
+// each.
+struct PrefillLaunch {
+  int RT;
+  int WM;
+  GemmDesc d;
+  uint32_t tiles;
+  uint32_t dp;
+  uint32_t psk;
+};
+// A prefill call: one launch, or two over disjoint column ranges (the second with
+// half-height tiles).
+struct PrefillConfig {
+  int n;
+  PrefillLaunch l[2];
+};
+PrefillConfig choose_prefill(int fmt, const GemmDesc& d);
+// Workspace bytes of a prefill call (0 without stream-K): the counter area, then two fp32
+// partial tiles per stream-K workgroup.
+size_t prefill_workspace_bytes(const GemmDesc& d, const PrefillConfig& c);
+// Upper bound of prefill_workspace_bytes over every N and segment split for this M and
+// K / 128 (what hq_workspace_bytes reports for M > 16).
+size_t prefill_workspace_bound(int fmt, uint32_t M, uint32_t nkb);
 // Prefill (M > 16): MFMA tile kernel.
-hipError_t launch_prefill(int fmt, int dtype, GemmDesc d, hipStream_t stream);
+hipError_t launch_prefill(int fmt, int dtype, const PrefillConfig& c, void* ws, hipStream_t stream);
+
+// Counter area at the start of every workspace, the same for all shapes and both kernels
+// so that one workspace can serve calls of different shapes (the counters stay zero
+// between calls; the partial area after them does not).
+constexpr uint32_t kMaxCounters = 16384;
+constexpr size_t kCounterBytes = kMaxCounters * 4u;
+
+// Compute units of the current device (256 if it cannot be queried).
+int cu_count();
 
 hipError_t launch_repack_int4(const uint32_t* src, uint32_t* dst, uint32_t K, uint32_t N,
                               hipStream_t stream);

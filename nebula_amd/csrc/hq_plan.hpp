@@ -62,6 +62,21 @@ HQ_HD uint32_t plan_piece_slab(uint32_t gfirst, uint32_t glast, uint32_t i) {
   return i == 0 ? gfirst : (i == 1 ? glast : gfirst + i - 1);
 }
 
+// Prefill grid: the first psk workgroups share the last (tiles - dp) output tiles along K
+// (stream-K over units (tile - dp) * nkb + kb, ranges as above); the dp workgroups after
+// them own one whole tile each. Splitting only the tiles that would leave the last round
+// of the grid part-empty keeps the fix-up traffic to that round.
+struct PrefillPlan {
+  uint32_t psk;     // stream-K workgroups (grid x indices [0, psk))
+  uint32_t dp;      // whole-tile workgroups after them (logical tiles [0, dp))
+  uint32_t xcd;     // 1: number the whole-tile workgroups XCD-major (dp % 8 == 0)
+  uint32_t L, rem;  // stream-K ranges: begin(s) = s * L + min(s, rem)
+  uint32_t nkb_m;   // plan_div_magic(nkb)
+  uint32_t nb;      // 256-column blocks over all segments (tile = row band * nb + block)
+  float* part;      // [psk][2][tile] fp32 partial tiles (null when psk == 0)
+  uint32_t* cnt;    // [tiles - dp] arrival counters, zero between launches
+};
+
 // Exact u / d for any 32-bit u without a divide instruction: m = floor((2^32 - 1) / d)
 // makes mulhi(u, m) at most one below the quotient, and one step corrects it.
 HQ_HD uint32_t plan_div_magic(uint32_t d) { return (uint32_t)(0xFFFFFFFFu / d); }

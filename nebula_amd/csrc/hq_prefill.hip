@@ -22,6 +22,7 @@
 
 #include "hq_device.hpp"
 #include "hq_internal.hpp"
+#include "hq_plan.hpp"
 
 namespace hq {
 namespace {
@@ -80,177 +81,365 @@ __device__ __forceinline__ u4 dq_scaled(const u4& w, int c, uint32_t s_f16, cons
   }
 }
 
-template <int FMT, int DT, int RT, int WM>
-__global__ void __launch_bounds__(256 * WM) hq_prefill_kernel(const GemmDesc d, uint32_t mtiles, uint32_t total_wg) {
+// Output tile `tile`, numbered row-band major over all segments' 256-column blocks
+// (tile = mt * nb + cb, cb counting segment 0's blocks, then segment 1's, ...; a
+// segment's first block is its blk_begin): its segment, first row and this wavefront's
+// first column tile. Consecutive tiles share their activation rows across segments.
+template <uint32_t BM>
+__device__ __forceinline__ void tile_geom(const GemmDesc& d, uint32_t nb, uint32_t tile, uint32_t wn, uint32_t& s,
+                                          uint32_t& m0, uint32_t& ct0) {
+  const uint32_t mt = tile / nb;
+  const uint32_t cb = tile - mt * nb;
+  s = 0;
+#pragma unroll
+  for (uint32_t i = 1; i < HQ_MAX_SEGMENTS; ++i)
+    if (i < d.nseg && cb >= d.seg[i].blk_begin) s = i;
+  m0 = mt * BM;
+  ct0 = (cb - d.seg[s].blk_begin) * 16u + wn * kTilesPerWave;
+}
+
+// SKP = false: workgroup b computes whole tile b (grid dp). SKP = true: workgroup b
+// computes stream-K range b (grid psk). Two kernels, so that the stream-K fix-up's
+// registers never weigh on the whole-tile pipeline.
+template <int FMT, int DT, int RT, int WM, bool SKP>
+__global__ void __launch_bounds__(256 * WM) hq_prefill_kernel(const GemmDesc d, const PrefillPlan pp) {
   constexpr uint32_t BM = 16u * RT * WM;
-  constexpr uint32_t kStageBytes = BM * 256u;  // BM rows x 128 fp16
+  constexpr uint32_t kStageBytes = BM * 256u;        // BM rows x 128 fp16
+  constexpr uint32_t kPartBytes = BM * 256u * 4u;    // one fp32 partial tile
+  constexpr uint32_t kWavePart = RT * kTilesPerWave * 1024u;  // one wavefront's share of it
+  // Partial tiles are stored and loaded with the sc1 cache policy: agent-coherent, so a
+  // store that has completed is visible to loads from any XCD.
+  constexpr int kCoherent = 16;
   extern __shared__ __attribute__((aligned(16))) char smem[];
+  uint32_t* const sh_last = reinterpret_cast<uint32_t*>(smem + 2u * kStageBytes);
 
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t c16 = lane & 15u, g4 = lane >> 4;
-
-  // XCD-aware renumbering: consecutive workgroup ids are spread round-robin over the 8
-  // XCDs; give each XCD a contiguous range of logical tiles (row-block major).
-  uint32_t lid = blockIdx.x;
-  if (total_wg % 8u == 0u) lid = (blockIdx.x % 8u) * (total_wg / 8u) + blockIdx.x / 8u;
-  uint32_t s = 0;
-#pragma unroll
-  for (uint32_t i = 1; i < HQ_MAX_SEGMENTS; ++i)
-    if (i < d.nseg && lid >= d.seg[i].blk_begin) s = i;
-  const SegDesc sg = d.seg[s];
-  const uint32_t nblk = (sg.ntiles + 15u) / 16u;
-  const uint32_t local = lid - sg.blk_begin;
-  const uint32_t mt = local / nblk, nt = local % nblk;
-  const uint32_t m0 = mt * BM;
   const uint32_t wm = wave / 4u, wn = wave % 4u;
-  const uint32_t ct0 = nt * 16u + wn * kTilesPerWave;
-  const uint32_t wrow0 = wm * 16u * RT;  // first workgroup row of this wavefront
+  const uint32_t wrow0 = wm * 16u * RT;  // first tile row of this wavefront
+  const uint32_t nkb = d.nkb;
 
-  // Activation rows [m0, m0 + BM) of X; rows >= M read as zero.
-  const uint32_t rows = min(BM, d.M - m0);
-  const __amdgpu_buffer_rsrc_t xr =
-      make_rsrc(reinterpret_cast<const char*>(d.X) + (size_t)m0 * (size_t)d.ldx * 2u, rows * (uint32_t)d.ldx * 2u);
-  // This lane's part of the wave's RT load instructions per k-block (BM / 4 in all): instruction
-  // i fills LDS rows 4q..4q+3, q = wave * RT + i; lane -> row 4q + g4, 16-byte slot c16
-  // holding unit c16 ^ (row & 15).
+  const uint32_t bid = blockIdx.x;
+
+  // The wave's RT activation load instructions per k-block (BM / 4 in all): instruction i
+  // fills LDS rows 4q..4q+3, q = wave * RT + i; lane -> row 4q + g4, 16-byte slot c16
+  // holding unit c16 ^ (row & 15). The k-block goes in the uniform offset; the row stays
+  // in the per-lane offset, which the descriptor's range check covers (rows >= M read 0).
   uint32_t aoff[RT];
 #pragma unroll
   for (int i = 0; i < RT; ++i) {
-    const uint32_t q = wave * RT + i;
-    const uint32_t r = 4u * q + g4;
+    const uint32_t r = 4u * (wave * RT + i) + g4;
     aoff[i] = (r * (uint32_t)d.ldx + 8u * (c16 ^ (r & 15u))) * 2u;
   }
-  auto load_a = [&](uint32_t stage, uint32_t kb) {
-#pragma unroll
-    for (int i = 0; i < RT; ++i) {
-      const uint32_t q = wave * RT + i;
-      buffer_to_lds16(xr, smem + stage * kStageBytes + q * 1024u, aoff[i] + kb * 256u);
-    }
-  };
-
-  // Weights: one descriptor per column tile of this wavefront.
-  __amdgpu_buffer_rsrc_t wrs[kTilesPerWave];
-  uint32_t soff[kTilesPerWave];
-  const uint32_t tile_bytes = d.nkb * 64u * (FMT == HQ_FORMAT_INT4 ? 16u : 8u);
-#pragma unroll
-  for (int t = 0; t < kTilesPerWave; ++t) {
-    const uint32_t ct = ct0 + t;
-    const bool ok = ct < sg.ntiles;
-    wrs[t] = make_rsrc(reinterpret_cast<const char*>(sg.Wp) + (size_t)(ok ? ct : 0u) * tile_bytes, ok ? tile_bytes : 0u);
-    soff[t] = min(ct * 16u + c16, sg.N - 1u) * 2u;
-  }
-  const __amdgpu_buffer_rsrc_t srs = make_rsrc(sg.S, (d.nkb / d.gkb) * sg.N * 2u);
-  // Weights and scales: a register ring of 3 k-blocks, two ahead of the one computed.
-  // Loads past the last k-block read zero (empty range) instead of branching.
-  u4 wr[3][kTilesPerWave];
-  uint32_t sr[3][kTilesPerWave];
-  auto load_b = [&](int slot, uint32_t kb) {
-    const bool ok = kb < d.nkb;
-    const uint32_t grp = min(kb, d.nkb - 1u) / d.gkb;
-#pragma unroll
-    for (int t = 0; t < kTilesPerWave; ++t) {
-      if constexpr (FMT == HQ_FORMAT_INT4) {
-        wr[slot][t] = __builtin_amdgcn_raw_buffer_load_b128(wrs[t], ok ? (kb * 64u + lane) * 16u : kOutOfRange, 0, 0);
-      } else {
-        const u2 v = __builtin_amdgcn_raw_buffer_load_b64(wrs[t], ok ? (kb * 64u + lane) * 8u : kOutOfRange, 0, 0);
-        wr[slot][t] = u4{v[0], v[1], 0u, 0u};
-      }
-      sr[slot][t] = __builtin_amdgcn_raw_buffer_load_b16(srs, grp * sg.N * 2u + soff[t], 0, 0);
-    }
-  };
-
-  const DqConst dqk = dq_const_f16();
-  f4 acc[RT][kTilesPerWave];
-#pragma unroll
-  for (int r = 0; r < RT; ++r)
-#pragma unroll
-    for (int t = 0; t < kTilesPerWave; ++t) acc[r][t] = f4{0.f, 0.f, 0.f, 0.f};
-
   // LDS fragment addresses: row 16 r + c16, unit (4 c + g4) ^ c16.
   uint32_t ldsoff[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c) ldsoff[c] = c16 * 256u + (((4u * c + g4) ^ c16) * 16u);
+  const DqConst dqk = dq_const_f16();
+  const uint32_t tile_bytes = nkb * 64u * (FMT == HQ_FORMAT_INT4 ? 16u : 8u);
+  const __amdgpu_buffer_rsrc_t partr = make_rsrc(pp.part, pp.part ? pp.psk * 2u * kPartBytes : 0u);
 
-  const uint32_t nkb = d.nkb;
-  // One k-block. Issue order per step: A(kb + 1) to LDS, then B(kb + 2) to registers, so
-  // at the top of the next step vmcnt(2 * kTilesPerWave) leaves only B(kb + 2) in flight.
-  auto step = [&](uint32_t kb, int slot) {
-    __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kTilesPerWave));  // A(kb), B(kb) landed for this wave
-    __syncthreads();                                            // ... for every wave; stage (kb+1)&1 is free
-    load_a((kb + 1) & 1u, kb + 1);
-    load_b((slot + 2) % 3, kb + 2);
-    // Keep this step's loads ahead of its compute: vmcnt retires in issue order, so a load
-    // sunk below the first use of this step's weights would be waited for with them.
-    __builtin_amdgcn_sched_barrier(0);
-    if (kb < nkb) {  // uniform; no loads inside
-      const char* sbase = smem + (kb & 1u) * kStageBytes;
+  f4 acc[RT][kTilesPerWave];
+
+  // Epilogue of a finished tile: tile (r, t), lane -> column 16 (ct0 + t) + c16, rows
+  // 16 r + 4 g4 + v. Rows past M fall outside the descriptor; columns past N get an
+  // out-of-range offset. Only row tiles r0 <= r < r1 (compile-time after unrolling).
+  auto store_tile = [&](uint32_t s, uint32_t m0, uint32_t ct0, int r0 = 0, int r1 = RT) {
+    constexpr float post = (FMT == HQ_FORMAT_TERNARY2 && DT == HQ_DTYPE_F16) ? 0.5f : 1.0f;
+    const SegDesc& sg = d.seg[s];
+    const uint32_t rows = min(BM, d.M - m0);
+    const __amdgpu_buffer_rsrc_t yr =
+        make_rsrc(reinterpret_cast<char*>(sg.Y) + (size_t)m0 * (size_t)sg.ldy * 2u, rows * (uint32_t)sg.ldy * 2u);
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        u4 b[kTilesPerWave];
+    for (int t = 0; t < kTilesPerWave; ++t) {
+      const uint32_t n = (ct0 + t) * 16u + c16;
+      const uint32_t cbase = n < sg.N ? n * 2u : kOutOfRange;
 #pragma unroll
-        for (int t = 0; t < kTilesPerWave; ++t) b[t] = dq_scaled<FMT, DT>(wr[slot][t], c, sr[slot][t], dqk);
+      for (int r = 0; r < RT; ++r)
 #pragma unroll
-        for (int r = 0; r < RT; ++r) {
-          const u4 a = *reinterpret_cast<const u4*>(sbase + (wrow0 + 16u * r) * 256u + ldsoff[c]);
-#pragma unroll
-          for (int t = 0; t < kTilesPerWave; ++t) acc[r][t] = mfma16x16x32<DT>(a, b[t], acc[r][t]);
+        for (int v = 0; v < 4; ++v) {
+          if (r < r0 || r >= r1) continue;
+          const uint32_t row = wrow0 + 16u * r + 4u * g4 + v;
+          __builtin_amdgcn_raw_buffer_store_b16(f32_to_out<DT>(acc[r][t][v] * post), yr,
+                                                cbase == kOutOfRange ? kOutOfRange : cbase + row * (uint32_t)sg.ldy * 2u,
+                                                0, 0);
         }
-      }
     }
   };
 
-  // Prologue in ring order (no reordering across the barriers): the loop header's wait
-  // counts assume slot 1 holds the youngest loads, as at the loop latch.
-  load_a(0, 0);
-  load_b(0, 0);
-  __builtin_amdgcn_sched_barrier(0);
-  load_b(1, 1);
-  __builtin_amdgcn_sched_barrier(0);
-  for (uint32_t kb = 0; kb < nkb; kb += 3) {
-    step(kb, 0);
-    step(kb + 1, 1);
-    step(kb + 2, 2);
-  }
-  __builtin_amdgcn_s_waitcnt(0);  // drain the out-of-range prefetches before the stores
-
-  // Epilogue: tile (r, t), lane -> column 16 (ct0 + t) + c16, rows 16 r + 4 g4 + v. Rows past M
-  // fall outside the descriptor; columns past N get an out-of-range offset.
-  constexpr float post = (FMT == HQ_FORMAT_TERNARY2 && DT == HQ_DTYPE_F16) ? 0.5f : 1.0f;
-  const __amdgpu_buffer_rsrc_t yr =
-      make_rsrc(reinterpret_cast<char*>(sg.Y) + (size_t)m0 * (size_t)sg.ldy * 2u, rows * (uint32_t)sg.ldy * 2u);
+  // k-blocks [ka, kz) of one tile into acc.
+  auto run_piece = [&](uint32_t s, uint32_t m0, uint32_t ct0, uint32_t ka, uint32_t kz) {
+    const SegDesc& sg = d.seg[s];
+    // Activation rows [m0, m0 + BM) of X; rows >= M read as zero.
+    const uint32_t rows = min(BM, d.M - m0);
+    const __amdgpu_buffer_rsrc_t xr =
+        make_rsrc(reinterpret_cast<const char*>(d.X) + (size_t)m0 * (size_t)d.ldx * 2u, rows * (uint32_t)d.ldx * 2u);
+    // Prefetches past the piece re-read its last k-block (in range, never computed on), so
+    // every step issues the same loads and the wait counts stay exact.
+    auto load_a = [&](uint32_t stage, uint32_t kb) {
+      const uint32_t ko = min(kb, kz - 1u) * 256u;
 #pragma unroll
-  for (int t = 0; t < kTilesPerWave; ++t) {
-    const uint32_t n = (ct0 + t) * 16u + c16;
-    const uint32_t cbase = n < sg.N ? n * 2u : kOutOfRange;
+      for (int i = 0; i < RT; ++i)
+        buffer_to_lds16(xr, smem + stage * kStageBytes + (wave * RT + i) * 1024u, aoff[i], ko);
+    };
+    // Weights: one descriptor per column tile of this wavefront.
+    __amdgpu_buffer_rsrc_t wrs[kTilesPerWave];
+#pragma unroll
+    for (int t = 0; t < kTilesPerWave; ++t) {
+      const uint32_t ct = ct0 + t;
+      const bool ok = ct < sg.ntiles;
+      wrs[t] = make_rsrc(reinterpret_cast<const char*>(sg.Wp) + (size_t)(ok ? ct : 0u) * tile_bytes, ok ? tile_bytes : 0u);
+    }
+    // Scale of column 16 ct + c16 (clamped to N - 1: columns past N are not stored).
+    const __amdgpu_buffer_rsrc_t srs = make_rsrc(sg.S, ((nkb / d.gkb - 1u) * sg.lds + sg.N) * 2u);
+    uint32_t soff[kTilesPerWave];
+#pragma unroll
+    for (int t = 0; t < kTilesPerWave; ++t) soff[t] = min((ct0 + t) * 16u + c16, sg.N - 1u) * 2u;
+    // Weights and scales: a register ring of 3 k-blocks, two ahead of the one computed.
+    // Column tiles past the segment have an empty descriptor and read zero.
+    u4 wr[3][kTilesPerWave];
+    uint32_t sr[3][kTilesPerWave];
+    auto load_b = [&](int slot, uint32_t kb) {
+      const uint32_t kc = min(kb, kz - 1u);
+      const uint32_t so = kc / d.gkb * sg.lds * 2u;
+#pragma unroll
+      for (int t = 0; t < kTilesPerWave; ++t) {
+        if constexpr (FMT == HQ_FORMAT_INT4) {
+          wr[slot][t] = __builtin_amdgcn_raw_buffer_load_b128(wrs[t], lane * 16u, kc * 1024u, 0);
+        } else {
+          const u2 v = __builtin_amdgcn_raw_buffer_load_b64(wrs[t], lane * 8u, kc * 512u, 0);
+          wr[slot][t] = u4{v[0], v[1], 0u, 0u};
+        }
+        sr[slot][t] = __builtin_amdgcn_raw_buffer_load_b16(srs, soff[t], so, 0);
+      }
+    };
+
 #pragma unroll
     for (int r = 0; r < RT; ++r)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const uint32_t row = wrow0 + 16u * r + 4u * g4 + v;
-        __builtin_amdgcn_raw_buffer_store_b16(f32_to_out<DT>(acc[r][t][v] * post), yr,
-                                              cbase == kOutOfRange ? kOutOfRange : cbase + row * (uint32_t)sg.ldy * 2u, 0, 0);
+      for (int t = 0; t < kTilesPerWave; ++t) acc[r][t] = f4{0.f, 0.f, 0.f, 0.f};
+
+    // One k-block. Issue order per step: A(kb + 1) to LDS, then B(kb + 2) to registers, so
+    // at the top of the next step vmcnt(2 * kTilesPerWave) leaves only B(kb + 2) in flight.
+    auto step = [&](uint32_t kb, int slot) {
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kTilesPerWave));  // A(kb), B(kb) landed for this wave
+      __syncthreads();                                            // ... for every wave; stage (kb+1)&1 is free
+      load_a((kb + 1) & 1u, kb + 1);
+      load_b((slot + 2) % 3, kb + 2);
+      // Keep this step's loads ahead of its compute: vmcnt retires in issue order, so a load
+      // sunk below the first use of this step's weights would be waited for with them.
+      __builtin_amdgcn_sched_barrier(0);
+      if (kb < kz) {  // uniform; no loads inside
+        const char* sbase = smem + (kb & 1u) * kStageBytes;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          u4 b[kTilesPerWave];
+#pragma unroll
+          for (int t = 0; t < kTilesPerWave; ++t) b[t] = dq_scaled<FMT, DT>(wr[slot][t], c, sr[slot][t], dqk);
+#pragma unroll
+          for (int r = 0; r < RT; ++r) {
+            const u4 a = *reinterpret_cast<const u4*>(sbase + (wrow0 + 16u * r) * 256u + ldsoff[c]);
+#pragma unroll
+            for (int t = 0; t < kTilesPerWave; ++t) acc[r][t] = mfma16x16x32<DT>(a, b[t], acc[r][t]);
+          }
+        }
       }
+    };
+
+    // Every wave is past the previous piece's last reads of both LDS stages.
+    __syncthreads();
+    // Prologue in ring order (no reordering across the barriers): the loop header's wait
+    // counts assume slot 1 holds the youngest loads, as at the loop latch.
+    load_a(ka & 1u, ka);
+    load_b(0, ka);
+    __builtin_amdgcn_sched_barrier(0);
+    load_b(1, ka + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    for (uint32_t kb = ka; kb < kz; kb += 3) {
+      step(kb, 0);
+      step(kb + 1, 1);
+      step(kb + 2, 2);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // drain the prefetches past the piece
+  };
+
+  if constexpr (!SKP) {
+    // Whole tiles, renumbered so that each XCD (consecutive workgroup ids go round-robin
+    // over the 8 XCDs) owns a contiguous range of tiles, row-block major, and keeps its
+    // activation rows resident in its own L2.
+    const uint32_t tile = pp.xcd ? (bid % 8u) * (pp.dp / 8u) + bid / 8u : bid;
+    uint32_t s, m0, ct0;
+    tile_geom<BM>(d, pp.nb, tile, wn, s, m0, ct0);
+    run_piece(s, m0, ct0, 0u, nkb);
+    store_tile(s, m0, ct0);
+    return;
+  }
+
+  // This workgroup's stream-K units (unit = tile * nkb + kb).
+  const uint32_t u0 = pp.dp * nkb + plan_begin(pp.L, pp.rem, bid);
+  const uint32_t u1 = pp.dp * nkb + plan_begin(pp.L, pp.rem, bid + 1u);
+
+  // Stream-K pieces: the tiles of [u0, u1), at most two since a range is shorter than a
+  // tile (L < nkb). Each goes to workspace slot 0 (first piece of the range) or 1 (last
+  // piece); the fix-up stores every tile, also one that a range holds whole (its only
+  // contributor is then the last). Keeping the output stores out of the piece loop keeps
+  // their addresses out of the k-loop's registers.
+  uint32_t ptile0 = ~0u, ptile1 = ~0u;
+  for (uint32_t u = u0; u < u1;) {  // uniform
+    const uint32_t tile = plan_div(u, nkb, pp.nkb_m);
+    const uint32_t ka = u - tile * nkb;
+    const uint32_t kz = min(nkb, u1 - tile * nkb);
+    const bool first = u == u0;
+    u = tile * nkb + kz;
+    uint32_t s, m0, ct0;
+    tile_geom<BM>(d, pp.nb, tile, wn, s, m0, ct0);
+    run_piece(s, m0, ct0, ka, kz);
+    const uint32_t slot = first ? 0u : 1u;
+    if (first) ptile0 = tile;
+    else ptile1 = tile;
+    const uint32_t base = (bid * 2u + slot) * kPartBytes + wave * kWavePart + lane * 16u;
+#pragma unroll
+    for (int r = 0; r < RT; ++r)
+#pragma unroll
+      for (int t = 0; t < kTilesPerWave; ++t)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u4, acc[r][t]), partr,
+                                               base + (uint32_t)(r * kTilesPerWave + t) * 1024u, 0, kCoherent);
+  }
+
+
+  // Fix-up: count arrivals per split tile; the last contributor sums every contributor's
+  // partial in workgroup order (so the result does not depend on arrival order) and
+  // stores the tile. Waiting for the coherent partial stores to complete before the
+  // barrier orders them before the arrival count.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x < 2u) {
+    const uint32_t tile = threadIdx.x == 0u ? ptile0 : ptile1;
+    uint32_t last = 0;
+    if (tile != ~0u) {
+      const uint32_t rel = tile - pp.dp;
+      const uint32_t bf = plan_wg_of_unit(pp.L, pp.rem, rel * nkb);
+      const uint32_t bl = plan_wg_of_unit(pp.L, pp.rem, (rel + 1u) * nkb - 1u);
+      const uint32_t old = __hip_atomic_fetch_add(pp.cnt + rel, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (old == bl - bf) {
+        last = 1u;
+        __hip_atomic_store(pp.cnt + rel, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    sh_last[threadIdx.x] = last;
+  }
+  __syncthreads();
+  const uint32_t last0 = sh_last[0], last1 = sh_last[1];
+  for (uint32_t i = 0; i < 2u; ++i) {
+    if (!(i == 0u ? last0 : last1)) continue;
+    const uint32_t tile = i == 0u ? ptile0 : ptile1;
+    const uint32_t rel = tile - pp.dp;
+    const uint32_t bf = plan_wg_of_unit(pp.L, pp.rem, rel * nkb);
+    const uint32_t bl = plan_wg_of_unit(pp.L, pp.rem, (rel + 1u) * nkb - 1u);
+    uint32_t s, m0, ct0;
+    tile_geom<BM>(d, pp.nb, tile, wn, s, m0, ct0);
+    // The sum runs over the contributors in workgroup order from zero (this workgroup's
+    // own partial is read back too: keeping it in registers across the fix-up would cost
+    // the k-loop registers). Four row tiles at a time: all 16 loads of a contributor in
+    // flight before the adds.
+    constexpr int kRG = 4;
+#pragma unroll
+    for (int rg = 0; rg < RT; rg += kRG) {
+#pragma unroll
+      for (int r = rg; r < rg + kRG; ++r)
+#pragma unroll
+        for (int t = 0; t < kTilesPerWave; ++t) acc[r][t] = f4{0.f, 0.f, 0.f, 0.f};
+      for (uint32_t c = bf; c <= bl; ++c) {  // contributors in workgroup order
+        const uint32_t cslot = plan_div(plan_begin(pp.L, pp.rem, c), nkb, pp.nkb_m) == rel ? 0u : 1u;
+        const uint32_t base = (c * 2u + cslot) * kPartBytes + wave * kWavePart + lane * 16u;
+        u4 part[kRG][kTilesPerWave];
+#pragma unroll
+        for (int r = 0; r < kRG; ++r)
+#pragma unroll
+          for (int t = 0; t < kTilesPerWave; ++t)
+            part[r][t] = __builtin_amdgcn_raw_buffer_load_b128(
+                partr, base + (uint32_t)((rg + r) * kTilesPerWave + t) * 1024u, 0, kCoherent);
+#pragma unroll
+        for (int r = 0; r < kRG; ++r)
+#pragma unroll
+          for (int t = 0; t < kTilesPerWave; ++t) acc[rg + r][t] += __builtin_bit_cast(f4, part[r][t]);
+      }
+      store_tile(s, m0, ct0, rg, rg + kRG);
+    }
   }
 }
 
 template <int FMT, int DT, int RT, int WM>
-hipError_t launch_rt(GemmDesc d, hipStream_t stream) {
-  constexpr uint32_t BM = 16u * RT * WM;
-  const uint32_t mtiles = (d.M + BM - 1) / BM;
-  uint32_t blk = 0;
+constexpr size_t prefill_lds() {
+  return 2u * (16u * RT * WM) * 256u + 16u;
+}
+
+// Whole-tile workgroups one CU holds at once (1 if the device cannot be queried).
+template <int FMT, int DT, int RT, int WM>
+int prefill_occupancy() {
+  static const int occ = [] {
+    const void* f = reinterpret_cast<const void*>(&hq_prefill_kernel<FMT, DT, RT, WM, false>);
+    int n = 0;
+    if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)prefill_lds<FMT, DT, RT, WM>()) !=
+            hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, f, 256 * WM, prefill_lds<FMT, DT, RT, WM>()) != hipSuccess ||
+        n < 1) {
+      (void)hipGetLastError();
+      n = 1;
+    }
+    return n;
+  }();
+  return occ;
+}
+
+// Column blocks: blk_begin = first 256-column block of each segment in the global block
+// order. Returns the number of blocks.
+uint32_t assign_blocks(GemmDesc& d) {
+  uint32_t nb = 0;
   for (uint32_t i = 0; i < d.nseg; ++i) {
-    d.seg[i].blk_begin = blk;
-    d.seg[i].blk_count = mtiles * ((d.seg[i].ntiles + 15u) / 16u);
-    blk += d.seg[i].blk_count;
+    d.seg[i].blk_begin = nb;
+    d.seg[i].blk_count = (d.seg[i].ntiles + 15u) / 16u;
+    nb += d.seg[i].blk_count;
   }
-  const size_t lds = 2u * BM * 256u;
+  return nb;
+}
+
+template <int FMT, int DT, int RT, int WM>
+hipError_t launch_rt(const PrefillLaunch& c, void* ws, hipStream_t stream) {
+  constexpr uint32_t BM = 16u * RT * WM;
+  GemmDesc d = c.d;
+  PrefillPlan pp{};
+  pp.nb = assign_blocks(d);
+  if ((d.M + BM - 1) / BM * pp.nb != c.tiles || c.dp + (c.psk ? 1u : 0u) > c.tiles) return hipErrorInvalidValue;
+  pp.psk = c.psk;
+  pp.dp = c.dp;
+  pp.xcd = c.dp % 8u == 0u ? 1u : 0u;
+  pp.nkb_m = plan_div_magic(d.nkb);
+  if (c.psk) {
+    if (!ws) return hipErrorInvalidValue;
+    const uint32_t units = (c.tiles - c.dp) * d.nkb;
+    pp.L = units / c.psk;
+    pp.rem = units % c.psk;
+    pp.cnt = static_cast<uint32_t*>(ws);
+    pp.part = reinterpret_cast<float*>(static_cast<char*>(ws) + kCounterBytes);
+  }
+  const size_t lds = prefill_lds<FMT, DT, RT, WM>();
   // More than the default 64 KiB of dynamic LDS needs an opt-in per kernel (idempotent).
   static const hipError_t attr =
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&hq_prefill_kernel<FMT, DT, RT, WM>),
-                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&hq_prefill_kernel<FMT, DT, RT, WM, false>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess
+          ? hipErrorInvalidConfiguration
+          : hipFuncSetAttribute(reinterpret_cast<const void*>(&hq_prefill_kernel<FMT, DT, RT, WM, true>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (attr != hipSuccess) return attr;
-  hipLaunchKernelGGL((hq_prefill_kernel<FMT, DT, RT, WM>), dim3(blk), dim3(256 * WM), lds, stream, d, mtiles, blk);
+  // Stream-K part first, then the whole tiles (stream order: one after the other).
+  if (c.psk) {
+    hipLaunchKernelGGL((hq_prefill_kernel<FMT, DT, RT, WM, true>), dim3(c.psk), dim3(256 * WM), lds, stream, d, pp);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  if (c.dp) hipLaunchKernelGGL((hq_prefill_kernel<FMT, DT, RT, WM, false>), dim3(c.dp), dim3(256 * WM), lds, stream, d, pp);
   return hipGetLastError();
 }
 
@@ -259,25 +448,160 @@ int env_int(const char* name, int dflt) {
   return v && *v ? std::atoi(v) : dflt;
 }
 
+// Tile height: 64 rows (RT 4, WM 1) up to M = 64, 128 rows (8, 1) up to 128, else 256 (8, 2).
+void prefill_shape(uint32_t M, int& RT, int& WM) {
+  const int eWM = env_int("HQ_PREFILL_WM", 0);  // tuning override: 128 (1) or 256 (2) rows
+  if (eWM == 1 || eWM == 2) {
+    RT = 8;
+    WM = eWM;
+  } else if (M <= 64) {
+    RT = 4;
+    WM = 1;
+  } else {
+    RT = 8;
+    WM = M <= 128 ? 1 : 2;
+  }
+}
+
+// Concurrent workgroups of the chosen shape on this device. The f16 instantiation stands
+// for both dtypes, so that the plan (and the workspace size) does not depend on the dtype.
+int prefill_slots(int fmt, int RT, int WM) {
+  int occ = 1;
+  if (fmt == HQ_FORMAT_INT4) {
+    occ = RT == 4 ? prefill_occupancy<HQ_FORMAT_INT4, HQ_DTYPE_F16, 4, 1>()
+                  : (WM == 1 ? prefill_occupancy<HQ_FORMAT_INT4, HQ_DTYPE_F16, 8, 1>()
+                             : prefill_occupancy<HQ_FORMAT_INT4, HQ_DTYPE_F16, 8, 2>());
+  } else {
+    occ = RT == 4 ? prefill_occupancy<HQ_FORMAT_TERNARY2, HQ_DTYPE_F16, 4, 1>()
+                  : (WM == 1 ? prefill_occupancy<HQ_FORMAT_TERNARY2, HQ_DTYPE_F16, 8, 1>()
+                             : prefill_occupancy<HQ_FORMAT_TERNARY2, HQ_DTYPE_F16, 8, 2>());
+  }
+  return cu_count() * occ;
+}
+
 template <int FMT, int DT>
-hipError_t launch_fd(GemmDesc d, hipStream_t stream) {
-  const int eWM = env_int("HQ_PREFILL_WM", 0);  // tuning override: workgroup height 128 (1) or 256 (2) rows
-  if (eWM == 1) return launch_rt<FMT, DT, 8, 1>(d, stream);
-  if (eWM == 2) return launch_rt<FMT, DT, 8, 2>(d, stream);
-  if (d.M <= 64) return launch_rt<FMT, DT, 4, 1>(d, stream);
-  if (d.M <= 128) return launch_rt<FMT, DT, 8, 1>(d, stream);
-  return launch_rt<FMT, DT, 8, 2>(d, stream);
+hipError_t launch_fd(const PrefillLaunch& c, void* ws, hipStream_t stream) {
+  if (c.RT == 4) return launch_rt<FMT, DT, 4, 1>(c, ws, stream);
+  if (c.WM == 1) return launch_rt<FMT, DT, 8, 1>(c, ws, stream);
+  return launch_rt<FMT, DT, 8, 2>(c, ws, stream);
+}
+
+// Global column blocks [cb0, cb1) of d as a descriptor of their own: segments outside
+// dropped, the others' weight, scale and output pointers advanced to their first column.
+GemmDesc column_range(int fmt, const GemmDesc& d, uint32_t cb0, uint32_t cb1) {
+  GemmDesc out = d;
+  out.nseg = 0;
+  const size_t tile_words = (size_t)d.nkb * 64u * words_per_lane(fmt);
+  uint32_t cb = 0;
+  for (uint32_t i = 0; i < d.nseg; ++i) {
+    const SegDesc& g = d.seg[i];
+    const uint32_t nb = (g.ntiles + 15u) / 16u;
+    const uint32_t lo = std::max(cb0, cb) - cb, hi = std::min(cb1, cb + nb);
+    if (cb + lo < hi) {
+      SegDesc t = g;
+      const uint32_t c0 = lo * 256u;
+      t.Wp = g.Wp + (size_t)lo * 16u * tile_words;
+      t.S = g.S + c0;
+      t.Y = static_cast<char*>(g.Y) + (size_t)c0 * 2u;
+      t.N = std::min<uint32_t>(g.N, (hi - cb) * 256u) - c0;
+      t.ntiles = col_tiles(t.N);
+      out.seg[out.nseg++] = t;
+    }
+    cb += nb;
+  }
+  return out;
+}
+
+uint32_t count_blocks(const GemmDesc& d) {
+  GemmDesc t = d;
+  return assign_blocks(t);
+}
+
+PrefillLaunch make_launch(int RT, int WM, const GemmDesc& d) {
+  PrefillLaunch l{};
+  l.RT = RT;
+  l.WM = WM;
+  l.d = d;
+  l.tiles = (d.M + 16u * RT * WM - 1) / (16u * RT * WM) * count_blocks(d);
+  l.dp = l.tiles;
+  l.psk = 0;
+  return l;
 }
 
 }  // namespace
 
-hipError_t launch_prefill(int fmt, int dtype, GemmDesc d, hipStream_t stream) {
-  if (fmt == HQ_FORMAT_INT4) {
-    return dtype == HQ_DTYPE_F16 ? launch_fd<HQ_FORMAT_INT4, HQ_DTYPE_F16>(d, stream)
-                                 : launch_fd<HQ_FORMAT_INT4, HQ_DTYPE_BF16>(d, stream);
+// Tiling of a prefill call (tile heights 256 / 128 / 64 rows as M allows):
+//  * A grid of at most half the workgroup slots is split s ways along K (stream-K,
+//    s = floor(slots / tiles), at most nkb / 4 so that a range keeps 4 k-blocks): s *
+//    tiles workgroups, each one aligned tile fraction, each tile s contributors.
+//  * Otherwise, when the last round of whole tiles would be part-empty, the last k column
+//    blocks (just enough to empty that round) run as a second launch of half-height
+//    tiles, if those fit in one round: the tail then takes half a round.
+//  * Otherwise whole tiles.
+PrefillConfig choose_prefill(int fmt, const GemmDesc& d) {
+  PrefillConfig c{};
+  int RT = 8, WM = 2;
+  prefill_shape(d.M, RT, WM);
+  c.n = 1;
+  c.l[0] = make_launch(RT, WM, d);
+  PrefillLaunch& l = c.l[0];
+  const uint32_t slots = (uint32_t)prefill_slots(fmt, RT, WM);
+  const int epsk = env_int("HQ_PREFILL_PSK", 0);  // tuning / test override: stream-K grid
+  if (env_int("HQ_PREFILL_SK", 1) != 0 && d.nkb >= 8u && l.tiles <= kMaxCounters &&
+      (uint64_t)l.tiles * d.nkb < (1ull << 31)) {
+    uint32_t psk = std::min<uint32_t>(slots / l.tiles, d.nkb / 4u) * l.tiles;
+    if (epsk > 0) psk = std::min<uint32_t>((uint32_t)epsk, l.tiles * d.nkb);
+    if (psk > l.tiles && (psk >= 2u * l.tiles || epsk > 0)) {
+      l.psk = psk;
+      l.dp = 0;
+      return c;
+    }
   }
-  return dtype == HQ_DTYPE_F16 ? launch_fd<HQ_FORMAT_TERNARY2, HQ_DTYPE_F16>(d, stream)
-                               : launch_fd<HQ_FORMAT_TERNARY2, HQ_DTYPE_BF16>(d, stream);
+  const uint32_t r = l.tiles % slots;
+  if (env_int("HQ_PREFILL_TAIL", 1) == 0 || r == 0u || RT == 4) return c;
+  const int hRT = WM == 2 ? 8 : 4;  // half-height tiles: 256 -> 128, 128 -> 64 rows
+  const uint32_t bands = (d.M + 16u * RT * WM - 1) / (16u * RT * WM);
+  const uint32_t nb = count_blocks(d);
+  const uint32_t k = (r + bands - 1) / bands;
+  if (k >= nb) return c;
+  const PrefillLaunch tail = make_launch(hRT, 1, column_range(fmt, d, nb - k, nb));
+  if (tail.tiles > (uint32_t)prefill_slots(fmt, hRT, 1)) return c;
+  c.n = 2;
+  c.l[0] = make_launch(RT, WM, column_range(fmt, d, 0, nb - k));
+  c.l[1] = tail;
+  return c;
+}
+
+size_t prefill_workspace_bytes(const GemmDesc& d, const PrefillConfig& c) {
+  (void)d;
+  size_t b = 0;
+  for (int i = 0; i < c.n; ++i)
+    if (c.l[i].psk)
+      b = std::max(b, kCounterBytes + (size_t)c.l[i].psk * 2u * (16u * c.l[i].RT * c.l[i].WM) * 256u * sizeof(float));
+  return b;
+}
+
+// Stream-K grids never exceed the workgroup slots (unless forced by HQ_PREFILL_PSK).
+size_t prefill_workspace_bound(int fmt, uint32_t M, uint32_t nkb) {
+  if (env_int("HQ_PREFILL_SK", 1) == 0 || nkb < 8u) return 0;
+  int RT = 8, WM = 2;
+  prefill_shape(M, RT, WM);
+  return kCounterBytes + (size_t)prefill_slots(fmt, RT, WM) * 2u * (16u * RT * WM) * 256u * sizeof(float);
+}
+
+hipError_t launch_prefill(int fmt, int dtype, const PrefillConfig& c, void* ws, hipStream_t stream) {
+  for (int i = 0; i < c.n; ++i) {
+    const PrefillLaunch& l = c.l[i];
+    hipError_t e;
+    if (fmt == HQ_FORMAT_INT4)
+      e = dtype == HQ_DTYPE_F16 ? launch_fd<HQ_FORMAT_INT4, HQ_DTYPE_F16>(l, ws, stream)
+                                : launch_fd<HQ_FORMAT_INT4, HQ_DTYPE_BF16>(l, ws, stream);
+    else
+      e = dtype == HQ_DTYPE_F16 ? launch_fd<HQ_FORMAT_TERNARY2, HQ_DTYPE_F16>(l, ws, stream)
+                                : launch_fd<HQ_FORMAT_TERNARY2, HQ_DTYPE_BF16>(l, ws, stream);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 }  // namespace hq

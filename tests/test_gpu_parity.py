@@ -349,3 +349,113 @@ def test_decode_variable_slabs_fused(cuda, G, Pg):
         outs = hq.gemm_fused(O.TERNARY2, devs[0].X, [(d.Wp, d.S, d.P.N) for d in devs])
     for d, y in zip(devs, outs):
         check(y, d.P.reference(), O.BF16, f"fused variable slabs G={G} P={Pg} N={d.P.N}", d.P)
+
+
+class prefill_env(decode_env):
+    """Force the prefill tiling for a block: WM (tile height 128 or 256 rows), SK=0 (no
+    stream-K), TAIL=0 (no half-height tail launch), PSK (stream-K workgroups)."""
+
+    def __init__(self, **kv):
+        self.kv = {f"HQ_PREFILL_{k}": str(v) for k, v in kv.items()}
+
+
+def normwise_between(a, b):
+    a, b = to_host_f32(a).astype(np.float64), to_host_f32(b).astype(np.float64)
+    return float(np.abs(a - b).max() / max(np.abs(b).max(), 1e-30))
+
+
+# Prefill grids smaller than half the workgroup slots split their tiles along K (stream-K,
+# by default s ways) and sum them in a last-arriver fix-up. That must agree with
+# whole-tile execution up to fp32 summation order (two output ulps of the largest value,
+# normwise) and be bit-reproducible.
+@pytest.mark.parametrize("fmt,xdt,M,K,N,psk", [
+    (O.TERNARY2, O.BF16, 512, 5120, 27648, 432),  # all 216 tiles split 2 ways (forced)
+    (O.INT4, O.F16, 256, 5120, 27648, 0),         # 108 tiles split 2 ways
+    (O.INT4, O.BF16, 40, 4096, 4096, 0),          # 64-row tiles, 16 tiles split 8 ways
+    (O.TERNARY2, O.F16, 200, 2048, 3000, 0),
+    (O.INT4, O.F16, 129, 1024, 700, 0),
+    (O.INT4, O.F16, 129, 1024, 700, 5),           # ranges straddling tiles
+])
+def test_prefill_stream_k_equals_whole_tiles(cuda, fmt, xdt, M, K, N, psk):
+    P = O.Problem(fmt, M, K, N, 128, xdt, seed=2600 + M)
+    D = DeviceProblem(P)
+    with prefill_env(PSK=psk):
+        y = D.run()
+        assert torch_equal(y, D.run())
+    with prefill_env(SK=0, TAIL=0):
+        y_whole = D.run()
+    tol = 2 * (2.0**-11 if xdt == O.F16 else 2.0**-8)
+    assert normwise_between(y, y_whole) <= tol
+    if M * K * N <= 4e9:
+        check(y, P.reference(), xdt, f"stream-K fmt={fmt} M={M} K={K} N={N}", P)
+    else:
+        rows = np.sort(np.random.default_rng(M).choice(M, size=16, replace=False))
+        err = O.normwise_error(to_host_f32(y)[rows], P.reference(rows=rows, threads=16))
+        assert err <= OUT_TOL[xdt]
+
+
+# A part-empty last round of whole tiles: the last column blocks run as a second launch of
+# half-height tiles. Each output element is the same fp32 chain in the same k order, so the
+# result equals whole-tile execution bit for bit. The fused case cuts a segment.
+@pytest.mark.parametrize("fmt,xdt,M,Ns", [
+    (O.INT4, O.F16, 2048, [27648]),         # 864 tiles: the last 12 of 108 blocks as 128-row tiles
+    (O.TERNARY2, O.BF16, 3072, [27648]),
+    (O.INT4, O.BF16, 2048, [26648, 1000]),  # 109 blocks: the tail spans both segments
+])
+def test_prefill_tail_equals_whole_tiles(cuda, fmt, xdt, M, Ns):
+    K = 1024
+    probs = [O.Problem(fmt, M, K, n, 128, xdt, seed=2650 + i) for i, n in enumerate(Ns)]
+    for p in probs[1:]:
+        p.X = probs[0].X
+    devs = [DeviceProblem(p) for p in probs]
+    segs = [(d.Wp, d.S, d.P.N) for d in devs]
+    outs = hq.gemm_fused(fmt, devs[0].X, segs)
+    with prefill_env(SK=0, TAIL=0):
+        whole = hq.gemm_fused(fmt, devs[0].X, segs)
+    rows = np.sort(np.random.default_rng(M).choice(M, size=8, replace=False))
+    for d, y, w in zip(devs, outs, whole):
+        assert torch_equal(y, w)
+        err = O.normwise_error(to_host_f32(y)[rows], d.P.reference(rows=rows, threads=16))
+        assert err <= OUT_TOL[xdt]
+
+
+# Forced stream-K grids on 15 tiles of 64 rows x 256 columns, K = 1024 (8 k-blocks):
+# 16 workgroups give ranges of 8 units aligned to tiles (whole-tile pieces inside the
+# stream-K part), 17 and 40 give ranges that straddle tiles, 119 gives 1-unit ranges.
+@pytest.mark.parametrize("psk", [16, 17, 40, 119])
+def test_prefill_stream_k_grids(cuda, psk):
+    P = O.Problem(O.INT4, 17, 1024, 3840, 128, O.F16, seed=2700 + psk)
+    D = DeviceProblem(P)
+    with prefill_env(PSK=psk):
+        y = D.run()
+    check(y, P.reference(), O.F16, f"psk={psk}", P)
+
+
+def test_prefill_stream_k_fused(cuda):
+    Ns, K, M = [1000, 300, 2600], 2048, 300
+    probs = [O.Problem(O.TERNARY2, M, K, n, 128, O.F16, seed=2800 + i) for i, n in enumerate(Ns)]
+    for p in probs[1:]:
+        p.X = probs[0].X
+    devs = [DeviceProblem(p) for p in probs]
+    for psk in (0, 37):
+        with prefill_env(PSK=psk):
+            outs = hq.gemm_fused(O.TERNARY2, devs[0].X, [(d.Wp, d.S, d.P.N) for d in devs])
+        for d, y in zip(devs, outs):
+            check(y, d.P.reference(), O.F16, f"fused stream-K psk={psk} N={d.P.N}", d.P)
+
+
+def test_prefill_caller_workspace_reused(cuda):
+    import torch
+
+    K, N = 5120, 27648
+    need = hq.workspace_bytes(O.INT4, 2048, K, N)
+    assert need > 0 and need == hq.workspace_bytes(O.INT4, 300, K, 16)
+    ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
+    P = O.Problem(O.INT4, 2048, K, N, 128, O.F16, seed=2900)
+    D = DeviceProblem(P)
+    y_int = D.run()
+    assert torch_equal(hq.gemm(O.INT4, D.X, D.Wp, D.S, N, workspace=ws), y_int)
+    X300 = D.X[:300].contiguous()
+    assert torch_equal(hq.gemm(O.INT4, X300, D.Wp, D.S, N, workspace=ws), D.run(X=X300))
+    torch.cuda.synchronize()
+    assert int(ws[:65536].view(torch.int32).abs().sum().item()) == 0  # counters left at zero
