@@ -76,7 +76,12 @@ def make_weights(hq, torch, K, N, copies, fmt=1):
 
 
 def graph_time_us(torch, stream, launches, reps: int = 3) -> float:
-    """Average duration of the launches captured in one HIP graph (events on the launch stream)."""
+    """Average duration of the launches captured in one HIP graph (events on the launch stream).
+    One eager pass on the stream first, so that a shape needing the library's workspace gets
+    it allocated outside the capture."""
+    with torch.cuda.stream(stream):
+        launches()
+    torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=stream):
         n = launches()

@@ -489,9 +489,17 @@ hipError_t launch_t(GemmDesc d, const DecodeConfig& c, void* ws, hipStream_t str
 template <int FMT, int DT>
 hipError_t launch_fd(const GemmDesc& d, const DecodeConfig& c, void* ws, hipStream_t stream) {
   switch (c.T) {
-    case 8: return launch_t<FMT, DT, 8, 3>(d, c, ws, stream);
-    case 4: return launch_t<FMT, DT, 4, 4>(d, c, ws, stream);
-    case 2: return launch_t<FMT, DT, 2, 4>(d, c, ws, stream);
+    // Ring depth U (k-blocks in flight per wavefront): measured best 2 for T = 8 and 3
+    // for T = 4 and 2 (deeper rings were slower); c.U overrides.
+    case 8: return c.U == 3 ? launch_t<FMT, DT, 8, 3>(d, c, ws, stream) : launch_t<FMT, DT, 8, 2>(d, c, ws, stream);
+    case 4:
+      return c.U == 2   ? launch_t<FMT, DT, 4, 2>(d, c, ws, stream)
+             : c.U == 4 ? launch_t<FMT, DT, 4, 4>(d, c, ws, stream)
+                        : launch_t<FMT, DT, 4, 3>(d, c, ws, stream);
+    case 2:
+      return c.U == 2   ? launch_t<FMT, DT, 2, 2>(d, c, ws, stream)
+             : c.U == 4 ? launch_t<FMT, DT, 2, 4>(d, c, ws, stream)
+                        : launch_t<FMT, DT, 2, 3>(d, c, ws, stream);
     default: return launch_t<FMT, DT, 1, 4>(d, c, ws, stream);
   }
 }
@@ -575,6 +583,7 @@ DecodeConfig choose_decode(int fmt, const GemmDesc& d) {
   if (eP >= 1) P = eP;
   const char* ec = std::getenv("HQ_DECODE_CONTIG");
   if (ec && *ec) contig = std::atoi(ec) != 0;
+  const int eU = env_int("HQ_DECODE_U", 0);  // tuning override: ring depth (T = 8: 2 or 3; T = 4: 3 or 4)
   uint32_t slabs = total_slabs(d, T, G);
   // More slabs than counters: use a grid that never cuts a slab.
   if (slabs > kMaxCounters) {
@@ -584,7 +593,7 @@ DecodeConfig choose_decode(int fmt, const GemmDesc& d) {
   }
   const uint32_t utot = slabs * d.nkb;
   P = std::max(1L, std::min<long>(P, utot));
-  DecodeConfig c{T, WK, (int)P, contig, G};
+  DecodeConfig c{T, WK, (int)P, contig, G, eU};
   // Grow the grid (fewer slabs per workgroup) until the per-piece LDS slots fit; with one
   // unit per workgroup a piece needs M * 16 * T floats per wavefront, which always fits.
   while ((uint32_t)c.SK < utot && lds_bytes(d, c, plan_np_max(utot, (uint32_t)c.SK, d.nkb)) > kLdsLimit)

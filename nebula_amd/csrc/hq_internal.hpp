@@ -42,6 +42,7 @@ struct DecodeConfig {
   int SK;      // workgroups (stream-K grid size)
   bool contig; // wavefronts take contiguous k runs of a piece (else interleaved)
   uint32_t G = 0;  // target slab count (0: ceil(tiles / T)); slabs then hold <= T tiles
+  int U = 0;       // register ring depth in k-blocks (0: the default for T)
 };
 DecodeConfig choose_decode(int fmt, const GemmDesc& d);
 // Workspace bytes a decode launch with this config needs (0 when SK == 1). The first

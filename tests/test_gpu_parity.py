@@ -240,7 +240,8 @@ def test_device_repack_matches_host(cuda, fmt):
 
 # ---------------------------------------------------------------- decode work decomposition
 class decode_env:
-    """Force the decode decomposition (slab width T, wavefronts WK, workgroups P) for a block."""
+    """Force the decode decomposition (slab width T, wavefronts WK, workgroups P, ring
+    depth U) for a block."""
 
     def __init__(self, **kv):
         self.kv = {f"HQ_DECODE_{k}": str(v) for k, v in kv.items()}
@@ -278,6 +279,21 @@ def test_decode_decompositions_int4(cuda, T, WK, Pg, M, contig):
     with decode_env(T=T, WK=WK, P=Pg, CONTIG=contig):
         y = D.run()
     check(y, P.reference(), O.F16, f"T={T} WK={WK} P={Pg} M={M} contig={contig}", P)
+
+
+# Register ring depths (k-blocks in flight per wavefront) other than each slab width's
+# default: the same per-wavefront k order, so the same bits as the default depth.
+@pytest.mark.parametrize("fmt,xdt", [(O.INT4, O.F16), (O.TERNARY2, O.BF16)])
+@pytest.mark.parametrize("T,U", [(8, 3), (4, 2), (4, 4), (2, 2), (2, 4)])
+def test_decode_ring_depths(cuda, fmt, xdt, T, U):
+    P = O.Problem(fmt, 5, 2048, 1000, 128, xdt, seed=2150 + T * 10 + U)
+    D = DeviceProblem(P)
+    with decode_env(T=T, WK=4, P=23):
+        y_default = D.run()
+        with decode_env(U=U):
+            y = D.run()
+    assert torch_equal(y, y_default)
+    check(y, P.reference(), xdt, f"fmt={fmt} T={T} U={U}", P)
 
 
 @pytest.mark.parametrize("fmt,xdt", [(O.INT4, O.BF16), (O.TERNARY2, O.F16), (O.TERNARY2, O.BF16)])
