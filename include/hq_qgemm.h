@@ -78,11 +78,13 @@ size_t hq_linear_words(hq_format fmt, uint32_t K, uint32_t N);
 /* Words of the gfx950 tile layout (N padded up to a multiple of 16). 0 on a bad shape. */
 size_t hq_packed_words(hq_format fmt, uint32_t K, uint32_t N);
 /* Device workspace a GEMM call of this shape needs on the current device (0: none).
- * Decode shapes (M <= 16) whose work is split across workgroups along K need one: a
- * 256-byte aligned buffer, zero-filled by the caller before its first use (every call
- * leaves it zero-filled again). Calls sharing one workspace must not overlap in time
- * (same stream, or ordered by events). For hq_gemm_fused pass N = sum of the segments'
- * N plus 16 per segment after the first. Passing NULL instead makes the library use a
+ * Calls whose work is split across workgroups along K need one (decode shapes with few
+ * column tiles, prefill calls with few output tiles): a 256-byte aligned buffer,
+ * zero-filled by the caller before its first use (every call leaves it zero-filled
+ * again). Calls sharing one workspace must not overlap in time (same stream, or ordered
+ * by events). For M > 16 the value is a bound that holds for every N and segment split;
+ * for a decode hq_gemm_fused pass N = sum of the segments' N plus 16 per segment after
+ * the first. Passing NULL instead makes the library use a
  * buffer of its own per (device, stream), allocated on first need outside stream
  * capture; a call that would need to allocate it during capture fails with
  * HQ_ERR_WORKSPACE. The reference has no workspace: it allocates inside
