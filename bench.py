@@ -215,7 +215,7 @@ def run_gpu(args):
     dom = cases[f"K{K}_N{N}_M{M}"]
     roofline = {"bound": "hbm", "achieved": dom["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(dom["GBps"] / HBM_PEAK_GBS, 4), "traffic": traffic_from_profile(),
-                "kernel": f"hq_decode_kernel<int4,f16>, K={K} N={N} M={M}",
+                "kernel": f"hq_decode_ls_kernel<int4,f16,KG=2,T=2,U=2>, K={K} N={N} M={M}",
                 "bytes_per_launch": wbytes(K, N), "avg_launch_us": dom["us"]}
 
     # ---- prefill and the split-fuse mixed batch ----

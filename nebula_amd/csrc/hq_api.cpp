@@ -5,6 +5,7 @@
 #include <algorithm>
 #include <cstdarg>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <mutex>
@@ -117,6 +118,17 @@ hq_status get_internal_ws(hipStream_t stream, size_t need, void** out) {
   return HQ_OK;
 }
 
+// Decode kernel family. With at most three activation rows the activation traffic is
+// negligible and the per-wavefront streaming kernel (hq_decode.hip) is as fast or faster;
+// from four rows on, the lockstep kernel (hq_decode_ls.hip), which fetches each activation
+// k-block once per workgroup, is (measured on MI355X over the 27B-class decode shapes).
+// HQ_DECODE_KERNEL=0 / 1 forces one of them (tuning and tests).
+bool use_lockstep(uint32_t M) {
+  const char* v = std::getenv("HQ_DECODE_KERNEL");
+  if (v && *v) return std::atoi(v) != 0;
+  return M >= 4;
+}
+
 // Validation shared by the GEMM entry points.
 hq_status check_gemm_common(const void* X, int dtype, int64_t ldx, uint32_t M, uint32_t K,
                             uint32_t group) {
@@ -171,12 +183,17 @@ hq_status run_gemm(const void* X, hq_dtype dtype, int64_t ldx, hq_format fmt, co
   }
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const bool prefill = M > 16;
+  const bool lockstep = !prefill && use_lockstep(M);
+  hq::LsConfig lc{};
   hq::DecodeConfig c{};
   hq::PrefillConfig pc{};
   size_t need = 0;
   if (prefill) {
     pc = hq::choose_prefill(fmt, d);
     need = hq::prefill_workspace_bytes(d, pc);
+  } else if (lockstep) {
+    lc = hq::choose_decode_ls(fmt, d);
+    need = hq::decode_ls_workspace_bytes(d, lc);
   } else {
     c = hq::choose_decode(fmt, d);
     need = hq::decode_workspace_bytes(d, c);
@@ -194,6 +211,7 @@ hq_status run_gemm(const void* X, hq_dtype dtype, int64_t ldx, hq_format fmt, co
     }
   }
   if (prefill) return from_hip(hq::launch_prefill(fmt, dtype, pc, w, s), "prefill launch");
+  if (lockstep) return from_hip(hq::launch_decode_ls(fmt, dtype, d, lc, w, s), "decode launch");
   return from_hip(hq::launch_decode(fmt, dtype, d, c, w, s), "decode launch");
 }
 
@@ -250,7 +268,8 @@ hq_status hq_workspace_bytes(hq_format fmt, uint32_t M, uint32_t K, uint32_t N, 
   d.seg[0].N = N;
   d.seg[0].lds = N;
   d.seg[0].ntiles = hq::col_tiles(N);
-  *bytes = hq::decode_workspace_bytes(d, hq::choose_decode(fmt, d));
+  *bytes = use_lockstep(M) ? hq::decode_ls_workspace_bytes(d, hq::choose_decode_ls(fmt, d))
+                          : hq::decode_workspace_bytes(d, hq::choose_decode(fmt, d));
   return ok();
 }
 

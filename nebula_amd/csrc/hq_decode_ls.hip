@@ -1,0 +1,515 @@
+// hq_decode_ls.hip — memory-bound qGEMM for M <= 16 (decode), gfx950: lockstep slabs.
+//
+// Replaces kernel_marlin_gemm_int4_templated / _dynamic
+// (hydrogen/src/model/marlin_gemm.cu:130-237, 242-322): the reference gives each thread
+// one output column and does 32 x M scalar FMAs per 16-byte weight load, then merges 16
+// fixed K-splits with fp32 atomics into a pre-zeroed Y.
+//
+// Here a workgroup owns a slab of 4 * T column tiles (16 columns each) and a contiguous
+// range of 128-deep k-blocks ("piece"); a slab's k-blocks are split over S workgroups
+// (S = 1 for wide weights). The workgroup has KG k-groups of four wavefronts; wavefront i
+// of every k-group streams tiles 4 i .. 4 i + T - 1 of the slab, and at step q k-group kg
+// takes k-block q * KG + kg of the piece, so the KG k-groups split K inside the CU and
+// meet once, at the end, in LDS. The four wavefronts of a k-group walk its k-blocks in
+// lockstep, each streaming its T tiles (1 KiB per tile and k-block, int4) from HBM into
+// a register ring U steps deep. The activation k-block (M rows x 256 B) is fetched once
+// per k-group (each wavefront loads four rows, full 128-byte lines) and shared through
+// LDS, so activation traffic is 1/(4 T) of a per-wavefront fetch; its 16-byte pieces are
+// XOR-swizzled by row so the MFMA A-fragment reads (ds_read_b128) are bank-conflict free.
+// Each step's loads are issued before the barrier that publishes the step's activations,
+// so the HBM stream never waits on the barrier.
+//
+// Hot-loop memory operations are inline asm: the compiler would otherwise re-order the
+// loads against the explicit wait counts and drain the ring at every barrier. Each use is
+// preceded by an explicit s_waitcnt tied to the registers it covers, so no instruction
+// reads a register whose load is in flight.
+//
+// Weights are dequantised in registers straight into v_mfma_f32_16x16x32 B fragments:
+// int4 in the biased form magic + q (one v_and_or_b32 per fragment word), with the bias
+// removed by a correction MFMA that seeds every tile's k-block sum; the fp16 group scale
+// multiplies the fp32 k-block sum. Pieces of a split slab are summed in piece order by
+// the last workgroup to finish (arrival counter), so results are deterministic.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdlib>
+
+#include "hq_device.hpp"
+#include "hq_internal.hpp"
+#include "hq_plan.hpp"
+
+namespace hq {
+namespace {
+
+// ---- inline-asm memory operations of the hot loop (see the header comment) ----
+__device__ __forceinline__ u4 ls_load_b128_nt(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  u4 v;
+  asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen nt" : "=v"(v) : "v"(voff), "s"(r), "s"(soff));
+  return v;
+}
+__device__ __forceinline__ u2 ls_load_b64_nt(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  u2 v;
+  asm volatile("buffer_load_dwordx2 %0, %1, %2, %3 offen nt" : "=v"(v) : "v"(voff), "s"(r), "s"(soff));
+  return v;
+}
+__device__ __forceinline__ uint32_t ls_load_u16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  uint32_t v;
+  asm volatile("buffer_load_ushort %0, %1, %2, %3 offen" : "=v"(v) : "v"(voff), "s"(r), "s"(soff));
+  return v;
+}
+__device__ __forceinline__ u4 ls_load_b128(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  u4 v;
+  asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen" : "=v"(v) : "v"(voff), "s"(r), "s"(soff));
+  return v;
+}
+__device__ __forceinline__ void ls_lds_write_b128(uint32_t addr, const u4& v) {
+  asm volatile("ds_write_b128 %0, %1" ::"v"(addr), "v"(v) : "memory");
+}
+__device__ __forceinline__ u4 ls_lds_read_b128(uint32_t addr) {
+  u4 v;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+  return v;
+}
+__device__ __forceinline__ void ls_lds_add_u32(uint32_t addr, uint32_t v) {
+  asm volatile("ds_add_u32 %0, %1" ::"v"(addr), "v"(v) : "memory");
+}
+__device__ __forceinline__ uint32_t ls_lds_read_u32_sync(uint32_t addr) {
+  uint32_t v;
+  asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr) : "memory");
+  return v;
+}
+__device__ __forceinline__ uint32_t ls_bpermute(uint32_t byte_lane, uint32_t v) {
+  uint32_t r;
+  asm volatile("ds_bpermute_b32 %0, %1, %2" : "=v"(r) : "v"(byte_lane), "v"(v));
+  return r;
+}
+
+template <int FMT>
+struct LsW;
+template <>
+struct LsW<HQ_FORMAT_INT4> {
+  using V = u4;
+  static constexpr uint32_t kLaneBytes = 16;
+};
+template <>
+struct LsW<HQ_FORMAT_TERNARY2> {
+  using V = u2;
+  static constexpr uint32_t kLaneBytes = 8;
+};
+
+constexpr uint32_t kStageBytes = 4096;  // one activation k-block: 16 rows x 256 B
+constexpr uint32_t kMaxPieces = 8;      // largest K split of a slab (pieces summed by the last one)
+
+// Waits, and ties registers to them: an empty asm that "rewrites" a register after the
+// wait keeps every instruction that reads it below the wait.
+template <int N>
+__device__ __forceinline__ void ls_wait_vmcnt() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"i"(N));
+}
+__device__ __forceinline__ void ls_wait_lgkmcnt0() { asm volatile("s_waitcnt lgkmcnt(0)"); }
+__device__ __forceinline__ void ls_tie(u4& a) { asm volatile("" : "+v"(a)); }
+__device__ __forceinline__ void ls_tie(u2& a) { asm volatile("" : "+v"(a)); }
+__device__ __forceinline__ void ls_tie(uint32_t& a) { asm volatile("" : "+v"(a)); }
+
+template <int FMT, int DT, int KG, int GW, int T, int U>
+__global__ void __launch_bounds__(64 * KG * GW) hq_decode_ls_kernel(const GemmDesc d, const LsPlan pl) {
+  static_assert(KG == 1 || KG == 2 || KG == 4, "one, two or four k-groups");
+  static_assert(GW == 2 || GW == 4, "k-groups of two or four wavefronts");
+  static_assert(T >= 1 && T <= 4, "the scale load covers at most four tiles");
+  using WV = typename LsW<FMT>::V;
+  constexpr uint32_t kLaneBytes = LsW<FMT>::kLaneBytes;
+  constexpr uint32_t kBlockBytes = 64u * kLaneBytes;  // one tile x one k-block
+  constexpr bool kInt4 = FMT == HQ_FORMAT_INT4;
+  // The register ring holds U steps in flight plus the one being consumed. Activations
+  // are staged through two LDS stages: a stage is written just before the barrier of its
+  // step and rewritten two steps later, after every wavefront has passed the next barrier
+  // (and so finished reading it). A stage holds one k-block per k-group.
+  constexpr int R = U + 1;
+  constexpr int NS = 2;
+  constexpr int XL = 4 / GW;        // activation loads (four rows each) per wavefront and step
+  constexpr int PER = XL + T + 1;  // loads per wavefront and step: activation rows, T tiles, scales
+  constexpr uint32_t kStep = KG * kStageBytes;
+  static_assert((KG - 1) * GW * T * 1024 <= NS * kStep, "the k-group reduction reuses the activation stages");
+  __shared__ __attribute__((aligned(16))) char xs[NS * kStep];
+  __shared__ uint32_t sh_last;
+  __shared__ uint32_t kg_arrived[KG];  // per k-group arrival count (k-group barrier)
+
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t wi = wave % GW, kg = wave / GW;  // wavefront within its k-group, k-group
+  const uint32_t c16 = lane & 15u, g4 = lane >> 4;
+  const uint32_t nkb = d.nkb;
+  const uint32_t M = d.M;
+  const uint32_t piece = blockIdx.x, g = blockIdx.y;  // grid (S, G)
+
+  // Segment and tiles of slab g.
+  uint32_t si = 0;
+  for (uint32_t i = 1; i < d.nseg; ++i)
+    if (g >= d.seg[i].blk_begin) si = i;
+  si = __builtin_amdgcn_readfirstlane(si);
+  // The segment's fields, read once (a reference into the kernel arguments would be
+  // re-read from memory inside the loop).
+  const uint32_t* const sWp = d.seg[si].Wp;
+  const uint16_t* const sS = d.seg[si].S;
+  void* const sY = d.seg[si].Y;
+  const uint32_t sN = d.seg[si].N, sLds = d.seg[si].lds, sNt = d.seg[si].ntiles;
+  const uint32_t sLdy = (uint32_t)d.seg[si].ldy;
+  const uint32_t ctw = (g - d.seg[si].blk_begin) * (GW * T) + wi * T;  // first tile of this wavefront
+  const uint32_t ntw = ctw < sNt ? min((uint32_t)T, sNt - ctw) : 0u;
+  const uint32_t srow2 = sLds * 2u;  // bytes per scale row
+  // k-blocks [ka, kz) of this piece; at step q k-group kg takes k-block ka + q * KG + kg.
+  const uint32_t ka = piece * pl.kq + min(piece, pl.kr);
+  const uint32_t kz = ka + pl.kq + (piece < pl.kr ? 1u : 0u);
+
+  // Weights: tile t of this wavefront at t * nkb blocks; missing tiles read zero.
+  const __amdgpu_buffer_rsrc_t wr =
+      make_rsrc(reinterpret_cast<const char*>(sWp) + (size_t)min(ctw, sNt) * nkb * kBlockBytes,
+                ntw * nkb * kBlockBytes);
+  uint32_t wvo[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) wvo[t] = lane * kLaneBytes + (uint32_t)t * nkb * kBlockBytes;
+  // Scales: lane l loads column 16 (ctw + l / 16) + l % 16 (clamped to N - 1).
+  const __amdgpu_buffer_rsrc_t srs = make_rsrc(sS, ((nkb / d.gkb - 1u) * sLds + sN) * 2u);
+  const uint32_t svo = min((ctw + min(g4, (uint32_t)T - 1u)) * 16u + c16, sN - 1u) * 2u;
+  // Activations: load x of this wavefront covers rows 4 (XL wi + x) + lane / 16 of its
+  // k-group's k-block; lane l holds the 16-byte piece (l % 16) ^ row of its row's 256
+  // bytes (rows >= M read zero) and writes it to LDS at row * 256 + 16 * (l % 16) of the
+  // k-group's stage slot.
+  const __amdgpu_buffer_rsrc_t xr = make_rsrc(d.X, M * (uint32_t)d.ldx * 2u);
+  const uint32_t xs0 = (uint32_t)(uintptr_t)xs + kg * kStageBytes;
+  uint32_t xvo[XL], xwo[XL];
+#pragma unroll
+  for (int x = 0; x < XL; ++x) {
+    const uint32_t xrow = 4u * (XL * wi + x) + g4;
+    xvo[x] = xrow < M ? xrow * (uint32_t)d.ldx * 2u + ((c16 ^ xrow) * 16u) : kOutOfRange;
+    xwo[x] = xs0 + (XL * wi + x) * 1024u + lane * 16u;
+  }
+  // A fragment of chunk c: row c16, 16-byte piece 4c + g4, at row * 256 + 16 * (piece ^ row).
+  uint32_t xro[4];
+#pragma unroll
+  for (int c = 0; c < 4; ++c) xro[c] = xs0 + c16 * 256u + 16u * ((4u * c + g4) ^ c16);
+
+  WV wring[R][T];
+  uint32_t sring[R];
+  u4 xring[R][XL];
+  // Loads of ring slot `slot` for step q (past the piece: zero reads).
+  auto issue = [&](int slot, uint32_t q) {
+    const uint32_t kb = ka + q * KG + kg;
+    const bool live = kb < kz;
+    const uint32_t kbu = __builtin_amdgcn_readfirstlane(live ? kb : 0u);
+#pragma unroll
+    for (int x = 0; x < XL; ++x) xring[slot][x] = ls_load_b128(xr, live ? xvo[x] : kOutOfRange, kbu * 256u);
+    const uint32_t kbo = kbu * kBlockBytes;
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      if constexpr (kInt4) wring[slot][t] = ls_load_b128_nt(wr, live ? wvo[t] : kOutOfRange, kbo);
+      else wring[slot][t] = ls_load_b64_nt(wr, live ? wvo[t] : kOutOfRange, kbo);
+    }
+    sring[slot] = ls_load_u16(srs, live ? svo : kOutOfRange,
+                              __builtin_amdgcn_readfirstlane(plan_group_of_kb(kbu, pl.gmul) * srow2));
+  };
+
+  f4 acc[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
+  const DqBiasConst dqb = DT == HQ_DTYPE_F16 ? dq_bias_const_f16() : dq_bias_const_bf16();
+  const u4 corr_b = int4_corr_fragment<DT>();
+
+  auto compute = [&](int slot, uint32_t stage) {
+    const uint32_t so = stage * kStep;
+    u4 xf[4];
+    uint32_t sb[T];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) xf[c] = ls_lds_read_b128(xro[c] + so);
+#pragma unroll
+    for (int t = 0; t < T; ++t) sb[t] = T == 1 ? sring[slot] : ls_bpermute((16u * t + c16) * 4u, sring[slot]);
+    ls_wait_lgkmcnt0();
+#pragma unroll
+    for (int c = 0; c < 4; ++c) ls_tie(xf[c]);
+#pragma unroll
+    for (int t = 0; t < T; ++t) ls_tie(sb[t]);
+    // Independent accumulation chains: one per tile and (int4) one for the bias
+    // correction -sum x (magic + 8), added after the chunk loop.
+    f4 corr = f4{0.f, 0.f, 0.f, 0.f}, gs[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) gs[t] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      if constexpr (kInt4) corr = mfma16x16x32<DT>(xf[c], corr_b, corr);
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        u4 bf;
+        if constexpr (kInt4) {
+          bf = dq_int4_biased<DT>(wring[slot][t][c], dqb);
+        } else {
+          const uint32_t word = wring[slot][t][c >> 1];
+          bf = (c & 1) ? dq_tern2<1>(word) : dq_tern2<0>(word);
+        }
+        gs[t] = mfma16x16x32<DT>(xf[c], bf, gs[t]);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      float sc = f16_to_f32((uint16_t)sb[t]);
+      if constexpr (!kInt4) sc = __builtin_isfinite(sc) ? 0.5f * sc : 0.0f;  // fields hold 2t; non-finite drops
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[t][v] = __builtin_fmaf(kInt4 ? gs[t][v] + corr[v] : gs[t][v], sc, acc[t][v]);
+    }
+  };
+
+  // Prologue: steps 0 .. U - 1 into slots 0 .. U - 1.
+#pragma unroll
+  for (int u = 0; u < U; ++u) issue(u, u);
+  const uint32_t nsteps = (kz - ka + KG - 1) / KG;
+  // The k-groups synchronise separately, so the wavefronts sharing a SIMD (one per
+  // k-group) drift apart and hide each other's waits. A k-group barrier is an LDS
+  // arrival count: each wavefront adds one after writing its activation rows (LDS
+  // executes a wavefront's operations in order) and waits until all four have arrived.
+  // The wait is bounded: every wavefront executes the same steps, so the bound is never
+  // reached by a correct launch, and a wrong one cannot hang the GPU.
+  const uint32_t arr = (uint32_t)(uintptr_t)&kg_arrived[kg];
+  const uint32_t arr_next = (uint32_t)(uintptr_t)&kg_arrived[(kg + 1u) % KG];
+  if constexpr (KG > 1) {
+    if (threadIdx.x < (uint32_t)KG) kg_arrived[threadIdx.x] = 0;
+    __syncthreads();
+  }
+  uint32_t arrivals = 0;
+  auto kgroup_barrier = [&]() {
+    if constexpr (KG == 1) {
+      ls_wait_lgkmcnt0();
+      __builtin_amdgcn_s_barrier();
+    } else {
+      arrivals += GW;
+      if (lane == 0) ls_lds_add_u32(arr, 1u);
+      for (uint32_t spin = 0; spin < (1u << 22); ++spin) {
+        if (__builtin_amdgcn_readfirstlane(ls_lds_read_u32_sync(arr)) >= arrivals) break;
+        __builtin_amdgcn_s_sleep(1);
+      }
+      // The SIMD arbiter favours older wavefronts, which would let k-group 0 run ahead
+      // and leave k-group 1 streaming alone at the end: a k-group behind the one after
+      // it (cyclically) raises its issue priority until it catches up.
+      const uint32_t other = __builtin_amdgcn_readfirstlane(ls_lds_read_u32_sync(arr_next));
+      if (other > arrivals) __builtin_amdgcn_s_setprio(2);
+      else __builtin_amdgcn_s_setprio(0);
+    }
+  };
+  uint32_t st = 0;  // LDS stage of step q
+  for (uint32_t i = 0; i < nsteps; i += R) {
+#pragma unroll
+    for (int s = 0; s < R; ++s) {
+      if (i + s < nsteps) {  // uniform; every step issues the same loads
+        ls_wait_vmcnt<(U - 1) * PER>();  // this wavefront's loads of step i + s have landed
+#pragma unroll
+        for (int t = 0; t < T; ++t) ls_tie(wring[s][t]);
+        ls_tie(sring[s]);
+#pragma unroll
+        for (int x = 0; x < XL; ++x) ls_tie(xring[s][x]);
+        issue((s + U) % R, i + s + U);
+#pragma unroll
+        for (int x = 0; x < XL; ++x) ls_lds_write_b128(xwo[x] + st * kStep, xring[s][x]);
+        kgroup_barrier();  // every wavefront's activation rows of step i + s are in LDS
+        compute(s, st);
+        st ^= 1u;
+      }
+    }
+  }
+  // The ring's trailing loads (past the piece) are still in flight and their results are
+  // never used: tie every ring register to the final wait, or the compiler would reuse
+  // those registers for the epilogue while the loads can still overwrite them.
+  ls_wait_vmcnt<0>();
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+#pragma unroll
+    for (int t = 0; t < T; ++t) ls_tie(wring[r][t]);
+    ls_tie(sring[r]);
+#pragma unroll
+    for (int x = 0; x < XL; ++x) ls_tie(xring[r][x]);
+  }
+
+  // k-groups 1.. hand their sums to k-group 0 through LDS, which adds them in k-group
+  // order. Every wavefront stays to the end so that all of them meet every barrier.
+  const bool lead = kg == 0;
+  if constexpr (KG > 1) {
+    __syncthreads();  // every wavefront is done reading the activation stages
+    float* red = reinterpret_cast<float*>(xs);
+    if (!lead) {
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+        *reinterpret_cast<f4*>(red + (((kg - 1u) * GW + wi) * T + t) * 256u + lane * 4u) = acc[t];
+    }
+    __syncthreads();
+    if (lead) {
+#pragma unroll
+      for (uint32_t k = 1; k < (uint32_t)KG; ++k)
+#pragma unroll
+        for (int t = 0; t < T; ++t) acc[t] += *reinterpret_cast<const f4*>(red + (((k - 1u) * GW + wi) * T + t) * 256u + lane * 4u);
+    }
+  }
+
+  // Output: lane holds rows 4 g4 + v of column 16 (ctw + t) + c16.
+  const __amdgpu_buffer_rsrc_t yr = make_rsrc(sY, M * sLdy * 2u);
+  auto store_out = [&](const f4* v) {
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      const uint32_t col = (ctw + t) * 16u + c16;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const uint32_t row = 4u * g4 + r;
+        const uint32_t o = row < M && col < sN ? (row * sLdy + col) * 2u : kOutOfRange;
+        __builtin_amdgcn_raw_buffer_store_b16(f32_to_out<DT>(v[t][r]), yr, o, 0, 0);
+      }
+    }
+  };
+  if (pl.S == 1) {
+    if (lead) store_out(acc);
+    return;
+  }
+
+  // Split slab: publish this piece (agent-coherent 16-byte stores, only lanes holding
+  // rows < M), count arrivals, and let the last piece to arrive sum all pieces in piece
+  // order. Waiting for the stores before the barrier orders them before the count.
+  constexpr int kCoherent = 16;
+  const uint32_t pieces = pl.S;
+  constexpr uint32_t kTilesWg = GW * T;
+  const __amdgpu_buffer_rsrc_t partr = make_rsrc(pl.part, gridDim.y * pieces * kTilesWg * 1024u);
+  auto part_off = [&](uint32_t p, int t) {
+    return 4u * g4 < M ? (((g * pieces + p) * kTilesWg + wi * T + t) * 64u + lane) * 16u : kOutOfRange;
+  };
+  if (lead) {
+#pragma unroll
+    for (int t = 0; t < T; ++t) __builtin_amdgcn_raw_buffer_store_b128(acc[t], partr, part_off(piece, t), 0, kCoherent);
+  }
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const uint32_t old = __hip_atomic_fetch_add(pl.cnt + g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint32_t last = old == pieces - 1u;
+    if (last) __hip_atomic_store(pl.cnt + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    sh_last = last;
+  }
+  __syncthreads();
+  if (!sh_last || !lead) return;
+  // Every piece's partial is loaded at once (a loop that waited for each piece before
+  // loading the next cost one memory round trip per piece), then summed in piece order.
+  f4 part[kMaxPieces][T];
+#pragma unroll
+  for (uint32_t p = 0; p < kMaxPieces; ++p)
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+      part[p][t] = p < pieces && p != piece ? __builtin_amdgcn_raw_buffer_load_b128(partr, part_off(p, t), 0, kCoherent)
+                                            : acc[t];
+  f4 sum[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) {
+    sum[t] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (uint32_t p = 0; p < kMaxPieces; ++p)
+      if (p < pieces) sum[t] += part[p][t];
+  }
+  store_out(sum);
+}
+
+int ls_env(const char* name, int dflt) {
+  const char* v = std::getenv(name);
+  return v && *v ? std::atoi(v) : dflt;
+}
+
+uint32_t ls_assign_slabs(GemmDesc& d, uint32_t sw) {
+  uint32_t g = 0;
+  for (uint32_t i = 0; i < d.nseg; ++i) {
+    const uint32_t ns = (d.seg[i].ntiles + sw - 1) / sw;
+    d.seg[i].blk_begin = g;
+    d.seg[i].blk_count = ns;
+    g += ns;
+  }
+  return g;
+}
+
+template <int FMT, int DT, int KG, int GW, int T, int U>
+hipError_t ls_launch_t(GemmDesc d, const LsConfig& c, void* ws, hipStream_t stream) {
+  LsPlan pl{};
+  const uint32_t G = ls_assign_slabs(d, GW * T);
+  pl.S = (uint32_t)c.S;
+  pl.kq = d.nkb / pl.S;
+  pl.kr = d.nkb % pl.S;
+  pl.gmul = plan_gmul(d.gkb);
+  if (pl.S > 1) {
+    if (!ws) return hipErrorInvalidValue;
+    pl.cnt = static_cast<uint32_t*>(ws);
+    pl.part = reinterpret_cast<float*>(static_cast<char*>(ws) + kCounterBytes);
+  }
+  // Byte offsets into X, Y and the partials are 32-bit buffer offsets.
+  const uint64_t xbytes = (uint64_t)d.M * (uint64_t)d.ldx * 2u;
+  bool fits = G >= 1 && G <= 65535 && xbytes < (1ull << 31) && (uint64_t)G * pl.S * GW * T * 1024u < (1ull << 31);
+  for (uint32_t i = 0; i < d.nseg; ++i) fits = fits && (uint64_t)d.M * (uint64_t)d.seg[i].ldy * 2u < (1ull << 31);
+  if (!fits) return hipErrorInvalidValue;
+  hipLaunchKernelGGL((hq_decode_ls_kernel<FMT, DT, KG, GW, T, U>), dim3(pl.S, G), dim3(64 * KG * GW), 0, stream, d, pl);
+  return hipGetLastError();
+}
+
+template <int FMT, int DT>
+hipError_t ls_launch_fd(const GemmDesc& d, const LsConfig& c, void* ws, hipStream_t stream) {
+  switch (c.GW * 1000 + c.KG * 100 + c.T * 10 + c.U) {
+    case 4124: return ls_launch_t<FMT, DT, 1, 4, 2, 4>(d, c, ws, stream);
+    case 4214: return ls_launch_t<FMT, DT, 2, 4, 1, 4>(d, c, ws, stream);
+    case 4222: return ls_launch_t<FMT, DT, 2, 4, 2, 2>(d, c, ws, stream);
+    case 4223: return ls_launch_t<FMT, DT, 2, 4, 2, 3>(d, c, ws, stream);
+    case 4242: return ls_launch_t<FMT, DT, 2, 4, 4, 2>(d, c, ws, stream);
+    case 4413: return ls_launch_t<FMT, DT, 4, 4, 1, 3>(d, c, ws, stream);
+    case 4422: return ls_launch_t<FMT, DT, 4, 4, 2, 2>(d, c, ws, stream);
+    case 4423: return ls_launch_t<FMT, DT, 4, 4, 2, 3>(d, c, ws, stream);
+    default: return hipErrorInvalidConfiguration;
+  }
+}
+
+}  // namespace
+
+// Lockstep tiling: KG k-groups of four wavefronts, T tiles per wavefront (slabs of 4 T
+// tiles), ring depth U, and S pieces per slab chosen so that the grid covers the CUs.
+// HQ_DECODE_LS_KG / _T / _U / _S override (tuning and tests).
+LsConfig choose_decode_ls(int fmt, const GemmDesc& d) {
+  (void)fmt;
+  const uint32_t cus = (uint32_t)cu_count();
+  // Measured on MI355X (27B-class shapes, M = 4..16): two k-groups of four wavefronts,
+  // two tiles per wavefront, two steps in flight; a K split only when the slabs alone
+  // leave more than a quarter of the CUs idle.
+  LsConfig c{2, 2, 1, 2, 4};
+  const int eKG = ls_env("HQ_DECODE_LS_KG", 0);
+  if (eKG == 1 || eKG == 2 || eKG == 4) c.KG = eKG;
+  const int eT = ls_env("HQ_DECODE_LS_T", 0);
+  if (eT == 1 || eT == 2 || eT == 4) c.T = eT;
+  const int eU = ls_env("HQ_DECODE_LS_U", 0);
+  if (eU >= 2 && eU <= 4) c.U = eU;
+  // Snap to an instantiated (KG, T, U).
+  if (c.KG == 1) { c.T = 2; c.U = 4; }
+  if (c.KG == 2 && c.T == 1) c.U = 4;
+  if (c.KG == 2 && c.T == 2) c.U = std::min(c.U, 3);
+  if (c.KG == 2 && c.T == 4) c.U = 2;
+  if (c.KG == 4) { c.T = std::min(c.T, 2); c.U = c.T == 1 ? 3 : std::min(c.U, 3); }
+  GemmDesc x = d;
+  const uint32_t G = ls_assign_slabs(x, c.GW * c.T);
+  if (G < cus * 3 / 4) c.S = (int)std::max<uint32_t>(1, std::min<uint32_t>(d.nkb, (cus * 15 / 16 + G - 1) / G));
+  const int eS = ls_env("HQ_DECODE_LS_S", 0);
+  if (eS >= 1) c.S = eS;
+  c.S = std::max(1, std::min<int>({c.S, (int)d.nkb, (int)kMaxPieces}));
+  if (c.S > 1 && G > kMaxCounters) c.S = 1;
+  return c;
+}
+
+size_t decode_ls_workspace_bytes(const GemmDesc& d, const LsConfig& c) {
+  if (c.S <= 1) return 0;
+  GemmDesc x = d;
+  const uint32_t G = ls_assign_slabs(x, c.GW * c.T);
+  return kCounterBytes + (size_t)G * c.S * c.GW * c.T * 1024u;
+}
+
+hipError_t launch_decode_ls(int fmt, int dtype, GemmDesc d, const LsConfig& c, void* ws, hipStream_t stream) {
+  if (fmt == HQ_FORMAT_INT4) {
+    return dtype == HQ_DTYPE_F16 ? ls_launch_fd<HQ_FORMAT_INT4, HQ_DTYPE_F16>(d, c, ws, stream)
+                                 : ls_launch_fd<HQ_FORMAT_INT4, HQ_DTYPE_BF16>(d, c, ws, stream);
+  }
+  return dtype == HQ_DTYPE_F16 ? ls_launch_fd<HQ_FORMAT_TERNARY2, HQ_DTYPE_F16>(d, c, ws, stream)
+                               : ls_launch_fd<HQ_FORMAT_TERNARY2, HQ_DTYPE_BF16>(d, c, ws, stream);
+}
+
+}  // namespace hq

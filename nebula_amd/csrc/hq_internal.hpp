@@ -53,6 +53,27 @@ size_t decode_workspace_bytes(const GemmDesc& d, const DecodeConfig& c);
 // Decode (M <= 16): HBM-streaming MFMA kernel. Validated descriptor in, status out.
 hipError_t launch_decode(int fmt, int dtype, GemmDesc d, const DecodeConfig& c, void* ws, hipStream_t stream);
 
+// Lockstep decode (M <= 16): KG k-groups of four wavefronts per workgroup own a slab of
+// 4 * T column tiles and walk one piece of its k-blocks together (S pieces per slab), each
+// k-group sharing its activation k-block through LDS.
+struct LsConfig {
+  int T;  // tiles per wavefront (1, 2 or 4)
+  int U;   // steps in flight per wavefront (register ring depth)
+  int S;   // pieces (workgroups) per slab along K
+  int KG;  // k-groups per workgroup (1, 2 or 4)
+  int GW;  // wavefronts per k-group (2 or 4); a slab is GW * T tiles
+};
+struct LsPlan {
+  uint32_t S;       // pieces per slab
+  uint32_t kq, kr;  // piece p covers k-blocks [p * kq + min(p, kr), ...) of kq (+1 if p < kr)
+  uint32_t gmul;    // plan_gmul(gkb)
+  uint32_t* cnt;    // [G] arrival counters, zero between launches (S > 1)
+  float* part;      // [G][S][4 * T tiles][64 lanes] f4 partial tiles (S > 1)
+};
+LsConfig choose_decode_ls(int fmt, const GemmDesc& d);
+size_t decode_ls_workspace_bytes(const GemmDesc& d, const LsConfig& c);
+hipError_t launch_decode_ls(int fmt, int dtype, GemmDesc d, const LsConfig& c, void* ws, hipStream_t stream);
+
 // One prefill launch: (16 * RT * WM)-row x 256-column tiles over the columns of d; psk
 // stream-K workgroups share the last tiles - dp tiles along K, dp workgroups own one tile
 // each.

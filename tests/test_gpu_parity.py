@@ -109,7 +109,13 @@ def test_golden_fixture(cuda):
         check(y, data[f"{case}/Y64"], xdt, case)
 
 
-def test_zero_point_and_one_hot_exact(cuda):
+@pytest.mark.parametrize("kernel", [0, 1])
+def test_zero_point_and_one_hot_exact(cuda, kernel):
+    with decode_env(KERNEL=kernel):
+        zero_point_and_one_hot(cuda)
+
+
+def zero_point_and_one_hot(cuda):
     K, N = 512, 48
     P = O.Problem(O.INT4, 1, K, N, 128, O.F16, seed=700)
     ks = [0, 7, 8, 127, 128, 300, 511]
@@ -121,10 +127,10 @@ def test_zero_point_and_one_hot_exact(cuda):
     Wdq = O.dequant(O.INT4, P.W, P.scales.ravel(), K, N, 128)
     expect = O.to_f32(O.from_f32(Wdq[ks], O.F16), O.F16)  # the dequantised row, rounded to fp16 once
     assert np.array_equal(y, expect)
-    # All weights at the zero point. The decode kernel dequantises int4 to magic + q (magic
-    # 1024 or 64 per fragment word) and removes magic + 8 with a correction MFMA, so q = 8
-    # leaves only the fp32 rounding of per-k-block sums of at most 1032 |x| (8 dependent
-    # MFMAs, each rounding at most twice): |y| <= 16 * 2^-24 * 1032 * sum_kb (sum|x|) s.
+    # All weights at the zero point. The decode kernels dequantise int4 to magic + q (magic
+    # 1024 or 64 per fragment word) and remove magic + 8 with correction MFMAs, so q = 8
+    # leaves only the fp32 rounding of per-k-block sums of at most 1032 |x| (8 MFMAs, each
+    # rounding at most twice): |y| <= 16 * 2^-24 * 1032 * sum_kb (sum|x|) s.
     W8 = np.full((K // 8) * N, 0x88888888, dtype=np.uint32)
     y0 = to_host_f32(hq.gemm(O.INT4, D.X, to_dev_u32(hq.repack(O.INT4, W8, K, N)), D.S, N))
     xsum = np.abs(O.to_f32(P.X, O.F16).astype(np.float64)).reshape(P.M, K // 128, 128).sum(-1)
@@ -239,11 +245,20 @@ def test_device_repack_matches_host(cuda, fmt):
 
 
 # ---------------------------------------------------------------- decode work decomposition
+# Keys of the per-wavefront kernel's decomposition; forcing any of them also selects that
+# kernel (HQ_DECODE_KERNEL=0), which otherwise serves only M <= 3.
+_PW_KEYS = {"T", "WK", "P", "G", "U", "CONTIG"}
+
+
 class decode_env:
-    """Force the decode decomposition (slab width T, wavefronts WK, workgroups P, ring
-    depth U) for a block."""
+    """Force the decode kernel (KERNEL=0 per-wavefront, 1 lockstep) and its decomposition
+    for a block: per-wavefront slab width T, wavefronts WK, workgroups P, ring depth U;
+    lockstep LS_KG (k-groups), LS_T (tiles per wavefront), LS_U (steps in flight), LS_S
+    (pieces per slab)."""
 
     def __init__(self, **kv):
+        if "KERNEL" not in kv and _PW_KEYS & set(kv):
+            kv["KERNEL"] = 0
         self.kv = {f"HQ_DECODE_{k}": str(v) for k, v in kv.items()}
 
     def __enter__(self):
@@ -365,6 +380,65 @@ def test_decode_variable_slabs_fused(cuda, G, Pg):
         outs = hq.gemm_fused(O.TERNARY2, devs[0].X, [(d.Wp, d.S, d.P.N) for d in devs])
     for d, y in zip(devs, outs):
         check(y, d.P.reference(), O.BF16, f"fused variable slabs G={G} P={Pg} N={d.P.N}", d.P)
+
+
+# ---------------------------------------------------------------- lockstep decode kernel
+# (KG, T, U, S): every instantiated (k-groups, tiles per wavefront, steps in flight), with
+# whole slabs (S = 1) and K splits into 2..8 pieces (S = 3 and 5 cut 16 k-blocks unevenly;
+# with four k-groups and 3-4 k-blocks per piece some k-groups get none).
+LS_CFGS = [(1, 2, 4, 1), (2, 1, 4, 1), (2, 2, 2, 1), (2, 2, 3, 1), (2, 4, 2, 1), (4, 1, 3, 1), (4, 2, 2, 1),
+           (4, 2, 3, 1), (2, 2, 2, 3), (2, 2, 3, 8), (4, 2, 2, 5), (2, 1, 4, 2), (1, 2, 4, 4)]
+
+
+@pytest.mark.parametrize("KG,T,U,S", LS_CFGS)
+@pytest.mark.parametrize("M", [4, 7, 16])
+def test_lockstep_configs_int4(cuda, KG, T, U, S, M):
+    # K = 2048 (16 k-blocks), N = 1000 (63 tiles: the last slab is partial for every width).
+    P = O.Problem(O.INT4, M, 2048, 1000, 128, O.F16, seed=3000 + M)
+    D = DeviceProblem(P)
+    with decode_env(KERNEL=1, LS_KG=KG, LS_T=T, LS_U=U, LS_S=S):
+        y = D.run()
+        y2 = D.run()
+    assert torch_equal(y, y2)  # fixed summation order: bit-identical from run to run
+    check(y, P.reference(), O.F16, f"KG={KG} T={T} U={U} S={S} M={M}", P)
+
+
+@pytest.mark.parametrize("fmt,xdt", [(O.INT4, O.BF16), (O.TERNARY2, O.F16), (O.TERNARY2, O.BF16)])
+@pytest.mark.parametrize("KG,T,U,S", [(2, 2, 2, 1), (2, 2, 2, 3), (4, 2, 3, 2), (2, 1, 4, 1), (1, 2, 4, 2)])
+def test_lockstep_formats(cuda, fmt, xdt, KG, T, U, S):
+    # group 256: one scale row serves two k-blocks.
+    P = O.Problem(fmt, 9, 1536, 700, 256, xdt, seed=3100)
+    D = DeviceProblem(P)
+    with decode_env(KERNEL=1, LS_KG=KG, LS_T=T, LS_U=U, LS_S=S):
+        y = D.run()
+    check(y, P.reference(), xdt, f"fmt={fmt} KG={KG} T={T} U={U} S={S}", P)
+
+
+@pytest.mark.parametrize("S", [1, 3])
+def test_lockstep_fused(cuda, S):
+    # Slabs never straddle segments; each segment's last slab is partial.
+    Ns, K, M = [600, 130, 1000], 1024, 6
+    probs = [O.Problem(O.INT4, M, K, n, 128, O.F16, seed=3200 + i) for i, n in enumerate(Ns)]
+    for p in probs[1:]:
+        p.X = probs[0].X
+    devs = [DeviceProblem(p) for p in probs]
+    with decode_env(KERNEL=1, LS_S=S):
+        outs = hq.gemm_fused(O.INT4, devs[0].X, [(d.Wp, d.S, d.P.N) for d in devs])
+    for d, y in zip(devs, outs):
+        check(y, d.P.reference(), O.F16, f"lockstep fused S={S} N={d.P.N}", d.P)
+
+
+@pytest.mark.parametrize("M", [4, 16])
+def test_lockstep_matches_per_wavefront(cuda, M):
+    # The two decode kernels compute the same values up to fp32 summation order.
+    P = O.Problem(O.INT4, M, 5120, 5120, 128, O.F16, seed=3300 + M)
+    D = DeviceProblem(P)
+    with decode_env(KERNEL=1):
+        y1 = D.run()
+    with decode_env(KERNEL=0):
+        y0 = D.run()
+    assert O.normwise_error(to_host_f32(y1), to_host_f32(y0)) <= OUT_TOL[O.F16]
+    check(y1, P.reference(threads=16), O.F16, f"lockstep M={M}")
 
 
 class prefill_env(decode_env):
