@@ -8,7 +8,7 @@
 // Here a workgroup owns a slab of 4 * T column tiles (16 columns each) and a contiguous
 // range of 128-deep k-blocks ("piece"); a slab's k-blocks are split over S workgroups
 // (S = 1 for wide weights). The workgroup has KG k-groups of four wavefronts; wavefront i
-// of every k-group streams tiles 4 i .. 4 i + T - 1 of the slab, and at step q k-group kg
+// of every k-group streams tiles T i .. T i + T - 1 of the slab, and at step q k-group kg
 // takes k-block q * KG + kg of the piece, so the KG k-groups split K inside the CU and
 // meet once, at the end, in LDS. The four wavefronts of a k-group walk its k-blocks in
 // lockstep, each streaming its T tiles (1 KiB per tile and k-block, int4) from HBM into
