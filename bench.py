@@ -263,7 +263,25 @@ def run_gpu(args):
             prefill[name] = {"M": M, "N": ntot, "us": round(us, 1), "TFLOPs": round(tf, 1),
                              "frac_mfma_f16": round(tf / MFMA_F16_PEAK_TFLOPS, 4)}
             log(f"{name}: {us:.1f} us, {tf:.1f} TFLOP/s")
-    return value, ms_per_step, roofline, cases, prefill
+    # ---- GGUF TQ1_0 import (model load): blocks -> packed ternary tiles + scales on the device ----
+    K, N = 5120, 27648
+    nbytes = hq.tq1_0_bytes(K, N)
+    blocks = [torch.randint(0, 256, (nbytes,), dtype=torch.uint8, device="cuda") for _ in range(4)]
+    outs = hq.repack_tq1_0_device(blocks[0], K, N)
+
+    def launches():
+        for r in range(16):
+            hq.repack_tq1_0_device(blocks[r % 4], K, N, out=outs)
+        return 16
+
+    us = graph_time_us(torch, stream, launches)
+    moved = nbytes + 4 * hq.packed_words(hq.FORMAT_TERNARY2, K, N) + 2 * (K // 256) * N
+    gbs = moved / (us * 1e-6) / 1e9
+    tq1 = {"K": K, "N": N, "us": round(us, 1), "bytes": moved, "GBps": round(gbs, 1),
+           "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+    log(f"TQ1_0 import K={K} N={N}: {us:.1f} us, {gbs:.1f} GB/s")
+    del blocks, outs
+    return value, ms_per_step, roofline, cases, prefill, tq1
 
 
 def run_cpu(budget_s: float = 10.0):
@@ -324,7 +342,7 @@ def main():
         else:
             run_roofline_only(torch, hq)
         return
-    value, ms_per_step, roofline, cases, prefill = run_gpu(args)
+    value, ms_per_step, roofline, cases, prefill, tq1 = run_gpu(args)
     cpu = None if args.no_cpu else run_cpu(args.cpu_budget)
     out = {
         "metric": "qGEMM GB/s at M<=16 (% of HBM peak) + TFLOP/s at M=2048 (% MFMA peak)",
@@ -346,6 +364,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "prefill": prefill,
+        "tq1_0_import": tq1,
         "cases": cases,
     }
     print(json.dumps(out), flush=True)

@@ -113,6 +113,28 @@ hq_status hq_repack_int4_device(const uint32_t* d_src_linear, uint32_t* d_dst_pa
 hq_status hq_repack_ternary2_device(const uint32_t* d_src_linear, uint32_t* d_dst_packed, uint32_t K,
                                     uint32_t N, uint32_t* d_bad_flag, hq_stream stream);
 
+/* ---- GGUF TQ1_0 import: the reference's ternary weight blocks (BlockTQ1_0,
+ *      native_decoder.cu:31-36), read today by kernel_gemv_tq1_0 (native_decoder.cu:155-206) ----
+ * A TQ1_0 tensor of N output rows and K inputs is N rows of K/256 blocks of 56 bytes
+ * ([out][in/256], native_decoder.cu:167): fp16 d, 52 bytes of base-3 trits, 2 padding bytes.
+ * Element i of a block is w = d * t_i, t_i in {-1, 0, 1}: digit i % 5 of trit byte i / 5 for
+ * i < 250, digit (i - 250) % 3 of trit byte 50 + (i - 250) / 3 after (native_decoder.cu:87-101;
+ * any byte value decodes digit by digit). The import is lossless: codes c = t + 1 and d are
+ * kept as they are, one scale per 256 inputs, so an imported weight is used with group = 256.
+ * A non-finite d is kept; the GEMM then drops its block, as kernel_gemv_tq1_0 skips it
+ * (native_decoder.cu:174). K % 256 == 0. */
+/* Bytes of such a tensor (0 on a bad shape). */
+size_t hq_tq1_0_bytes(uint32_t K, uint32_t N);
+/* Host to host: blocks -> ternary linear codes u32 [K/16][N] (the hq_repack_ternary2 input)
+ * and fp16 scales [K/256][N]. */
+hq_status hq_convert_tq1_0(const void* blocks, uint32_t K, uint32_t N, uint32_t* codes_linear,
+                           uint16_t* scales);
+/* On the device, one kernel on `stream`: blocks (8-byte aligned) -> the gfx950 ternary tile
+ * layout (hq_packed_words(HQ_FORMAT_TERNARY2, K, N) words) and fp16 scales [K/256][N]; the
+ * same words as hq_convert_tq1_0 followed by hq_repack_ternary2. */
+hq_status hq_repack_tq1_0_device(const void* d_blocks, uint32_t K, uint32_t N, uint32_t* d_packed,
+                                 uint16_t* d_scales, hq_stream stream);
+
 /* ---- forward: replaces MarlinGemmEngine::forward_marlin_int4 (marlin_gemm.hpp:100-107,
  *      marlin_gemm.cu:556-601) ----
  * Y[m, n] = sum_k X[m, k] * w(k, n), fp32 accumulation, Y rounded to the activation dtype.

@@ -385,6 +385,43 @@ hq_status hq_unpack_ternary2(const uint32_t* packed, uint32_t* dst, uint32_t K, 
   return ok();
 }
 
+size_t hq_tq1_0_bytes(uint32_t K, uint32_t N) {
+  if (K == 0 || N == 0 || K % hq::kTq1K) return 0;
+  return (size_t)N * (K / hq::kTq1K) * hq::kTq1Bytes;
+}
+
+hq_status hq_convert_tq1_0(const void* blocks, uint32_t K, uint32_t N, uint32_t* codes, uint16_t* scales) {
+  if (!blocks || !codes || !scales) return fail(HQ_ERR_INVALID_ARG, "null pointer");
+  if (hq_tq1_0_bytes(K, N) == 0) return fail(HQ_ERR_SHAPE, "K=%u must be a positive multiple of 256, N=%u > 0", K, N);
+  const uint32_t nb = K / hq::kTq1K;
+  const uint8_t* src = static_cast<const uint8_t*>(blocks);
+  parallel_for(N, [=](size_t b, size_t e) {
+    for (size_t n = b; n < e; ++n)
+      for (uint32_t blk = 0; blk < nb; ++blk) {
+        const uint8_t* p = src + (n * nb + blk) * hq::kTq1Bytes;
+        scales[(size_t)blk * N + n] = (uint16_t)(p[0] | (p[1] << 8));
+        for (uint32_t w = 0; w < hq::kTq1K / 16; ++w) {
+          uint32_t lin = 0;
+          for (uint32_t i = 0; i < 16; ++i) lin |= hq::tq1_code(p + 2, 16 * w + i) << (2 * i);
+          codes[((size_t)blk * (hq::kTq1K / 16) + w) * N + n] = lin;
+        }
+      }
+  });
+  return ok();
+}
+
+hq_status hq_repack_tq1_0_device(const void* blocks, uint32_t K, uint32_t N, uint32_t* packed, uint16_t* scales,
+                                 hq_stream stream) {
+  if (!blocks || !packed || !scales) return fail(HQ_ERR_INVALID_ARG, "null pointer");
+  if (hq_tq1_0_bytes(K, N) == 0) return fail(HQ_ERR_SHAPE, "K=%u must be a positive multiple of 256, N=%u > 0", K, N);
+  if (reinterpret_cast<uintptr_t>(blocks) % 8 || reinterpret_cast<uintptr_t>(packed) % 4 ||
+      reinterpret_cast<uintptr_t>(scales) % 2)
+    return fail(HQ_ERR_ALIGNMENT, "blocks must be 8-byte, packed 4-byte and scales 2-byte aligned");
+  return from_hip(hq::launch_repack_tq1_0(static_cast<const uint8_t*>(blocks), packed, scales, K, N,
+                                          reinterpret_cast<hipStream_t>(stream)),
+                  "repack launch");
+}
+
 hq_status hq_repack_int4_device(const uint32_t* src, uint32_t* dst, uint32_t K, uint32_t N, hq_stream stream) {
   if (!src || !dst) return fail(HQ_ERR_INVALID_ARG, "null pointer");
   hq_status st = check_repack_shape(HQ_FORMAT_INT4, K, N);

@@ -114,5 +114,7 @@ hipError_t launch_repack_int4(const uint32_t* src, uint32_t* dst, uint32_t K, ui
                               hipStream_t stream);
 hipError_t launch_repack_ternary2(const uint32_t* src, uint32_t* dst, uint32_t K, uint32_t N,
                                   uint32_t* bad_flag, hipStream_t stream);
+hipError_t launch_repack_tq1_0(const uint8_t* blocks, uint32_t* dst, uint16_t* scales, uint32_t K, uint32_t N,
+                               hipStream_t stream);
 
 }  // namespace hq

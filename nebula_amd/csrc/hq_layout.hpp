@@ -87,4 +87,19 @@ HQ_HD uint32_t tern_pack_word(uint32_t lin0, uint32_t lin1, uint32_t half, bool*
   return out;
 }
 
+
+// GGUF TQ1_0 (the PrismML block, GGML type 143; hydrogen/src/model/native_decoder.cu:31-36):
+// 256 weights in 56 bytes: fp16 d (bytes 0..1), 52 bytes of base-3 trits (2..53), 2 padding
+// bytes. Element i < 250 is digit i % 5 of trit byte i / 5, element 250 + j is digit j % 3 of
+// trit byte 50 + j / 3, digit j of a byte being (byte / 3^j) % 3 for any byte value
+// (native_decoder.cu:87-101). The digit is the ternary code c = t + 1 of the element.
+constexpr uint32_t kTq1Bytes = 56;
+constexpr uint32_t kTq1K = 256;
+HQ_HD uint32_t tq1_code(const uint8_t* trits, uint32_t i) {
+  const uint32_t byte = i < 250u ? i / 5u : 50u + (i - 250u) / 3u;
+  const uint32_t digit = i < 250u ? i % 5u : (i - 250u) % 3u;
+  uint32_t v = trits[byte];
+  for (uint32_t j = 0; j < digit; ++j) v /= 3u;
+  return v % 3u;
+}
 }  // namespace hq

@@ -232,11 +232,16 @@ __global__ void __launch_bounds__(256 * WM) hq_prefill_kernel(const GemmDesc d, 
       __builtin_amdgcn_sched_barrier(0);
       if (kb < kz) {  // uniform; no loads inside
         const char* sbase = smem + (kb & 1u) * kStageBytes;
+        // Ternary: a group whose scale is not finite contributes nothing (its scale reads as 0).
+        uint32_t sc[kTilesPerWave];
+#pragma unroll
+        for (int t = 0; t < kTilesPerWave; ++t)
+          sc[t] = FMT == HQ_FORMAT_TERNARY2 && (sr[slot][t] & 0x7C00u) == 0x7C00u ? 0u : sr[slot][t];
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           u4 b[kTilesPerWave];
 #pragma unroll
-          for (int t = 0; t < kTilesPerWave; ++t) b[t] = dq_scaled<FMT, DT>(wr[slot][t], c, sr[slot][t], dqk);
+          for (int t = 0; t < kTilesPerWave; ++t) b[t] = dq_scaled<FMT, DT>(wr[slot][t], c, sc[t], dqk);
 #pragma unroll
           for (int r = 0; r < RT; ++r) {
             const u4 a = *reinterpret_cast<const u4*>(sbase + (wrow0 + 16u * r) * 256u + ldsoff[c]);
@@ -451,7 +456,11 @@ int env_int(const char* name, int dflt) {
 // Tile height: 64 rows (RT 4, WM 1) up to M = 64, 128 rows (8, 1) up to 128, else 256 (8, 2).
 void prefill_shape(uint32_t M, int& RT, int& WM) {
   const int eWM = env_int("HQ_PREFILL_WM", 0);  // tuning override: 128 (1) or 256 (2) rows
-  if (eWM == 1 || eWM == 2) {
+  const int eRT = env_int("HQ_PREFILL_RT", 0);  // tuning override: 16 = 256 rows, one row wave
+  if (eRT == 16 && M > 128) {
+    RT = 16;
+    WM = 1;
+  } else if (eWM == 1 || eWM == 2) {
     RT = 8;
     WM = eWM;
   } else if (M <= 64) {
@@ -468,13 +477,15 @@ void prefill_shape(uint32_t M, int& RT, int& WM) {
 int prefill_slots(int fmt, int RT, int WM) {
   int occ = 1;
   if (fmt == HQ_FORMAT_INT4) {
-    occ = RT == 4 ? prefill_occupancy<HQ_FORMAT_INT4, HQ_DTYPE_F16, 4, 1>()
-                  : (WM == 1 ? prefill_occupancy<HQ_FORMAT_INT4, HQ_DTYPE_F16, 8, 1>()
-                             : prefill_occupancy<HQ_FORMAT_INT4, HQ_DTYPE_F16, 8, 2>());
+    occ = RT == 4    ? prefill_occupancy<HQ_FORMAT_INT4, HQ_DTYPE_F16, 4, 1>()
+          : RT == 16 ? prefill_occupancy<HQ_FORMAT_INT4, HQ_DTYPE_F16, 16, 1>()
+                     : (WM == 1 ? prefill_occupancy<HQ_FORMAT_INT4, HQ_DTYPE_F16, 8, 1>()
+                                : prefill_occupancy<HQ_FORMAT_INT4, HQ_DTYPE_F16, 8, 2>());
   } else {
-    occ = RT == 4 ? prefill_occupancy<HQ_FORMAT_TERNARY2, HQ_DTYPE_F16, 4, 1>()
-                  : (WM == 1 ? prefill_occupancy<HQ_FORMAT_TERNARY2, HQ_DTYPE_F16, 8, 1>()
-                             : prefill_occupancy<HQ_FORMAT_TERNARY2, HQ_DTYPE_F16, 8, 2>());
+    occ = RT == 4    ? prefill_occupancy<HQ_FORMAT_TERNARY2, HQ_DTYPE_F16, 4, 1>()
+          : RT == 16 ? prefill_occupancy<HQ_FORMAT_TERNARY2, HQ_DTYPE_F16, 16, 1>()
+                     : (WM == 1 ? prefill_occupancy<HQ_FORMAT_TERNARY2, HQ_DTYPE_F16, 8, 1>()
+                                : prefill_occupancy<HQ_FORMAT_TERNARY2, HQ_DTYPE_F16, 8, 2>());
   }
   return cu_count() * occ;
 }
@@ -482,6 +493,7 @@ int prefill_slots(int fmt, int RT, int WM) {
 template <int FMT, int DT>
 hipError_t launch_fd(const PrefillLaunch& c, void* ws, hipStream_t stream) {
   if (c.RT == 4) return launch_rt<FMT, DT, 4, 1>(c, ws, stream);
+  if (c.RT == 16) return launch_rt<FMT, DT, 16, 1>(c, ws, stream);
   if (c.WM == 1) return launch_rt<FMT, DT, 8, 1>(c, ws, stream);
   return launch_rt<FMT, DT, 8, 2>(c, ws, stream);
 }
@@ -559,7 +571,7 @@ PrefillConfig choose_prefill(int fmt, const GemmDesc& d) {
   }
   const uint32_t r = l.tiles % slots;
   if (env_int("HQ_PREFILL_TAIL", 1) == 0 || r == 0u || RT == 4) return c;
-  const int hRT = WM == 2 ? 8 : 4;  // half-height tiles: 256 -> 128, 128 -> 64 rows
+  const int hRT = RT * WM / 2;  // half-height tiles of one row wave: 256 -> 128, 128 -> 64 rows
   const uint32_t bands = (d.M + 16u * RT * WM - 1) / (16u * RT * WM);
   const uint32_t nb = count_blocks(d);
   const uint32_t k = (r + bands - 1) / bands;

@@ -37,7 +37,8 @@ EXPORTS = (
     "hq_version", "hq_last_error", "hq_status_string", "hq_linear_words", "hq_packed_words",
     "hq_workspace_bytes", "hq_repack_int4_ref", "hq_repack_int4", "hq_repack_ternary2",
     "hq_unpack_int4", "hq_unpack_ternary2", "hq_repack_int4_device", "hq_repack_ternary2_device",
-    "hq_gemm_w4a16", "hq_gemm_w2a16", "hq_gemm_fused",
+    "hq_gemm_w4a16", "hq_gemm_w2a16", "hq_gemm_fused", "hq_tq1_0_bytes", "hq_convert_tq1_0",
+    "hq_repack_tq1_0_device",
 )
 
 
@@ -92,6 +93,12 @@ def lib() -> ctypes.CDLL:
         f = getattr(L, name)
         f.restype = i32
         f.argtypes = [vp, i32, i64, vp, vp, vp, i64, u32, u32, u32, u32, vp, sz, vp]
+    L.hq_tq1_0_bytes.restype = sz
+    L.hq_tq1_0_bytes.argtypes = [u32, u32]
+    L.hq_convert_tq1_0.restype = i32
+    L.hq_convert_tq1_0.argtypes = [vp, u32, u32, vp, vp]
+    L.hq_repack_tq1_0_device.restype = i32
+    L.hq_repack_tq1_0_device.argtypes = [vp, u32, u32, vp, vp, vp]
     L.hq_gemm_fused.restype = i32
     L.hq_gemm_fused.argtypes = [vp, i32, i64, i32, ctypes.POINTER(Segment), u32, u32, u32, u32, vp, sz, vp]
     _lib = L
@@ -148,6 +155,22 @@ def unpack(fmt: int, packed: np.ndarray, K: int, N: int) -> np.ndarray:
     return dst
 
 
+def tq1_0_bytes(K: int, N: int) -> int:
+    return int(lib().hq_tq1_0_bytes(K, N))
+
+
+def convert_tq1_0(blocks: np.ndarray, K: int, N: int) -> tuple[np.ndarray, np.ndarray]:
+    """GGUF TQ1_0 blocks (N rows of K/256 56-byte blocks) -> (ternary linear codes [K/16 * N] u32,
+    fp16 scale bits [K/256, N] u16); use the scales with group = 256."""
+    src = np.ascontiguousarray(blocks, dtype=np.uint8)
+    if src.size != tq1_0_bytes(K, N):
+        raise ValueError(f"TQ1_0 tensor has {src.size} bytes, expected {tq1_0_bytes(K, N)}")
+    codes = np.empty(linear_words(FORMAT_TERNARY2, K, N), dtype=np.uint32)
+    scales = np.empty((K // 256, N), dtype=np.uint16)
+    check(lib().hq_convert_tq1_0(src.ctypes.data, K, N, codes.ctypes.data, scales.ctypes.data))
+    return codes, scales
+
+
 # ---------------------------------------------------------------- device calls
 def _stream_ptr(stream) -> Optional[int]:
     import torch
@@ -178,6 +201,27 @@ def repack_device(fmt: int, linear, K: int, N: int, stream=None, bad_flag=None):
         flag = bad_flag.data_ptr() if bad_flag is not None else None
         check(lib().hq_repack_ternary2_device(linear.data_ptr(), out.data_ptr(), K, N, flag, sp))
     return out
+
+
+def repack_tq1_0_device(blocks, K: int, N: int, stream=None, out=None):
+    """GGUF TQ1_0 blocks in a device uint8 tensor -> (packed ternary weight, fp16 scales [K/256, N]),
+    device tensors (new ones, or the pair `out`); use them with FORMAT_TERNARY2 and group = 256."""
+    import torch
+
+    if blocks.numel() * blocks.element_size() != tq1_0_bytes(K, N):
+        raise ValueError(f"TQ1_0 tensor has {blocks.numel() * blocks.element_size()} bytes, "
+                         f"expected {tq1_0_bytes(K, N)}")
+    if out is None:
+        packed = torch.empty(packed_words(FORMAT_TERNARY2, K, N), dtype=torch.int32, device=blocks.device)
+        scales = torch.empty((K // 256, N), dtype=torch.float16, device=blocks.device)
+    else:
+        packed, scales = out
+        if packed.numel() * packed.element_size() < 4 * packed_words(FORMAT_TERNARY2, K, N) or \
+                scales.numel() * scales.element_size() < 2 * (K // 256) * N:
+            raise ValueError("output tensors too small")
+    check(lib().hq_repack_tq1_0_device(blocks.data_ptr(), K, N, packed.data_ptr(), scales.data_ptr(),
+                                       _stream_ptr(stream)))
+    return packed, scales
 
 
 def workspace_bytes(fmt: int, M: int, K: int, N: int, group: int = 128) -> int:

@@ -258,3 +258,46 @@ void hqo_fidelity(const float* a, const float* b, size_t count, double* max_abs,
     *max_abs = mx;
     *mse = count ? sq / (double)count : 0.0;
 }
+
+/* ---- GGUF TQ1_0 ---- */
+uint32_t hqo_tq1_0_code(const uint8_t* block, uint32_t i) {
+    const uint8_t* packed = block + 2;
+    uint32_t byte_idx, digit;
+    if (i < 250) {
+        byte_idx = i / 5;
+        digit = i % 5;
+    } else {
+        byte_idx = 50 + (i - 250) / 3;
+        digit = (i - 250) % 3;
+    }
+    uint32_t val = packed[byte_idx];
+    for (uint32_t s = 0; s < digit; ++s) val /= 3;
+    return val % 3;
+}
+
+uint16_t hqo_tq1_0_scale(const uint8_t* block) {
+    return (uint16_t)(block[0] | (block[1] << 8));
+}
+
+void hqo_gemv_tq1_0(const float* X, const uint8_t* W, float* Y, uint32_t M, uint32_t K, uint32_t N,
+                    int threads) {
+    const uint32_t nb = K / 256;
+    if (threads > 0) omp_set_num_threads(threads);
+#pragma omp parallel for schedule(static)
+    for (long long n = 0; n < (long long)N; ++n) {
+        for (uint32_t m = 0; m < M; ++m) {
+            const float* x = X + (size_t)m * K;
+            float sum = 0.0f;
+            for (uint32_t b = 0; b < nb; ++b) {
+                const uint8_t* blk = W + ((size_t)n * nb + b) * 56;
+                const float d = hqo_f16_to_f32(hqo_tq1_0_scale(blk));
+                if (!isfinite(d)) continue;
+                for (uint32_t i = 0; i < 256; ++i) {
+                    const float t = (float)((int)hqo_tq1_0_code(blk, i) - 1);
+                    sum = fmaf(d * t, x[256 * b + i], sum);
+                }
+            }
+            Y[(size_t)m * N + n] = sum;
+        }
+    }
+}

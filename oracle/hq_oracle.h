@@ -13,6 +13,8 @@
  *   hqo_gemm_f32          hydrogen/src/model/marlin_gemm.cu:52-70 (fp32, k ascending, FMA)
  *   hqo_qgemm             the two above fused row by row (bit-identical to running them in turn)
  *   hqo_fidelity          hydrogen/src/model/marlin_gemm.cu:619-644 (max |d|, MSE in fp64)
+ *   hqo_tq1_0_code        hydrogen/src/model/native_decoder.cu:31-36, 87-101 (base-3 trits of a TQ1_0 block)
+ *   hqo_gemv_tq1_0        hydrogen/src/model/native_decoder.cu:155-206 (kernel_gemv_tq1_0, any M)
  *
  * The generator (hqo_rng_*, hqo_gen_*) is this build's own specification, not
  * the reference's: the reference seeds std::mt19937 with implementation-defined
@@ -76,6 +78,23 @@ int hqo_qgemm(const uint16_t* X, int xdtype, size_t ldx, int fmt, const uint32_t
               float* Y, int threads);
 /* marlin_gemm.cu:619-644: max |a - b| and mean squared difference, accumulated in fp64. */
 void hqo_fidelity(const float* a, const float* b, size_t count, double* max_abs, double* mse);
+
+/* ---- GGUF TQ1_0 (the reference's PrismML block, GGML type 143): 256 weights in 56 bytes,
+ *      fp16 d at bytes 0..1, 52 bytes of base-3 trits at 2..53, 2 padding bytes ---- */
+/* native_decoder.cu:87-101: code c = t + 1 (0, 1, 2) of element i (0..255) of one block.
+ * Elements 0..249 are digit i % 5 of packed byte i / 5, elements 250..255 digit (i - 250) % 3
+ * of packed byte 50 + (i - 250) / 3; digit j of a byte is (byte / 3^j) % 3, by repeated
+ * division, for any byte value. */
+uint32_t hqo_tq1_0_code(const uint8_t* block, uint32_t i);
+/* The block's d as fp16 bits (little-endian bytes 0..1). */
+uint16_t hqo_tq1_0_scale(const uint8_t* block);
+/* native_decoder.cu:155-206 (kernel_gemv_tq1_0) for M activation rows: W holds N rows of
+ * K/256 blocks ([out][in/256], :167). Y[m*N + n] = sum over blocks b of row n whose d is finite
+ * (non-finite d: the block is skipped, :174) of sum_i fma(d * t_i, X[m*K + 256 b + i], .), fp32,
+ * blocks and elements ascending (the reference splits blocks over 32 lanes and sums the lanes
+ * in a tree; results agree within fp32 reassociation). */
+void hqo_gemv_tq1_0(const float* X, const uint8_t* W, float* Y, uint32_t M, uint32_t K, uint32_t N,
+                    int threads);
 
 #ifdef __cplusplus
 }

@@ -52,6 +52,11 @@ def lib() -> ctypes.CDLL:
     L.hqo_qgemm.restype = i32
     L.hqo_qgemm.argtypes = [vp, i32, sz, i32, vp, vp, u32, u32, u32, u32, vp, i32]
     L.hqo_fidelity.argtypes = [vp, vp, sz, ctypes.POINTER(dbl), ctypes.POINTER(dbl)]
+    L.hqo_tq1_0_code.restype = u32
+    L.hqo_tq1_0_code.argtypes = [vp, u32]
+    L.hqo_tq1_0_scale.restype = u16
+    L.hqo_tq1_0_scale.argtypes = [vp]
+    L.hqo_gemv_tq1_0.argtypes = [vp, vp, vp, u32, u32, u32, i32]
     _lib = L
     return L
 
@@ -145,6 +150,48 @@ def fidelity(a: np.ndarray, b: np.ndarray) -> tuple[float, float]:
     mx, mse = ctypes.c_double(), ctypes.c_double()
     lib().hqo_fidelity(_p(a), _p(b), a.size, ctypes.byref(mx), ctypes.byref(mse))
     return mx.value, mse.value
+
+
+TQ1_0_BLOCK_BYTES = 56
+
+
+def tq1_0_codes(block: np.ndarray) -> np.ndarray:
+    """Codes c = t + 1 of the 256 elements of one 56-byte TQ1_0 block."""
+    b = np.ascontiguousarray(block, dtype=np.uint8)
+    assert b.size == TQ1_0_BLOCK_BYTES
+    return np.array([lib().hqo_tq1_0_code(_p(b), i) for i in range(256)], dtype=np.uint32)
+
+
+def tq1_0_scale(block: np.ndarray) -> int:
+    b = np.ascontiguousarray(block, dtype=np.uint8)
+    return int(lib().hqo_tq1_0_scale(_p(b)))
+
+
+def gemv_tq1_0(X: np.ndarray, blocks: np.ndarray, N: int, threads: int = 8) -> np.ndarray:
+    """kernel_gemv_tq1_0 over the rows of X (fp32 [M, K]); blocks: N rows of K/256 blocks."""
+    X = np.ascontiguousarray(X, dtype=np.float32)
+    W = np.ascontiguousarray(blocks, dtype=np.uint8)
+    M, K = X.shape
+    assert W.size == N * (K // 256) * TQ1_0_BLOCK_BYTES
+    Y = np.empty((M, N), dtype=np.float32)
+    lib().hqo_gemv_tq1_0(_p(X), _p(W), _p(Y), M, K, N, threads)
+    return Y
+
+
+def gen_tq1_0(seed: int, N: int, K: int, nonfinite_every: int = 0) -> np.ndarray:
+    """Random TQ1_0 blocks [N][K/256][56] (bytes uniform on 0..255, so every byte value, also those
+    above 242 that no encoder writes, is exercised); d = |N(0, 0.02)| in fp16; with nonfinite_every
+    > 0, every such block gets an Inf or NaN d."""
+    nb = K // 256
+    raw = np.random.default_rng(seed).integers(0, 256, N * nb * TQ1_0_BLOCK_BYTES, dtype=np.uint8)
+    blocks = raw.reshape(N * nb, TQ1_0_BLOCK_BYTES)
+    d = gen_normal(seed, 12, N * nb, 0.02, True, F16)
+    if nonfinite_every:
+        d[::nonfinite_every] = 0x7C00  # +Inf
+        d[nonfinite_every // 2::nonfinite_every] = 0x7E00  # NaN
+    blocks[:, 0] = (d & 0xFF).astype(np.uint8)
+    blocks[:, 1] = (d >> 8).astype(np.uint8)
+    return blocks.reshape(N, nb, TQ1_0_BLOCK_BYTES)
 
 
 # ------------------------------------------------------------ problem builder

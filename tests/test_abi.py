@@ -230,3 +230,36 @@ def test_ternary_repack_rejects_code_3():
     with pytest.raises(hq.HQError) as ei:
         hq.repack(hq.FORMAT_TERNARY2, src, K, N)
     assert ei.value.status == hq.HQ_ERR_BAD_CODE
+
+
+# ---------------------------------------------------------------- GGUF TQ1_0 import
+def test_tq1_0_bytes():
+    assert hq.tq1_0_bytes(5120, 27648) == 27648 * 20 * 56
+    assert hq.tq1_0_bytes(128, 16) == 0 and hq.tq1_0_bytes(0, 16) == 0
+
+
+@pytest.mark.parametrize("K,N", [(256, 1), (512, 17), (1280, 40)])
+def test_convert_tq1_0_matches_oracle(K, N):
+    blocks = O.gen_tq1_0(K + N, N, K, nonfinite_every=7)
+    codes, scales = hq.convert_tq1_0(blocks, K, N)
+    lin = codes.reshape(K // 16, N)
+    for n in range(N):
+        for b in range(K // 256):
+            assert scales[b, n] == O.tq1_0_scale(blocks[n, b])
+            c = O.tq1_0_codes(blocks[n, b])
+            words = lin[16 * b:16 * (b + 1), n]
+            mine = (words[:, None] >> (2 * np.arange(16, dtype=np.uint32))[None, :]) & 3
+            assert np.array_equal(mine.reshape(256), c), (n, b)
+    # The codes are valid ternary input: the host repack accepts them and round-trips.
+    packed = hq.repack(hq.FORMAT_TERNARY2, codes, K, N)
+    assert np.array_equal(hq.unpack(hq.FORMAT_TERNARY2, packed, K, N), codes)
+
+
+def test_convert_tq1_0_rejects_bad_arguments():
+    L = hq.lib()
+    buf = np.zeros(1 << 16, dtype=np.uint8)
+    p = buf.ctypes.data
+    assert L.hq_convert_tq1_0(p, 128, 4, p, p) == hq.HQ_ERR_SHAPE
+    assert L.hq_convert_tq1_0(None, 256, 4, p, p) == hq.HQ_ERR_INVALID_ARG
+    assert L.hq_repack_tq1_0_device(p, 384, 4, p, p, None) == hq.HQ_ERR_SHAPE
+    assert L.hq_repack_tq1_0_device(p + 4, 256, 4, p, p, None) == hq.HQ_ERR_ALIGNMENT

@@ -280,3 +280,65 @@ def test_golden_fixture_pins_oracle():
         Xf = O.to_f32(X, xdt)
         Wdq = O.dequant(fmt, W, S.ravel(), X.shape[1], N, int(data[f"{case}/group"]))
         assert np.all(np.abs(Y - expect) <= fp32_bound(Xf, Wdq)), case
+
+
+# ---------------------------------------------------------------- GGUF TQ1_0 (native_decoder.cu:31-36, 87-101)
+def tq1_block(trit_bytes, d_bits=0x3C00):
+    b = np.zeros(O.TQ1_0_BLOCK_BYTES, dtype=np.uint8)
+    b[0], b[1] = d_bits & 0xFF, d_bits >> 8
+    b[2:54] = trit_bytes
+    return b
+
+
+def test_tq1_0_constant_bytes():
+    # 0 -> every digit 0 (t = -1); 121 = 11111 in base 3 (t = 0); 242 = 22222 (t = +1).
+    for byte, c in ((0, 0), (121, 1), (242, 2)):
+        assert np.all(O.tq1_0_codes(tq1_block(byte)) == c)
+    assert O.tq1_0_scale(tq1_block(0, 0xBEEF)) == 0xBEEF
+
+
+def test_tq1_0_encode_decode_round_trip():
+    # Encode chosen trits the way a writer would (Horner, least significant digit first:
+    # element 5j + s is digit s of byte j; elements 250 + 3j + s digit s of byte 50 + j),
+    # then decode with the oracle. A wrong digit order, byte index or offset fails.
+    rng = np.random.default_rng(7)
+    for _ in range(20):
+        codes = rng.integers(0, 3, 256)
+        trit_bytes = np.zeros(52, dtype=np.int64)
+        for j in range(50):
+            trit_bytes[j] = sum(int(codes[5 * j + s]) * 3**s for s in range(5))
+        for j in range(2):
+            trit_bytes[50 + j] = sum(int(codes[250 + 3 * j + s]) * 3**s for s in range(3))
+        assert trit_bytes.max() <= 242
+        assert np.array_equal(O.tq1_0_codes(tq1_block(trit_bytes.astype(np.uint8))), codes)
+
+
+def test_tq1_0_bytes_above_242_decode_digit_by_digit():
+    # 255 = 100110 in base 3: digits (least first) 0, 1, 1, 0, 0 (the sixth is dropped); 243 = 100000.
+    c = O.tq1_0_codes(tq1_block(np.array([255] * 50 + [255, 243], dtype=np.uint8)))
+    assert list(c[:5]) == [0, 1, 1, 0, 0]
+    assert list(c[250:253]) == [0, 1, 1] and list(c[253:256]) == [0, 0, 0]
+
+
+def test_tq1_0_gemv_closed_forms():
+    K, N = 512, 3
+    blocks = np.stack([np.stack([tq1_block(242, 0x3800), tq1_block(0, 0x4000)]),     # +0.5 then -2.0
+                       np.stack([tq1_block(121, 0x3C00), tq1_block(242, 0x7C00)]),   # zeros, Inf d (skipped)
+                       np.stack([tq1_block(0, 0x7E00), tq1_block(121, 0x3C00)])])    # NaN d (skipped), zeros
+    X = np.random.default_rng(3).standard_normal((2, K)).astype(np.float32)
+    Y = O.gemv_tq1_0(X, blocks, N)
+    ref0 = 0.5 * X[:, :256].astype(np.float64).sum(1) - 2.0 * X[:, 256:].astype(np.float64).sum(1)
+    np.testing.assert_allclose(Y[:, 0], ref0, rtol=1e-5, atol=1e-4)
+    assert np.all(Y[:, 1] == 0) and np.all(Y[:, 2] == 0)
+
+
+def test_tq1_0_gemv_matches_float64_brute_force():
+    K, N, M = 768, 5, 3
+    blocks = O.gen_tq1_0(5, N, K)
+    X = np.random.default_rng(4).standard_normal((M, K)).astype(np.float32)
+    W = np.zeros((K, N))
+    for n in range(N):
+        for b in range(K // 256):
+            d = np.uint16(O.tq1_0_scale(blocks[n, b])).view(np.float16).astype(np.float64)
+            W[256 * b:256 * (b + 1), n] = d * (O.tq1_0_codes(blocks[n, b]).astype(np.float64) - 1)
+    np.testing.assert_allclose(O.gemv_tq1_0(X, blocks, N), X.astype(np.float64) @ W, rtol=1e-4, atol=1e-4)
