@@ -140,11 +140,14 @@ def zero_point_and_one_hot(cuda):
     assert np.abs(y0).max() < 1e-3
 
 
-def test_ternary_nonfinite_scale_drops_group(cuda):
-    P = O.Problem(O.TERNARY2, 4, 512, 64, 128, O.BF16, seed=710)
+@pytest.mark.parametrize("M,xdt", [(4, O.BF16), (4, O.F16), (40, O.F16), (100, O.BF16), (300, O.F16), (300, O.BF16)])
+def test_ternary_nonfinite_scale_drops_group(cuda, M, xdt):
+    # Decode (M <= 16) and every prefill tile shape (64, 128, 256 rows, stream-K at M = 300).
+    P = O.Problem(O.TERNARY2, M, 512, 64, 128, xdt, seed=710 + M)
     P.scales[1, 5] = 0x7E00
     P.scales[2, 9] = 0x7C00
-    check(DeviceProblem(P).run(), P.reference(), O.BF16, "nonfinite scale")
+    P.scales[3, 60] = 0xFC00
+    check(DeviceProblem(P).run(), P.reference(), xdt, f"nonfinite scale M={M}")
 
 
 def test_strided_operands(cuda):
