@@ -101,8 +101,10 @@ __device__ __forceinline__ void tile_geom(const GemmDesc& d, uint32_t nb, uint32
 // SKP = false: workgroup b computes whole tile b (grid dp). SKP = true: workgroup b
 // computes stream-K range b (grid psk). Two kernels, so that the stream-K fix-up's
 // registers never weigh on the whole-tile pipeline.
+// One-row-wave 128-row tiles are held to 256 VGPRs so that two workgroups share a CU (their
+// barriers are independent, so one's dequantisation overlaps the other's MFMAs).
 template <int FMT, int DT, int RT, int WM, bool SKP>
-__global__ void __launch_bounds__(256 * WM) hq_prefill_kernel(const GemmDesc d, const PrefillPlan pp) {
+__global__ void __launch_bounds__(256 * WM, WM == 1 && RT == 8 ? 2 : 1) hq_prefill_kernel(const GemmDesc d, const PrefillPlan pp) {
   constexpr uint32_t BM = 16u * RT * WM;
   constexpr uint32_t kStageBytes = BM * 256u;        // BM rows x 128 fp16
   constexpr uint32_t kPartBytes = BM * 256u * 4u;    // one fp32 partial tile
@@ -453,7 +455,9 @@ int env_int(const char* name, int dflt) {
   return v && *v ? std::atoi(v) : dflt;
 }
 
-// Tile height: 64 rows (RT 4, WM 1) up to M = 64, 128 rows (8, 1) up to 128, else 256 (8, 2).
+// Tile height: 64 rows (RT 4, WM 1) up to M = 64, else 128 rows (8, 1), two workgroups per
+// CU. Measured on MI355X at K = 5120, N = 27648: 128-row tiles two to a CU beat 256-row tiles
+// (two row waves, one workgroup per CU) by 3-8% from M = 512 to 4096.
 void prefill_shape(uint32_t M, int& RT, int& WM) {
   const int eWM = env_int("HQ_PREFILL_WM", 0);  // tuning override: 128 (1) or 256 (2) rows
   const int eRT = env_int("HQ_PREFILL_RT", 0);  // tuning override: 16 = 256 rows, one row wave
@@ -468,7 +472,7 @@ void prefill_shape(uint32_t M, int& RT, int& WM) {
     WM = 1;
   } else {
     RT = 8;
-    WM = M <= 128 ? 1 : 2;
+    WM = 1;
   }
 }
 
@@ -542,13 +546,13 @@ PrefillLaunch make_launch(int RT, int WM, const GemmDesc& d) {
 
 }  // namespace
 
-// Tiling of a prefill call (tile heights 256 / 128 / 64 rows as M allows):
+// Tiling of a prefill call (tile heights 128 / 64 rows as M allows; 256 on request):
 //  * A grid of at most half the workgroup slots is split s ways along K (stream-K,
 //    s = floor(slots / tiles), at most nkb / 4 so that a range keeps 4 k-blocks): s *
 //    tiles workgroups, each one aligned tile fraction, each tile s contributors.
-//  * Otherwise, when the last round of whole tiles would be part-empty, the last k column
-//    blocks (just enough to empty that round) run as a second launch of half-height
-//    tiles, if those fit in one round: the tail then takes half a round.
+//  * Otherwise, for 256-row tiles, when the last round of whole tiles would be part-empty,
+//    the last k column blocks (just enough to empty that round) run as a second launch of
+//    half-height tiles, if those fit in one round: the tail then takes half a round.
 //  * Otherwise whole tiles.
 PrefillConfig choose_prefill(int fmt, const GemmDesc& d) {
   PrefillConfig c{};
@@ -569,8 +573,10 @@ PrefillConfig choose_prefill(int fmt, const GemmDesc& d) {
       return c;
     }
   }
+  // Part-empty last rounds of 128-row tiles (two per CU) cost little: a lone workgroup has
+  // its CU to itself. Only 256-row tiles get the half-height tail launch.
   const uint32_t r = l.tiles % slots;
-  if (env_int("HQ_PREFILL_TAIL", 1) == 0 || r == 0u || RT == 4) return c;
+  if (env_int("HQ_PREFILL_TAIL", 1) == 0 || r == 0u || WM == 1) return c;
   const int hRT = RT * WM / 2;  // half-height tiles of one row wave: 256 -> 128, 128 -> 64 rows
   const uint32_t bands = (d.M + 16u * RT * WM - 1) / (16u * RT * WM);
   const uint32_t nb = count_blocks(d);

@@ -487,9 +487,10 @@ def test_prefill_stream_k_equals_whole_tiles(cuda, fmt, xdt, M, K, N, psk):
         assert err <= OUT_TOL[xdt]
 
 
-# A part-empty last round of whole tiles: the last column blocks run as a second launch of
-# half-height tiles. Each output element is the same fp32 chain in the same k order, so the
-# result equals whole-tile execution bit for bit. The fused case cuts a segment.
+# 256-row tiles (one workgroup per CU, on request): a part-empty last round of whole tiles
+# runs the last column blocks as a second launch of half-height tiles. Each output element
+# is the same fp32 chain in the same k order, so the result equals whole-tile execution bit
+# for bit, and both match the default 128-row tiling. The fused case cuts a segment.
 @pytest.mark.parametrize("fmt,xdt,M,Ns", [
     (O.INT4, O.F16, 2048, [27648]),         # 864 tiles: the last 12 of 108 blocks as 128-row tiles
     (O.TERNARY2, O.BF16, 3072, [27648]),
@@ -502,12 +503,15 @@ def test_prefill_tail_equals_whole_tiles(cuda, fmt, xdt, M, Ns):
         p.X = probs[0].X
     devs = [DeviceProblem(p) for p in probs]
     segs = [(d.Wp, d.S, d.P.N) for d in devs]
-    outs = hq.gemm_fused(fmt, devs[0].X, segs)
-    with prefill_env(SK=0, TAIL=0):
+    with prefill_env(WM=2):
+        outs = hq.gemm_fused(fmt, devs[0].X, segs)
+    with prefill_env(WM=2, SK=0, TAIL=0):
         whole = hq.gemm_fused(fmt, devs[0].X, segs)
+    default = hq.gemm_fused(fmt, devs[0].X, segs)
     rows = np.sort(np.random.default_rng(M).choice(M, size=8, replace=False))
-    for d, y, w in zip(devs, outs, whole):
+    for d, y, w, y128 in zip(devs, outs, whole, default):
         assert torch_equal(y, w)
+        assert torch_equal(y, y128)
         err = O.normwise_error(to_host_f32(y)[rows], d.P.reference(rows=rows, threads=16))
         assert err <= OUT_TOL[xdt]
 
