@@ -60,12 +60,12 @@ def test_workspace_bytes():
     assert b16 > b1 > 0 and b16 % 256 == 0 and b1 % 256 == 0
     assert (b16 - 65536) == 16 * (b1 - 65536)  # fixed 64 KiB counter area, then M-row partial tiles
     # Prefill shapes report one bound for every N: the counter area plus two fp32 tiles
-    # (64 rows up to M = 64, 256 rows from M = 129) per concurrent workgroup; K < 1024
+    # (64 rows up to M = 64, 128 rows from M = 65) per concurrent workgroup; K < 1024
     # is never split along K and needs none.
     st, p17 = workspace_bytes(hq.FORMAT_INT4, 17, 4096, 4096)
     _, p2048 = workspace_bytes(hq.FORMAT_TERNARY2, 2048, 5120, 27648)
     assert st == hq.HQ_OK and p17 > 65536 and (p17 - 65536) % (2 * 64 * 256 * 4) == 0
-    assert p2048 - 65536 == 4 * (p17 - 65536)
+    assert p2048 > p17 and (p2048 - 65536) % (2 * 128 * 256 * 4) == 0
     assert workspace_bytes(hq.FORMAT_TERNARY2, 2048, 5120, 16) == (hq.HQ_OK, p2048)
     assert workspace_bytes(hq.FORMAT_INT4, 2048, 896, 4096) == (hq.HQ_OK, 0)
     # Bad shapes are reported, not sized.
