@@ -154,8 +154,11 @@ __global__ void __launch_bounds__(64 * KG * GW) hq_decode_ls_kernel(const GemmDe
   void* const sY = d.seg[si].Y;
   const uint32_t sN = d.seg[si].N, sLds = d.seg[si].lds, sNt = d.seg[si].ntiles;
   const uint32_t sLdy = (uint32_t)d.seg[si].ldy;
-  const uint32_t ctw = (g - d.seg[si].blk_begin) * (GW * T) + wi * T;  // first tile of this wavefront
-  const uint32_t ntw = ctw < sNt ? min((uint32_t)T, sNt - ctw) : 0u;
+  // First tile of this wavefront, and how many of its T tiles it owns (the slab may be
+  // narrower than GW * T tiles, and the segment's last slab narrower still).
+  const uint32_t ctw = (g - d.seg[si].blk_begin) * pl.sw + wi * T;
+  const uint32_t own = wi * T < pl.sw ? min((uint32_t)T, pl.sw - wi * T) : 0u;
+  const uint32_t ntw = ctw < sNt ? min(own, sNt - ctw) : 0u;
   const uint32_t srow2 = sLds * 2u;  // bytes per scale row
   // k-blocks [ka, kz) of this piece; at step q k-group kg takes k-block ka + q * KG + kg.
   const uint32_t ka = piece * pl.kq + min(piece, pl.kr);
@@ -352,10 +355,11 @@ __global__ void __launch_bounds__(64 * KG * GW) hq_decode_ls_kernel(const GemmDe
 #pragma unroll
     for (int t = 0; t < T; ++t) {
       const uint32_t col = (ctw + t) * 16u + c16;
+      const bool mine = (uint32_t)t < ntw && col < sN;  // tiles past ntw belong to the next slab
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const uint32_t row = 4u * g4 + r;
-        const uint32_t o = row < M && col < sN ? (row * sLdy + col) * 2u : kOutOfRange;
+        const uint32_t o = row < M && mine ? (row * sLdy + col) * 2u : kOutOfRange;
         __builtin_amdgcn_raw_buffer_store_b16(f32_to_out<DT>(v[t][r]), yr, o, 0, 0);
       }
     }
@@ -428,7 +432,9 @@ uint32_t ls_assign_slabs(GemmDesc& d, uint32_t sw) {
 template <int FMT, int DT, int KG, int GW, int T, int U>
 hipError_t ls_launch_t(GemmDesc d, const LsConfig& c, void* ws, hipStream_t stream) {
   LsPlan pl{};
-  const uint32_t G = ls_assign_slabs(d, GW * T);
+  if (c.SW < 1 || c.SW > GW * T) return hipErrorInvalidValue;
+  pl.sw = (uint32_t)c.SW;
+  const uint32_t G = ls_assign_slabs(d, pl.sw);
   pl.S = (uint32_t)c.S;
   pl.kq = d.nkb / pl.S;
   pl.kr = d.nkb % pl.S;
@@ -464,16 +470,16 @@ hipError_t ls_launch_fd(const GemmDesc& d, const LsConfig& c, void* ws, hipStrea
 
 }  // namespace
 
-// Lockstep tiling: KG k-groups of four wavefronts, T tiles per wavefront (slabs of 4 T
-// tiles), ring depth U, and S pieces per slab chosen so that the grid covers the CUs.
-// HQ_DECODE_LS_KG / _T / _U / _S override (tuning and tests).
+// Lockstep tiling: KG k-groups of four wavefronts, T tiles per wavefront (slabs of up to
+// 4 T tiles), ring depth U, and S pieces per slab chosen so that the grid covers the CUs.
+// HQ_DECODE_LS_KG / _T / _U / _S / _SW override (tuning and tests).
 LsConfig choose_decode_ls(int fmt, const GemmDesc& d) {
   (void)fmt;
   const uint32_t cus = (uint32_t)cu_count();
   // Measured on MI355X (27B-class shapes, M = 4..16): two k-groups of four wavefronts,
   // two tiles per wavefront, two steps in flight; a K split only when the slabs alone
   // leave more than a quarter of the CUs idle.
-  LsConfig c{2, 2, 1, 2, 4};
+  LsConfig c{2, 2, 1, 2, 4, 0};
   const int eKG = ls_env("HQ_DECODE_LS_KG", 0);
   if (eKG == 1 || eKG == 2 || eKG == 4) c.KG = eKG;
   const int eT = ls_env("HQ_DECODE_LS_T", 0);
@@ -487,19 +493,24 @@ LsConfig choose_decode_ls(int fmt, const GemmDesc& d) {
   if (c.KG == 2 && c.T == 4) c.U = 2;
   if (c.KG == 4) { c.T = std::min(c.T, 2); c.U = c.T == 1 ? 3 : std::min(c.U, 3); }
   GemmDesc x = d;
-  const uint32_t G = ls_assign_slabs(x, c.GW * c.T);
+  c.SW = c.GW * c.T;
+  const uint32_t G = ls_assign_slabs(x, (uint32_t)c.SW);
   if (G < cus * 3 / 4) c.S = (int)std::max<uint32_t>(1, std::min<uint32_t>(d.nkb, (cus * 15 / 16 + G - 1) / G));
+  // Narrower slabs that would cover every CU measured slower (5120 x 27648, M = 1..16:
+  // 247 slabs of 7 tiles 2-15% behind 216 of 8), so slabs stay GW * T tiles wide.
+  const int eSW = ls_env("HQ_DECODE_LS_SW", 0);
+  if (eSW >= 1 && eSW <= c.GW * c.T) c.SW = eSW;
   const int eS = ls_env("HQ_DECODE_LS_S", 0);
   if (eS >= 1) c.S = eS;
   c.S = std::max(1, std::min<int>({c.S, (int)d.nkb, (int)kMaxPieces}));
-  if (c.S > 1 && G > kMaxCounters) c.S = 1;
+  if (c.S > 1 && ls_assign_slabs(x, (uint32_t)c.SW) > kMaxCounters) c.S = 1;
   return c;
 }
 
 size_t decode_ls_workspace_bytes(const GemmDesc& d, const LsConfig& c) {
   if (c.S <= 1) return 0;
   GemmDesc x = d;
-  const uint32_t G = ls_assign_slabs(x, c.GW * c.T);
+  const uint32_t G = ls_assign_slabs(x, (uint32_t)c.SW);
   return kCounterBytes + (size_t)G * c.S * c.GW * c.T * 1024u;
 }
 

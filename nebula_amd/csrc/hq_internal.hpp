@@ -61,14 +61,16 @@ struct LsConfig {
   int U;   // steps in flight per wavefront (register ring depth)
   int S;   // pieces (workgroups) per slab along K
   int KG;  // k-groups per workgroup (1, 2 or 4)
-  int GW;  // wavefronts per k-group (2 or 4); a slab is GW * T tiles
+  int GW;  // wavefronts per k-group (2 or 4)
+  int SW;  // tiles per slab, at most GW * T (wavefront i takes tiles T i .. min(T i + T, SW) - 1)
 };
 struct LsPlan {
+  uint32_t sw;      // tiles per slab
   uint32_t S;       // pieces per slab
   uint32_t kq, kr;  // piece p covers k-blocks [p * kq + min(p, kr), ...) of kq (+1 if p < kr)
   uint32_t gmul;    // plan_gmul(gkb)
   uint32_t* cnt;    // [G] arrival counters, zero between launches (S > 1)
-  float* part;      // [G][S][4 * T tiles][64 lanes] f4 partial tiles (S > 1)
+  float* part;      // [G][S][GW * T tiles][64 lanes] f4 partial tiles (S > 1)
 };
 LsConfig choose_decode_ls(int fmt, const GemmDesc& d);
 size_t decode_ls_workspace_bytes(const GemmDesc& d, const LsConfig& c);

@@ -73,6 +73,8 @@ struct PrefillPlan {
   uint32_t L, rem;  // stream-K ranges: begin(s) = s * L + min(s, rem)
   uint32_t nkb_m;   // plan_div_magic(nkb)
   uint32_t nb;      // 256-column blocks over all segments (tile = row band * nb + block)
+  uint32_t bands;   // row bands (tiles = bands * nb)
+  uint32_t gb;      // whole tiles are visited in groups of gb row bands, column-block major
   float* part;      // [psk][2][tile] fp32 partial tiles (null when psk == 0)
   uint32_t* cnt;    // [tiles - dp] arrival counters, zero between launches
 };

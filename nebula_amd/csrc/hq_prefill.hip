@@ -273,9 +273,18 @@ __global__ void __launch_bounds__(256 * WM, WM == 1 && RT == 8 ? 2 : 1) hq_prefi
 
   if constexpr (!SKP) {
     // Whole tiles, renumbered so that each XCD (consecutive workgroup ids go round-robin
-    // over the 8 XCDs) owns a contiguous range of tiles, row-block major, and keeps its
-    // activation rows resident in its own L2.
-    const uint32_t tile = pp.xcd ? (bid % 8u) * (pp.dp / 8u) + bid / 8u : bid;
+    // over the 8 XCDs) owns a contiguous range of the visiting order, and visited in groups
+    // of gb row bands (4 by default), column-block major inside a group: an XCD keeps the
+    // group's activation rows near (its L2 and the MALL), and the gb tiles of one column
+    // block run at about the same time, so their weight reads after the first hit L2.
+    uint32_t tile = pp.xcd ? (bid % 8u) * (pp.dp / 8u) + bid / 8u : bid;
+    if (pp.gb > 1u) {
+      const uint32_t span = pp.gb * pp.nb;
+      const uint32_t g = tile / span, r = tile - g * span;
+      const uint32_t nbg = min(pp.gb, pp.bands - g * pp.gb);  // bands in this group
+      const uint32_t cb = r / nbg;
+      tile = (g * pp.gb + (r - cb * nbg)) * pp.nb + cb;
+    }
     uint32_t s, m0, ct0;
     tile_geom<BM>(d, pp.nb, tile, wn, s, m0, ct0);
     run_piece(s, m0, ct0, 0u, nkb);
@@ -412,6 +421,8 @@ uint32_t assign_blocks(GemmDesc& d) {
   return nb;
 }
 
+int env_int(const char* name, int dflt);
+
 template <int FMT, int DT, int RT, int WM>
 hipError_t launch_rt(const PrefillLaunch& c, void* ws, hipStream_t stream) {
   constexpr uint32_t BM = 16u * RT * WM;
@@ -422,6 +433,9 @@ hipError_t launch_rt(const PrefillLaunch& c, void* ws, hipStream_t stream) {
   pp.psk = c.psk;
   pp.dp = c.dp;
   pp.xcd = c.dp % 8u == 0u ? 1u : 0u;
+  pp.bands = (d.M + BM - 1) / BM;
+  // Band groups reorder whole-tile launches only (every tile of the launch is whole).
+  pp.gb = c.dp == pp.bands * pp.nb ? (uint32_t)std::max(1, env_int("HQ_PREFILL_GB", 4)) : 1u;
   pp.nkb_m = plan_div_magic(d.nkb);
   if (c.psk) {
     if (!ws) return hipErrorInvalidValue;

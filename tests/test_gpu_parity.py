@@ -406,6 +406,19 @@ def test_lockstep_configs_int4(cuda, KG, T, U, S, M):
     check(y, P.reference(), O.F16, f"KG={KG} T={T} U={U} S={S} M={M}", P)
 
 
+# Slabs narrower than GW * T tiles (SW): the last wavefronts own fewer tiles or none, and the
+# tiles past a slab belong to the next one (they must read zero and never be stored).
+@pytest.mark.parametrize("KG,T,U,S,SW", [(2, 2, 2, 1, 7), (2, 2, 2, 1, 5), (2, 2, 3, 3, 7), (2, 4, 2, 1, 13),
+                                         (4, 2, 2, 2, 3), (2, 1, 4, 1, 3), (1, 2, 4, 1, 6)])
+@pytest.mark.parametrize("M", [4, 16])
+def test_lockstep_narrow_slabs(cuda, KG, T, U, S, SW, M):
+    P = O.Problem(O.INT4, M, 2048, 1000, 128, O.F16, seed=3050 + M + SW)
+    D = DeviceProblem(P)
+    with decode_env(KERNEL=1, LS_KG=KG, LS_T=T, LS_U=U, LS_S=S, LS_SW=SW):
+        y = D.run()
+    check(y, P.reference(), O.F16, f"KG={KG} T={T} U={U} S={S} SW={SW} M={M}", P)
+
+
 @pytest.mark.parametrize("fmt,xdt", [(O.INT4, O.BF16), (O.TERNARY2, O.F16), (O.TERNARY2, O.BF16)])
 @pytest.mark.parametrize("KG,T,U,S", [(2, 2, 2, 1), (2, 2, 2, 3), (4, 2, 3, 2), (2, 1, 4, 1), (1, 2, 4, 2)])
 def test_lockstep_formats(cuda, fmt, xdt, KG, T, U, S):
@@ -417,18 +430,18 @@ def test_lockstep_formats(cuda, fmt, xdt, KG, T, U, S):
     check(y, P.reference(), xdt, f"fmt={fmt} KG={KG} T={T} U={U} S={S}", P)
 
 
-@pytest.mark.parametrize("S", [1, 3])
-def test_lockstep_fused(cuda, S):
+@pytest.mark.parametrize("S,SW", [(1, 0), (3, 0), (1, 7), (2, 5)])
+def test_lockstep_fused(cuda, S, SW):
     # Slabs never straddle segments; each segment's last slab is partial.
     Ns, K, M = [600, 130, 1000], 1024, 6
     probs = [O.Problem(O.INT4, M, K, n, 128, O.F16, seed=3200 + i) for i, n in enumerate(Ns)]
     for p in probs[1:]:
         p.X = probs[0].X
     devs = [DeviceProblem(p) for p in probs]
-    with decode_env(KERNEL=1, LS_S=S):
+    with decode_env(KERNEL=1, LS_S=S, **({"LS_SW": SW} if SW else {})):
         outs = hq.gemm_fused(O.INT4, devs[0].X, [(d.Wp, d.S, d.P.N) for d in devs])
     for d, y in zip(devs, outs):
-        check(y, d.P.reference(), O.F16, f"lockstep fused S={S} N={d.P.N}", d.P)
+        check(y, d.P.reference(), O.F16, f"lockstep fused S={S} SW={SW} N={d.P.N}", d.P)
 
 
 @pytest.mark.parametrize("M", [4, 16])
