@@ -588,9 +588,13 @@ PrefillConfig choose_prefill(int fmt, const GemmDesc& d) {
     }
   }
   // Part-empty last rounds of 128-row tiles (two per CU) cost little: a lone workgroup has
-  // its CU to itself. Only 256-row tiles get the half-height tail launch.
+  // its CU to itself. Measured on MI355X (M = 1024, 2048, 4096 at N = 27648) and slower
+  // than whole tiles: 64-row tail tiles (their dequantisation is shared by half as many
+  // rows) and a stream-K launch over the last round's tiles (its partial-tile traffic).
+  // Only 256-row tiles get the half-height tail launch.
   const uint32_t r = l.tiles % slots;
-  if (env_int("HQ_PREFILL_TAIL", 1) == 0 || r == 0u || WM == 1) return c;
+  if (WM == 1) return c;
+  if (env_int("HQ_PREFILL_TAIL", 1) == 0 || r == 0u) return c;
   const int hRT = RT * WM / 2;  // half-height tiles of one row wave: 256 -> 128, 128 -> 64 rows
   const uint32_t bands = (d.M + 16u * RT * WM - 1) / (16u * RT * WM);
   const uint32_t nb = count_blocks(d);
