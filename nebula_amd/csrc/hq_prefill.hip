@@ -474,9 +474,12 @@ int env_int(const char* name, int dflt) {
 // (two row waves, one workgroup per CU) by 3-8% from M = 512 to 4096.
 void prefill_shape(uint32_t M, int& RT, int& WM) {
   const int eWM = env_int("HQ_PREFILL_WM", 0);  // tuning override: 128 (1) or 256 (2) rows
-  const int eRT = env_int("HQ_PREFILL_RT", 0);  // tuning override: 16 = 256 rows, one row wave
+  const int eRT = env_int("HQ_PREFILL_RT", 0);  // tuning override: 4 = 64 rows, 16 = 256 rows, one row wave
   if (eRT == 16 && M > 128) {
     RT = 16;
+    WM = 1;
+  } else if (eRT == 4) {
+    RT = 4;
     WM = 1;
   } else if (eWM == 1 || eWM == 2) {
     RT = 8;
@@ -572,6 +575,16 @@ PrefillConfig choose_prefill(int fmt, const GemmDesc& d) {
   PrefillConfig c{};
   int RT = 8, WM = 2;
   prefill_shape(d.M, RT, WM);
+  // 128-row tiles too few for the slots would be split along K; when those pieces would be
+  // short (under 64 k-blocks) 64-row tiles do better: twice the tiles, split half as often
+  // or not at all. Measured on MI355X: fused QKV (N = 7168) M = 256..1024 7-38% faster,
+  // K = 27648 x N = 5120 at M = 256 17% faster; with long pieces (K = 27648, M = 1024) the
+  // 128-row split stays (64-row tiles there: 40% slower).
+  if (RT == 8 && WM == 1 && env_int("HQ_PREFILL_RT", 0) == 0 && env_int("HQ_PREFILL_WM", 0) == 0) {
+    const uint32_t t128 = make_launch(8, 1, d).tiles, s128 = (uint32_t)prefill_slots(fmt, 8, 1);
+    const uint32_t split = std::min<uint32_t>(s128 / std::max(t128, 1u), d.nkb / 4u);
+    if (split >= 2u && d.nkb / split < 64u) RT = 4;
+  }
   c.n = 1;
   c.l[0] = make_launch(RT, WM, d);
   PrefillLaunch& l = c.l[0];
@@ -622,7 +635,10 @@ size_t prefill_workspace_bound(int fmt, uint32_t M, uint32_t nkb) {
   if (env_int("HQ_PREFILL_SK", 1) == 0 || nkb < 8u) return 0;
   int RT = 8, WM = 2;
   prefill_shape(M, RT, WM);
-  return kCounterBytes + (size_t)prefill_slots(fmt, RT, WM) * 2u * (16u * RT * WM) * 256u * sizeof(float);
+  size_t b = (size_t)prefill_slots(fmt, RT, WM) * 2u * (16u * RT * WM) * 256u * sizeof(float);
+  if (RT == 8 && WM == 1)  // choose_prefill may take 64-row tiles instead
+    b = std::max(b, (size_t)prefill_slots(fmt, 4, 1) * 2u * 64u * 256u * sizeof(float));
+  return kCounterBytes + b;
 }
 
 hipError_t launch_prefill(int fmt, int dtype, const PrefillConfig& c, void* ws, hipStream_t stream) {

@@ -476,7 +476,8 @@ def normwise_between(a, b):
 # normwise) and be bit-reproducible.
 @pytest.mark.parametrize("fmt,xdt,M,K,N,psk", [
     (O.TERNARY2, O.BF16, 512, 5120, 27648, 432),  # all 216 tiles split 2 ways (forced)
-    (O.INT4, O.F16, 256, 5120, 27648, 0),         # 108 tiles split 2 ways
+    (O.INT4, O.F16, 256, 27648, 5120, 0),         # 80 64-row tiles split 6 ways (short pieces)
+    (O.INT4, O.F16, 1024, 27648, 5120, 0),        # 160 128-row tiles split 3 ways (72 k-blocks each)
     (O.INT4, O.BF16, 40, 4096, 4096, 0),          # 64-row tiles, 16 tiles split 8 ways
     (O.TERNARY2, O.F16, 200, 2048, 3000, 0),
     (O.INT4, O.F16, 129, 1024, 700, 0),
