@@ -281,7 +281,41 @@ def run_gpu(args):
            "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
     log(f"TQ1_0 import K={K} N={N}: {us:.1f} us, {gbs:.1f} GB/s")
     del blocks, outs
-    return value, ms_per_step, roofline, cases, prefill, tq1
+
+    # ---- the reference decoder's layer projections (attention layer + FFN) as fused calls ----
+    from nebula_amd import decoder as dec
+
+    g = torch.Generator(device="cuda").manual_seed(11)
+    layer = dec.random_layer("attention", generator=g)
+    names = [n for grp in dec.FUSED_GROUPS["attention"] + dec.FUSED_GROUPS["ffn"] for n in grp]
+    wbytes_layer = sum(hq.packed_words(hq.FORMAT_TERNARY2, *dec.SHAPES[n]) * 4 + (dec.SHAPES[n][0] // 256) *
+                       dec.SHAPES[n][1] * 2 for n in names)
+    flops_row = sum(2 * dec.SHAPES[n][0] * dec.SHAPES[n][1] for n in names)
+    layer_res = {"weight_bytes": wbytes_layer}
+    for M in (1, 16, 80, 512):
+        xs = torch.randn((M, dec.EMBEDDING), device="cuda", generator=g).half()
+        ys = torch.randn((M, dec.MIXER_IN), device="cuda", generator=g).half()
+        acts = torch.randn((M, dec.FFN), device="cuda", generator=g).half()
+        o_in = [torch.empty((M, dec.SHAPES[n][1]), device="cuda", dtype=torch.float16) for n in ("attn_q", "attn_k", "attn_v")]
+        o_ffn = [torch.empty((M, dec.FFN), device="cuda", dtype=torch.float16) for _ in range(2)]
+        o_x = torch.empty((M, dec.EMBEDDING), device="cuda", dtype=torch.float16)
+
+        def launches(xs=xs, ys=ys, acts=acts, o_in=o_in, o_ffn=o_ffn, o_x=o_x):
+            for _ in range(4):
+                layer.mixer_in(xs, outs=o_in)
+                layer.mixer_out(ys, out=o_x)
+                layer.ffn_in(xs, outs=o_ffn)
+                layer.ffn_out(acts, out=o_x)
+            return 4
+
+        us = graph_time_us(torch, stream, launches)
+        layer_res[f"M{M}"] = {"us": round(us, 1), "GBps": round(wbytes_layer / (us * 1e-6) / 1e9, 1),
+                              "TFLOPs": round(M * flops_row / (us * 1e-6) / 1e12, 1)}
+        log(f"decoder layer projections M={M}: {us:.1f} us")
+    # Token-by-token prefill (the reference runs prompt tokens one at a time) against one call.
+    layer_res["prefill_512_speedup_vs_token_by_token"] = round(512 * layer_res["M1"]["us"] / layer_res["M512"]["us"], 1)
+    del layer
+    return value, ms_per_step, roofline, cases, prefill, tq1, layer_res
 
 
 def run_cpu(budget_s: float = 10.0):
@@ -342,7 +376,7 @@ def main():
         else:
             run_roofline_only(torch, hq)
         return
-    value, ms_per_step, roofline, cases, prefill, tq1 = run_gpu(args)
+    value, ms_per_step, roofline, cases, prefill, tq1, layer_res = run_gpu(args)
     cpu = None if args.no_cpu else run_cpu(args.cpu_budget)
     out = {
         "metric": "qGEMM GB/s at M<=16 (% of HBM peak) + TFLOP/s at M=2048 (% MFMA peak)",
@@ -365,6 +399,7 @@ def main():
         "cpu_baseline": cpu,
         "prefill": prefill,
         "tq1_0_import": tq1,
+        "decoder_layer": layer_res,
         "cases": cases,
     }
     print(json.dumps(out), flush=True)

@@ -123,10 +123,26 @@ hq_status get_internal_ws(hipStream_t stream, size_t need, void** out) {
 // from four rows on, the lockstep kernel (hq_decode_ls.hip), which fetches each activation
 // k-block once per workgroup, is (measured on MI355X over the 27B-class decode shapes).
 // HQ_DECODE_KERNEL=0 / 1 forces one of them (tuning and tests).
-bool use_lockstep(uint32_t M) {
+// With ternary weights the lockstep kernel's four-k-group configuration is faster from
+// one row on (5120 x 27648 at M = 1: 12.8 us against 14.7 us), so it is taken whenever the
+// lockstep planner picks it.
+bool use_lockstep(int fmt, const hq::GemmDesc& d) {
+  if (d.M > 16) return true;  // only the lockstep kernel takes several row tiles
   const char* v = std::getenv("HQ_DECODE_KERNEL");
   if (v && *v) return std::atoi(v) != 0;
-  return M >= 4;
+  if (d.M >= 4) return true;
+  return fmt == HQ_FORMAT_TERNARY2 && hq::choose_decode_ls(fmt, d).KG == 4;
+}
+
+// Rows up to which the streaming (decode) kernels run; the MFMA tile kernel above. The
+// lockstep kernel takes up to 16 * kLsMaxRowTiles rows: a split-fuse step (16 decode
+// tokens and a 64-token prefill chunk) stays a weight stream. HQ_DECODE_MAX_M overrides
+// (16 .. 80; tuning and tests).
+uint32_t decode_max_m() {
+  const char* v = std::getenv("HQ_DECODE_MAX_M");
+  const int e = v && *v ? std::atoi(v) : 0;
+  const uint32_t top = 16u * hq::kLsMaxRowTiles;
+  return e >= 16 && (uint32_t)e <= top ? (uint32_t)e : top;
 }
 
 // Validation shared by the GEMM entry points.
@@ -182,8 +198,8 @@ hq_status run_gemm(const void* X, hq_dtype dtype, int64_t ldx, hq_format fmt, co
     d.seg[i].ntiles = hq::col_tiles(segs[i].N);
   }
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const bool prefill = M > 16;
-  const bool lockstep = !prefill && use_lockstep(M);
+  const bool prefill = M > decode_max_m();
+  const bool lockstep = !prefill && use_lockstep(fmt, d);
   hq::LsConfig lc{};
   hq::DecodeConfig c{};
   hq::PrefillConfig pc{};
@@ -255,7 +271,7 @@ hq_status hq_workspace_bytes(hq_format fmt, uint32_t M, uint32_t K, uint32_t N, 
   if (M == 0 || N == 0 || K == 0 || K % hq::kBlockK || group == 0 || group % hq::kBlockK || K % group)
     return fail(HQ_ERR_SHAPE, "bad shape M=%u K=%u N=%u group=%u", M, K, N, group);
   *bytes = 0;
-  if (M > 16) {
+  if (M > decode_max_m()) {
     *bytes = hq::prefill_workspace_bound(fmt, M, K / hq::kBlockK);
     return ok();
   }
@@ -268,7 +284,7 @@ hq_status hq_workspace_bytes(hq_format fmt, uint32_t M, uint32_t K, uint32_t N, 
   d.seg[0].N = N;
   d.seg[0].lds = N;
   d.seg[0].ntiles = hq::col_tiles(N);
-  *bytes = use_lockstep(M) ? hq::decode_ls_workspace_bytes(d, hq::choose_decode_ls(fmt, d))
+  *bytes = use_lockstep(fmt, d) ? hq::decode_ls_workspace_bytes(d, hq::choose_decode_ls(fmt, d))
                           : hq::decode_workspace_bytes(d, hq::choose_decode(fmt, d));
   return ok();
 }

@@ -111,11 +111,12 @@ __device__ __forceinline__ void ls_tie(u4& a) { asm volatile("" : "+v"(a)); }
 __device__ __forceinline__ void ls_tie(u2& a) { asm volatile("" : "+v"(a)); }
 __device__ __forceinline__ void ls_tie(uint32_t& a) { asm volatile("" : "+v"(a)); }
 
-template <int FMT, int DT, int KG, int GW, int T, int U>
+template <int FMT, int DT, int KG, int GW, int T, int U, int MT>
 __global__ void __launch_bounds__(64 * KG * GW) hq_decode_ls_kernel(const GemmDesc d, const LsPlan pl) {
   static_assert(KG == 1 || KG == 2 || KG == 4, "one, two or four k-groups");
   static_assert(GW == 2 || GW == 4, "k-groups of two or four wavefronts");
   static_assert(T >= 1 && T <= 4, "the scale load covers at most four tiles");
+  static_assert(MT >= 1 && MT <= 5 && (4 * MT) % GW == 0, "one to five 16-row tiles, whole loads per wavefront");
   using WV = typename LsW<FMT>::V;
   constexpr uint32_t kLaneBytes = LsW<FMT>::kLaneBytes;
   constexpr uint32_t kBlockBytes = 64u * kLaneBytes;  // one tile x one k-block
@@ -126,10 +127,11 @@ __global__ void __launch_bounds__(64 * KG * GW) hq_decode_ls_kernel(const GemmDe
   // (and so finished reading it). A stage holds one k-block per k-group.
   constexpr int R = U + 1;
   constexpr int NS = 2;
-  constexpr int XL = 4 / GW;        // activation loads (four rows each) per wavefront and step
+  constexpr int XL = 4 * MT / GW;   // activation loads (four rows each) per wavefront and step
   constexpr int PER = XL + T + 1;  // loads per wavefront and step: activation rows, T tiles, scales
-  constexpr uint32_t kStep = KG * kStageBytes;
-  static_assert((KG - 1) * GW * T * 1024 <= NS * kStep, "the k-group reduction reuses the activation stages");
+  constexpr uint32_t kXStage = MT * kStageBytes;  // one k-group's activation k-block: 16 MT rows
+  constexpr uint32_t kStep = KG * kXStage;
+  static_assert((KG - 1) * GW * T * MT * 1024 <= NS * kStep, "the k-group reduction reuses the activation stages");
   __shared__ __attribute__((aligned(16))) char xs[NS * kStep];
   __shared__ uint32_t sh_last;
   __shared__ uint32_t kg_arrived[KG];  // per k-group arrival count (k-group barrier)
@@ -179,15 +181,16 @@ __global__ void __launch_bounds__(64 * KG * GW) hq_decode_ls_kernel(const GemmDe
   // bytes (rows >= M read zero) and writes it to LDS at row * 256 + 16 * (l % 16) of the
   // k-group's stage slot.
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(d.X, M * (uint32_t)d.ldx * 2u);
-  const uint32_t xs0 = (uint32_t)(uintptr_t)xs + kg * kStageBytes;
+  const uint32_t xs0 = (uint32_t)(uintptr_t)xs + kg * kXStage;
   uint32_t xvo[XL], xwo[XL];
 #pragma unroll
   for (int x = 0; x < XL; ++x) {
     const uint32_t xrow = 4u * (XL * wi + x) + g4;
-    xvo[x] = xrow < M ? xrow * (uint32_t)d.ldx * 2u + ((c16 ^ xrow) * 16u) : kOutOfRange;
+    xvo[x] = xrow < M ? xrow * (uint32_t)d.ldx * 2u + ((c16 ^ (xrow & 15u)) * 16u) : kOutOfRange;
     xwo[x] = xs0 + (XL * wi + x) * 1024u + lane * 16u;
   }
-  // A fragment of chunk c: row c16, 16-byte piece 4c + g4, at row * 256 + 16 * (piece ^ row).
+  // A fragment of row tile r, chunk c: row 16 r + c16, 16-byte piece 4c + g4, at
+  // r * 4096 + c16 * 256 + 16 * (piece ^ c16).
   uint32_t xro[4];
 #pragma unroll
   for (int c = 0; c < 4; ++c) xro[c] = xs0 + c16 * 256u + 16u * ((4u * c + g4) ^ c16);
@@ -212,51 +215,65 @@ __global__ void __launch_bounds__(64 * KG * GW) hq_decode_ls_kernel(const GemmDe
                               __builtin_amdgcn_readfirstlane(plan_group_of_kb(kbu, pl.gmul) * srow2));
   };
 
-  f4 acc[T];
+  f4 acc[MT][T];
 #pragma unroll
-  for (int t = 0; t < T; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
+  for (int r = 0; r < MT; ++r)
+#pragma unroll
+    for (int t = 0; t < T; ++t) acc[r][t] = f4{0.f, 0.f, 0.f, 0.f};
   const DqBiasConst dqb = DT == HQ_DTYPE_F16 ? dq_bias_const_f16() : dq_bias_const_bf16();
   const u4 corr_b = int4_corr_fragment<DT>();
 
   auto compute = [&](int slot, uint32_t stage) {
     const uint32_t so = stage * kStep;
-    u4 xf[4];
     uint32_t sb[T];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) xf[c] = ls_lds_read_b128(xro[c] + so);
-#pragma unroll
     for (int t = 0; t < T; ++t) sb[t] = T == 1 ? sring[slot] : ls_bpermute((16u * t + c16) * 4u, sring[slot]);
-    ls_wait_lgkmcnt0();
+    // The weight fragments of the k-block, dequantised once and used by every row tile.
+    u4 bf[4][T];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) ls_tie(xf[c]);
-#pragma unroll
-    for (int t = 0; t < T; ++t) ls_tie(sb[t]);
-    // Independent accumulation chains: one per tile and (int4) one for the bias
-    // correction -sum x (magic + 8), added after the chunk loop.
-    f4 corr = f4{0.f, 0.f, 0.f, 0.f}, gs[T];
-#pragma unroll
-    for (int t = 0; t < T; ++t) gs[t] = f4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      if constexpr (kInt4) corr = mfma16x16x32<DT>(xf[c], corr_b, corr);
+    for (int c = 0; c < 4; ++c)
 #pragma unroll
       for (int t = 0; t < T; ++t) {
-        u4 bf;
         if constexpr (kInt4) {
-          bf = dq_int4_biased<DT>(wring[slot][t][c], dqb);
+          bf[c][t] = dq_int4_biased<DT>(wring[slot][t][c], dqb);
         } else {
           const uint32_t word = wring[slot][t][c >> 1];
-          bf = (c & 1) ? dq_tern2<1>(word) : dq_tern2<0>(word);
+          bf[c][t] = (c & 1) ? dq_tern2<1>(word) : dq_tern2<0>(word);
         }
-        gs[t] = mfma16x16x32<DT>(xf[c], bf, gs[t]);
       }
-    }
+    float sc[T];
 #pragma unroll
-    for (int t = 0; t < T; ++t) {
-      float sc = f16_to_f32((uint16_t)sb[t]);
-      if constexpr (!kInt4) sc = __builtin_isfinite(sc) ? 0.5f * sc : 0.0f;  // fields hold 2t; non-finite drops
+    for (int r = 0; r < MT; ++r) {
+      u4 xf[4];
 #pragma unroll
-      for (int v = 0; v < 4; ++v) acc[t][v] = __builtin_fmaf(kInt4 ? gs[t][v] + corr[v] : gs[t][v], sc, acc[t][v]);
+      for (int c = 0; c < 4; ++c) xf[c] = ls_lds_read_b128(xro[c] + so + (uint32_t)r * kStageBytes);
+      ls_wait_lgkmcnt0();
+#pragma unroll
+      for (int c = 0; c < 4; ++c) ls_tie(xf[c]);
+      if (r == 0) {
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+          ls_tie(sb[t]);
+          sc[t] = f16_to_f32((uint16_t)sb[t]);
+          if constexpr (!kInt4) sc[t] = __builtin_isfinite(sc[t]) ? 0.5f * sc[t] : 0.0f;  // fields hold 2t; non-finite drops
+        }
+      }
+      // Independent accumulation chains: one per tile and (int4) one for the bias
+      // correction -sum x (magic + 8), added after the chunk loop.
+      f4 corr = f4{0.f, 0.f, 0.f, 0.f}, gs[T];
+#pragma unroll
+      for (int t = 0; t < T; ++t) gs[t] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        if constexpr (kInt4) corr = mfma16x16x32<DT>(xf[c], corr_b, corr);
+#pragma unroll
+        for (int t = 0; t < T; ++t) gs[t] = mfma16x16x32<DT>(xf[c], bf[c][t], gs[t]);
+      }
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int v = 0; v < 4; ++v)
+          acc[r][t][v] = __builtin_fmaf(kInt4 ? gs[t][v] + corr[v] : gs[t][v], sc[t], acc[r][t][v]);
     }
   };
 
@@ -337,35 +354,43 @@ __global__ void __launch_bounds__(64 * KG * GW) hq_decode_ls_kernel(const GemmDe
     float* red = reinterpret_cast<float*>(xs);
     if (!lead) {
 #pragma unroll
-      for (int t = 0; t < T; ++t)
-        *reinterpret_cast<f4*>(red + (((kg - 1u) * GW + wi) * T + t) * 256u + lane * 4u) = acc[t];
+      for (int r = 0; r < MT; ++r)
+#pragma unroll
+        for (int t = 0; t < T; ++t)
+          *reinterpret_cast<f4*>(red + ((((kg - 1u) * GW + wi) * T + t) * MT + r) * 256u + lane * 4u) = acc[r][t];
     }
     __syncthreads();
     if (lead) {
 #pragma unroll
       for (uint32_t k = 1; k < (uint32_t)KG; ++k)
 #pragma unroll
-        for (int t = 0; t < T; ++t) acc[t] += *reinterpret_cast<const f4*>(red + (((k - 1u) * GW + wi) * T + t) * 256u + lane * 4u);
+        for (int r = 0; r < MT; ++r)
+#pragma unroll
+          for (int t = 0; t < T; ++t)
+            acc[r][t] += *reinterpret_cast<const f4*>(red + ((((k - 1u) * GW + wi) * T + t) * MT + r) * 256u + lane * 4u);
     }
   }
 
-  // Output: lane holds rows 4 g4 + v of column 16 (ctw + t) + c16.
+  // Output: lane holds rows 16 r + 4 g4 + v of column 16 (ctw + t) + c16.
   const __amdgpu_buffer_rsrc_t yr = make_rsrc(sY, M * sLdy * 2u);
-  auto store_out = [&](const f4* v) {
+  auto store_out = [&](int r, const f4* v) {  // row tile r
 #pragma unroll
     for (int t = 0; t < T; ++t) {
       const uint32_t col = (ctw + t) * 16u + c16;
       const bool mine = (uint32_t)t < ntw && col < sN;  // tiles past ntw belong to the next slab
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const uint32_t row = 4u * g4 + r;
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t row = 16u * r + 4u * g4 + e;
         const uint32_t o = row < M && mine ? (row * sLdy + col) * 2u : kOutOfRange;
-        __builtin_amdgcn_raw_buffer_store_b16(f32_to_out<DT>(v[t][r]), yr, o, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b16(f32_to_out<DT>(v[t][e]), yr, o, 0, 0);
       }
     }
   };
   if (pl.S == 1) {
-    if (lead) store_out(acc);
+    if (lead) {
+#pragma unroll
+      for (int r = 0; r < MT; ++r) store_out(r, acc[r]);
+    }
     return;
   }
 
@@ -374,14 +399,18 @@ __global__ void __launch_bounds__(64 * KG * GW) hq_decode_ls_kernel(const GemmDe
   // order. Waiting for the stores before the barrier orders them before the count.
   constexpr int kCoherent = 16;
   const uint32_t pieces = pl.S;
-  constexpr uint32_t kTilesWg = GW * T;
+  constexpr uint32_t kTilesWg = GW * T * MT;  // 16 x 16 fp32 tiles per workgroup
   const __amdgpu_buffer_rsrc_t partr = make_rsrc(pl.part, gridDim.y * pieces * kTilesWg * 1024u);
-  auto part_off = [&](uint32_t p, int t) {
-    return 4u * g4 < M ? (((g * pieces + p) * kTilesWg + wi * T + t) * 64u + lane) * 16u : kOutOfRange;
+  auto part_off = [&](uint32_t p, int r, int t) {
+    return 16u * r + 4u * g4 < M ? (((g * pieces + p) * kTilesWg + (wi * T + t) * MT + r) * 64u + lane) * 16u
+                                 : kOutOfRange;
   };
   if (lead) {
 #pragma unroll
-    for (int t = 0; t < T; ++t) __builtin_amdgcn_raw_buffer_store_b128(acc[t], partr, part_off(piece, t), 0, kCoherent);
+    for (int r = 0; r < MT; ++r)
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+        __builtin_amdgcn_raw_buffer_store_b128(acc[r][t], partr, part_off(piece, r, t), 0, kCoherent);
   }
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
   __syncthreads();
@@ -393,24 +422,29 @@ __global__ void __launch_bounds__(64 * KG * GW) hq_decode_ls_kernel(const GemmDe
   }
   __syncthreads();
   if (!sh_last || !lead) return;
-  // Every piece's partial is loaded at once (a loop that waited for each piece before
-  // loading the next cost one memory round trip per piece), then summed in piece order.
-  f4 part[kMaxPieces][T];
+  // Every piece's partial of a row tile is loaded at once (a loop that waited for each
+  // piece before loading the next cost one memory round trip per piece), then summed in
+  // piece order.
 #pragma unroll
-  for (uint32_t p = 0; p < kMaxPieces; ++p)
-#pragma unroll
-    for (int t = 0; t < T; ++t)
-      part[p][t] = p < pieces && p != piece ? __builtin_amdgcn_raw_buffer_load_b128(partr, part_off(p, t), 0, kCoherent)
-                                            : acc[t];
-  f4 sum[T];
-#pragma unroll
-  for (int t = 0; t < T; ++t) {
-    sum[t] = f4{0.f, 0.f, 0.f, 0.f};
+  for (int r = 0; r < MT; ++r) {
+    f4 part[kMaxPieces][T];
 #pragma unroll
     for (uint32_t p = 0; p < kMaxPieces; ++p)
-      if (p < pieces) sum[t] += part[p][t];
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+        part[p][t] = p < pieces && p != piece
+                         ? __builtin_amdgcn_raw_buffer_load_b128(partr, part_off(p, r, t), 0, kCoherent)
+                         : acc[r][t];
+    f4 sum[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      sum[t] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (uint32_t p = 0; p < kMaxPieces; ++p)
+        if (p < pieces) sum[t] += part[p][t];
+    }
+    store_out(r, sum);
   }
-  store_out(sum);
 }
 
 int ls_env(const char* name, int dflt) {
@@ -429,8 +463,9 @@ uint32_t ls_assign_slabs(GemmDesc& d, uint32_t sw) {
   return g;
 }
 
-template <int FMT, int DT, int KG, int GW, int T, int U>
+template <int FMT, int DT, int KG, int GW, int T, int U, int MT>
 hipError_t ls_launch_t(GemmDesc d, const LsConfig& c, void* ws, hipStream_t stream) {
+  if (d.M > 16u * MT) return hipErrorInvalidValue;
   LsPlan pl{};
   if (c.SW < 1 || c.SW > GW * T) return hipErrorInvalidValue;
   pl.sw = (uint32_t)c.SW;
@@ -446,24 +481,35 @@ hipError_t ls_launch_t(GemmDesc d, const LsConfig& c, void* ws, hipStream_t stre
   }
   // Byte offsets into X, Y and the partials are 32-bit buffer offsets.
   const uint64_t xbytes = (uint64_t)d.M * (uint64_t)d.ldx * 2u;
-  bool fits = G >= 1 && G <= 65535 && xbytes < (1ull << 31) && (uint64_t)G * pl.S * GW * T * 1024u < (1ull << 31);
+  bool fits = G >= 1 && G <= 65535 && xbytes < (1ull << 31) && (uint64_t)G * pl.S * GW * T * MT * 1024u < (1ull << 31);
   for (uint32_t i = 0; i < d.nseg; ++i) fits = fits && (uint64_t)d.M * (uint64_t)d.seg[i].ldy * 2u < (1ull << 31);
   if (!fits) return hipErrorInvalidValue;
-  hipLaunchKernelGGL((hq_decode_ls_kernel<FMT, DT, KG, GW, T, U>), dim3(pl.S, G), dim3(64 * KG * GW), 0, stream, d, pl);
+  hipLaunchKernelGGL((hq_decode_ls_kernel<FMT, DT, KG, GW, T, U, MT>), dim3(pl.S, G), dim3(64 * KG * GW), 0, stream, d,
+                     pl);
   return hipGetLastError();
 }
 
 template <int FMT, int DT>
 hipError_t ls_launch_fd(const GemmDesc& d, const LsConfig& c, void* ws, hipStream_t stream) {
+  if (c.MT > 1) {  // several row tiles: two k-groups of four wavefronts, two tiles each, two steps in flight
+    if (c.GW * 1000 + c.KG * 100 + c.T * 10 + c.U != 4222) return hipErrorInvalidConfiguration;
+    switch (c.MT) {
+      case 2: return ls_launch_t<FMT, DT, 2, 4, 2, 2, 2>(d, c, ws, stream);
+      case 3: return ls_launch_t<FMT, DT, 2, 4, 2, 2, 3>(d, c, ws, stream);
+      case 4: return ls_launch_t<FMT, DT, 2, 4, 2, 2, 4>(d, c, ws, stream);
+      case 5: return ls_launch_t<FMT, DT, 2, 4, 2, 2, 5>(d, c, ws, stream);
+      default: return hipErrorInvalidConfiguration;
+    }
+  }
   switch (c.GW * 1000 + c.KG * 100 + c.T * 10 + c.U) {
-    case 4124: return ls_launch_t<FMT, DT, 1, 4, 2, 4>(d, c, ws, stream);
-    case 4214: return ls_launch_t<FMT, DT, 2, 4, 1, 4>(d, c, ws, stream);
-    case 4222: return ls_launch_t<FMT, DT, 2, 4, 2, 2>(d, c, ws, stream);
-    case 4223: return ls_launch_t<FMT, DT, 2, 4, 2, 3>(d, c, ws, stream);
-    case 4242: return ls_launch_t<FMT, DT, 2, 4, 4, 2>(d, c, ws, stream);
-    case 4413: return ls_launch_t<FMT, DT, 4, 4, 1, 3>(d, c, ws, stream);
-    case 4422: return ls_launch_t<FMT, DT, 4, 4, 2, 2>(d, c, ws, stream);
-    case 4423: return ls_launch_t<FMT, DT, 4, 4, 2, 3>(d, c, ws, stream);
+    case 4124: return ls_launch_t<FMT, DT, 1, 4, 2, 4, 1>(d, c, ws, stream);
+    case 4214: return ls_launch_t<FMT, DT, 2, 4, 1, 4, 1>(d, c, ws, stream);
+    case 4222: return ls_launch_t<FMT, DT, 2, 4, 2, 2, 1>(d, c, ws, stream);
+    case 4223: return ls_launch_t<FMT, DT, 2, 4, 2, 3, 1>(d, c, ws, stream);
+    case 4242: return ls_launch_t<FMT, DT, 2, 4, 4, 2, 1>(d, c, ws, stream);
+    case 4413: return ls_launch_t<FMT, DT, 4, 4, 1, 3, 1>(d, c, ws, stream);
+    case 4422: return ls_launch_t<FMT, DT, 4, 4, 2, 2, 1>(d, c, ws, stream);
+    case 4423: return ls_launch_t<FMT, DT, 4, 4, 2, 3, 1>(d, c, ws, stream);
     default: return hipErrorInvalidConfiguration;
   }
 }
@@ -474,19 +520,19 @@ hipError_t ls_launch_fd(const GemmDesc& d, const LsConfig& c, void* ws, hipStrea
 // 4 T tiles), ring depth U, and S pieces per slab chosen so that the grid covers the CUs.
 // HQ_DECODE_LS_KG / _T / _U / _S / _SW override (tuning and tests).
 LsConfig choose_decode_ls(int fmt, const GemmDesc& d) {
-  (void)fmt;
   const uint32_t cus = (uint32_t)cu_count();
   // Measured on MI355X (27B-class shapes, M = 4..16): two k-groups of four wavefronts,
   // two tiles per wavefront, two steps in flight; a K split only when the slabs alone
   // leave more than a quarter of the CUs idle.
-  LsConfig c{2, 2, 1, 2, 4, 0};
+  LsConfig c{2, 2, 1, 2, 4, 0, (int)std::min<uint32_t>(kLsMaxRowTiles, (d.M + 15u) / 16u)};
   const int eKG = ls_env("HQ_DECODE_LS_KG", 0);
   if (eKG == 1 || eKG == 2 || eKG == 4) c.KG = eKG;
   const int eT = ls_env("HQ_DECODE_LS_T", 0);
   if (eT == 1 || eT == 2 || eT == 4) c.T = eT;
   const int eU = ls_env("HQ_DECODE_LS_U", 0);
   if (eU >= 2 && eU <= 4) c.U = eU;
-  // Snap to an instantiated (KG, T, U).
+  // Snap to an instantiated (KG, T, U); several row tiles have one configuration.
+  if (c.MT > 1) { c.KG = 2; c.T = 2; c.U = 2; }
   if (c.KG == 1) { c.T = 2; c.U = 4; }
   if (c.KG == 2 && c.T == 1) c.U = 4;
   if (c.KG == 2 && c.T == 2) c.U = std::min(c.U, 3);
@@ -496,6 +542,19 @@ LsConfig choose_decode_ls(int fmt, const GemmDesc& d) {
   c.SW = c.GW * c.T;
   const uint32_t G = ls_assign_slabs(x, (uint32_t)c.SW);
   if (G < cus * 3 / 4) c.S = (int)std::max<uint32_t>(1, std::min<uint32_t>(d.nkb, (cus * 15 / 16 + G - 1) / G));
+  // Ternary tiles are half the bytes of int4 ones, so a step of the same shape has half the
+  // bytes in flight: when the grid is one round and each k-group still gets at least five
+  // steps, four k-groups (16 wavefronts) keep more of them in flight. Measured on MI355X:
+  // 5120 x 27648 20% faster, 17408 x 5120 13% faster; shorter pieces (5120 x 14336 cut in
+  // three) or two rounds (5120 x 34816) are slower so.
+  if (fmt == HQ_FORMAT_TERNARY2 && c.MT == 1 && eKG == 0 && eT == 0 && eU == 0 && c.T == 2 && c.KG == 2 &&
+      (uint64_t)G * (uint32_t)c.S <= cus) {
+    const uint32_t steps4 = (d.nkb / (uint32_t)c.S + 3u) / 4u;
+    if (steps4 >= 5u) {
+      c.KG = 4;
+      c.U = steps4 >= 8u ? 3 : 2;
+    }
+  }
   // Narrower slabs that would cover every CU measured slower (5120 x 27648, M = 1..16:
   // 247 slabs of 7 tiles 2-15% behind 216 of 8), so slabs stay GW * T tiles wide.
   const int eSW = ls_env("HQ_DECODE_LS_SW", 0);
@@ -511,7 +570,7 @@ size_t decode_ls_workspace_bytes(const GemmDesc& d, const LsConfig& c) {
   if (c.S <= 1) return 0;
   GemmDesc x = d;
   const uint32_t G = ls_assign_slabs(x, (uint32_t)c.SW);
-  return kCounterBytes + (size_t)G * c.S * c.GW * c.T * 1024u;
+  return kCounterBytes + (size_t)G * c.S * c.GW * c.T * c.MT * 1024u;
 }
 
 hipError_t launch_decode_ls(int fmt, int dtype, GemmDesc d, const LsConfig& c, void* ws, hipStream_t stream) {

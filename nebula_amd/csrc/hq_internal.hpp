@@ -53,7 +53,7 @@ size_t decode_workspace_bytes(const GemmDesc& d, const DecodeConfig& c);
 // Decode (M <= 16): HBM-streaming MFMA kernel. Validated descriptor in, status out.
 hipError_t launch_decode(int fmt, int dtype, GemmDesc d, const DecodeConfig& c, void* ws, hipStream_t stream);
 
-// Lockstep decode (M <= 16): KG k-groups of four wavefronts per workgroup own a slab of
+// Lockstep decode (M <= 80): KG k-groups of four wavefronts per workgroup own a slab of
 // 4 * T column tiles and walk one piece of its k-blocks together (S pieces per slab), each
 // k-group sharing its activation k-block through LDS.
 struct LsConfig {
@@ -63,14 +63,18 @@ struct LsConfig {
   int KG;  // k-groups per workgroup (1, 2 or 4)
   int GW;  // wavefronts per k-group (2 or 4)
   int SW;  // tiles per slab, at most GW * T (wavefront i takes tiles T i .. min(T i + T, SW) - 1)
+  int MT;  // 16-row tiles of activations (1 .. kLsMaxRowTiles): rows M <= 16 MT
 };
+// The lockstep kernel takes up to this many 16-row tiles (M <= 80: a split-fuse step of 16
+// decode tokens and a 64-token prefill chunk fits one call).
+constexpr uint32_t kLsMaxRowTiles = 5;
 struct LsPlan {
   uint32_t sw;      // tiles per slab
   uint32_t S;       // pieces per slab
   uint32_t kq, kr;  // piece p covers k-blocks [p * kq + min(p, kr), ...) of kq (+1 if p < kr)
   uint32_t gmul;    // plan_gmul(gkb)
   uint32_t* cnt;    // [G] arrival counters, zero between launches (S > 1)
-  float* part;      // [G][S][GW * T tiles][64 lanes] f4 partial tiles (S > 1)
+  float* part;      // [G][S][GW * T * MT tiles][64 lanes] f4 partial tiles (S > 1)
 };
 LsConfig choose_decode_ls(int fmt, const GemmDesc& d);
 size_t decode_ls_workspace_bytes(const GemmDesc& d, const LsConfig& c);

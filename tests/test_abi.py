@@ -59,13 +59,17 @@ def test_workspace_bytes():
     assert st == st1 == hq.HQ_OK
     assert b16 > b1 > 0 and b16 % 256 == 0 and b1 % 256 == 0
     assert (b16 - 65536) == 16 * (b1 - 65536)  # fixed 64 KiB counter area, then M-row partial tiles
-    # Prefill shapes report one bound for every N: the counter area plus two fp32 tiles
-    # (64 rows up to M = 64, 128 rows from M = 65) per concurrent workgroup; K < 1024
-    # is never split along K and needs none.
-    st, p17 = workspace_bytes(hq.FORMAT_INT4, 17, 4096, 4096)
+    # Up to M = 80 the streaming kernel runs (row tiles of 16): its partials grow with the
+    # row tiles. Prefill shapes (M > 80) report one bound for every N: the counter area plus
+    # two fp32 tiles of 128 rows per concurrent workgroup (or 64-row ones, whichever is
+    # more); K < 1024 is never split along K and needs none.
+    _, d16 = workspace_bytes(hq.FORMAT_INT4, 16, 4096, 4096)
+    _, d80 = workspace_bytes(hq.FORMAT_INT4, 80, 4096, 4096)
+    assert d16 > 65536 and d80 - 65536 == 5 * (d16 - 65536)
+    st, p81 = workspace_bytes(hq.FORMAT_INT4, 81, 4096, 4096)
     _, p2048 = workspace_bytes(hq.FORMAT_TERNARY2, 2048, 5120, 27648)
-    assert st == hq.HQ_OK and p17 > 65536 and (p17 - 65536) % (2 * 64 * 256 * 4) == 0
-    assert p2048 > p17 and (p2048 - 65536) % (2 * 128 * 256 * 4) == 0
+    assert st == hq.HQ_OK and p81 > 65536 and (p81 - 65536) % (2 * 64 * 256 * 4) == 0
+    assert p2048 == p81 and (p2048 - 65536) % (2 * 128 * 256 * 4) == 0
     assert workspace_bytes(hq.FORMAT_TERNARY2, 2048, 5120, 16) == (hq.HQ_OK, p2048)
     assert workspace_bytes(hq.FORMAT_INT4, 2048, 896, 4096) == (hq.HQ_OK, 0)
     # Bad shapes are reported, not sized.

@@ -458,11 +458,13 @@ def test_lockstep_matches_per_wavefront(cuda, M):
 
 
 class prefill_env(decode_env):
-    """Force the prefill tiling for a block: WM (tile height 128 or 256 rows), SK=0 (no
+    """Force the prefill kernel (also for M <= 80, which the lockstep kernel takes by
+    default) and its tiling for a block: WM (tile height 128 or 256 rows), SK=0 (no
     stream-K), TAIL=0 (no half-height tail launch), PSK (stream-K workgroups)."""
 
     def __init__(self, **kv):
         self.kv = {f"HQ_PREFILL_{k}": str(v) for k, v in kv.items()}
+        self.kv["HQ_DECODE_MAX_M"] = "16"
 
 
 def normwise_between(a, b):
@@ -570,3 +572,47 @@ def test_prefill_caller_workspace_reused(cuda):
     assert torch_equal(hq.gemm(O.INT4, X300, D.Wp, D.S, N, workspace=ws), D.run(X=X300))
     torch.cuda.synchronize()
     assert int(ws[:65536].view(torch.int32).abs().sum().item()) == 0  # counters left at zero
+
+
+# ---------------------------------------------------------------- lockstep kernel, 17 <= M <= 80
+# Two to five 16-row tiles per workgroup share each dequantised weight fragment (a
+# split-fuse step of 16 decode tokens and a 64-token prefill chunk is one weight stream).
+@pytest.mark.parametrize("M", [17, 31, 32, 48, 63, 64, 65, 79, 80])
+def test_lockstep_row_tiles_int4(cuda, M):
+    P = O.Problem(O.INT4, M, 2048, 1000, 128, O.F16, seed=3400 + M)
+    D = DeviceProblem(P)
+    y = D.run()
+    assert torch_equal(y, D.run())
+    check(y, P.reference(), O.F16, f"row tiles M={M}", P)
+
+
+@pytest.mark.parametrize("fmt,xdt,M", [(O.INT4, O.BF16, 40), (O.TERNARY2, O.F16, 33), (O.TERNARY2, O.BF16, 80)])
+def test_lockstep_row_tiles_formats(cuda, fmt, xdt, M):
+    P = O.Problem(fmt, M, 1536, 700, 256, xdt, seed=3500 + M)
+    check(DeviceProblem(P).run(), P.reference(), xdt, f"row tiles fmt={fmt} M={M}", P)
+
+
+@pytest.mark.parametrize("M,S", [(24, 3), (80, 5), (50, 2)])
+def test_lockstep_row_tiles_split(cuda, M, S):
+    # Slabs cut along K: every row tile's partials go through the fix-up.
+    P = O.Problem(O.INT4, M, 4096, 640, 128, O.F16, seed=3600 + M)
+    D = DeviceProblem(P)
+    with decode_env(LS_S=S):
+        y = D.run()
+        assert torch_equal(y, D.run())
+    check(y, P.reference(), O.F16, f"row tiles split S={S} M={M}", P)
+
+
+def test_lockstep_row_tiles_fused_and_vs_prefill(cuda):
+    Ns, K, M = [600, 130, 1000], 1024, 70
+    probs = [O.Problem(O.INT4, M, K, n, 128, O.F16, seed=3700 + i) for i, n in enumerate(Ns)]
+    for p in probs[1:]:
+        p.X = probs[0].X
+    devs = [DeviceProblem(p) for p in probs]
+    segs = [(d.Wp, d.S, d.P.N) for d in devs]
+    outs = hq.gemm_fused(O.INT4, devs[0].X, segs)
+    with prefill_env():
+        outs_p = hq.gemm_fused(O.INT4, devs[0].X, segs)  # the MFMA tile kernel on the same rows
+    for d, y, yp in zip(devs, outs, outs_p):
+        check(y, d.P.reference(), O.F16, f"row tiles fused N={d.P.N}", d.P)
+        assert O.normwise_error(to_host_f32(y), to_host_f32(yp)) <= OUT_TOL[O.F16]
