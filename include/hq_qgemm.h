@@ -82,7 +82,7 @@ size_t hq_packed_words(hq_format fmt, uint32_t K, uint32_t N);
  * column tiles, prefill calls with few output tiles): a 256-byte aligned buffer,
  * zero-filled by the caller before its first use (every call leaves it zero-filled
  * again). Calls sharing one workspace must not overlap in time (same stream, or ordered
- * by events). For M > 16 the value is a bound that holds for every N and segment split;
+ * by events). For M > 80 the value is a bound that holds for every N and segment split;
  * for a decode hq_gemm_fused pass N = sum of the segments' N plus 16 per segment after
  * the first. Passing NULL instead makes the library use a
  * buffer of its own per (device, stream), allocated on first need outside stream
@@ -143,7 +143,8 @@ hq_status hq_repack_tq1_0_device(const void* d_blocks, uint32_t K, uint32_t N, u
  * Y: [M][ldy], 2-byte aligned, ldy >= N; written in full (no zero-fill needed).
  * K % 128 == 0, group % 128 == 0, K % group == 0, M >= 1, N >= 1.
  * workspace / workspace_bytes: see hq_workspace_bytes (NULL, 0 is always accepted).
- * Decode shapes (M <= 16) run the HBM-streaming kernel; larger M the MFMA tile kernel.
+ * Up to M = 80 (decode steps, split-fuse steps of decode tokens and a prefill chunk) the
+ * HBM-streaming kernels run; larger M the MFMA tile kernel.
  * Results are deterministic: repeated calls with the same shapes give identical bits. */
 hq_status hq_gemm_w4a16(const void* X, hq_dtype dtype, int64_t ldx, const uint32_t* Wp,
                         const uint16_t* scales, void* Y, int64_t ldy, uint32_t M, uint32_t K,
