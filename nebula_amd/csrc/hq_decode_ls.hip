@@ -1,13 +1,15 @@
-// hq_decode_ls.hip — memory-bound qGEMM for M <= 16 (decode), gfx950: lockstep slabs.
+// hq_decode_ls.hip — memory-bound qGEMM for M <= 80 (decode and split-fuse steps), gfx950:
+// lockstep slabs.
 //
 // Replaces kernel_marlin_gemm_int4_templated / _dynamic
 // (hydrogen/src/model/marlin_gemm.cu:130-237, 242-322): the reference gives each thread
 // one output column and does 32 x M scalar FMAs per 16-byte weight load, then merges 16
 // fixed K-splits with fp32 atomics into a pre-zeroed Y.
 //
-// Here a workgroup owns a slab of 4 * T column tiles (16 columns each) and a contiguous
-// range of 128-deep k-blocks ("piece"); a slab's k-blocks are split over S workgroups
-// (S = 1 for wide weights). The workgroup has KG k-groups of four wavefronts; wavefront i
+// Here a workgroup owns a slab of up to 4 * T column tiles (16 columns each) and a
+// contiguous range of 128-deep k-blocks ("piece"); a slab's k-blocks are split over S
+// workgroups (S = 1 for wide weights). The activation rows come in MT tiles of 16 rows
+// (M <= 16 MT): every dequantised weight fragment feeds all MT row tiles. The workgroup has KG k-groups of four wavefronts; wavefront i
 // of every k-group streams tiles T i .. T i + T - 1 of the slab, and at step q k-group kg
 // takes k-block q * KG + kg of the piece, so the KG k-groups split K inside the CU and
 // meet once, at the end, in LDS. The four wavefronts of a k-group walk its k-blocks in
