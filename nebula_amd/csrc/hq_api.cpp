@@ -118,14 +118,14 @@ hq_status get_internal_ws(hipStream_t stream, size_t need, void** out) {
   return HQ_OK;
 }
 
-// Decode kernel family. With at most three activation rows the activation traffic is
-// negligible and the per-wavefront streaming kernel (hq_decode.hip) is as fast or faster;
-// from four rows on, the lockstep kernel (hq_decode_ls.hip), which fetches each activation
-// k-block once per workgroup, is (measured on MI355X over the 27B-class decode shapes).
-// HQ_DECODE_KERNEL=0 / 1 forces one of them (tuning and tests).
-// With ternary weights the lockstep kernel's four-k-group configuration is faster from
-// one row on (5120 x 27648 at M = 1: 12.8 us against 14.7 us), so it is taken whenever the
-// lockstep planner picks it.
+// Streaming kernel family. With at most three activation rows the activation traffic is
+// negligible and the per-wavefront kernel (hq_decode.hip) is as fast or faster; from four
+// rows on, the lockstep kernel (hq_decode_ls.hip), which fetches each activation k-block
+// once per workgroup, is (measured on MI355X over the 27B-class decode shapes), and above
+// 16 rows only the lockstep kernel takes them. With ternary weights the lockstep kernel's
+// four-k-group configuration is faster from one row on (5120 x 27648 at M = 1: 12.8 us
+// against 14.7 us), so it is taken whenever the lockstep planner picks it.
+// HQ_DECODE_KERNEL=0 / 1 forces one of them for M <= 16 (tuning and tests).
 bool use_lockstep(int fmt, const hq::GemmDesc& d) {
   if (d.M > 16) return true;  // only the lockstep kernel takes several row tiles
   const char* v = std::getenv("HQ_DECODE_KERNEL");

@@ -53,9 +53,9 @@ size_t decode_workspace_bytes(const GemmDesc& d, const DecodeConfig& c);
 // Decode (M <= 16): HBM-streaming MFMA kernel. Validated descriptor in, status out.
 hipError_t launch_decode(int fmt, int dtype, GemmDesc d, const DecodeConfig& c, void* ws, hipStream_t stream);
 
-// Lockstep decode (M <= 80): KG k-groups of four wavefronts per workgroup own a slab of
-// 4 * T column tiles and walk one piece of its k-blocks together (S pieces per slab), each
-// k-group sharing its activation k-block through LDS.
+// Lockstep decode (M <= 80): KG k-groups of GW wavefronts per workgroup own a slab of up
+// to GW * T column tiles and walk one piece of its k-blocks together (S pieces per slab),
+// each k-group sharing its activation k-block (MT tiles of 16 rows) through LDS.
 struct LsConfig {
   int T;  // tiles per wavefront (1, 2 or 4)
   int U;   // steps in flight per wavefront (register ring depth)
