@@ -52,7 +52,7 @@ struct Piece {
   uint32_t g, ka, kz;  // slab and its k-block range [ka, kz) inside this workgroup
 };
 
-template <int FMT, int DT, int T, int U>
+template <int FMT, int DT, int T, int U, bool FUSED>
 __global__ void __launch_bounds__(64 * max_wk(T)) hq_decode_kernel(const GemmDesc d, const DecodePlan pl) {
   using W = typename WTraits<FMT>::V;
   constexpr uint32_t WPL = WTraits<FMT>::wpl;
@@ -120,8 +120,11 @@ __global__ void __launch_bounds__(64 * max_wk(T)) hq_decode_kernel(const GemmDes
 #pragma unroll
   for (int j = 0; j < kSL; ++j) svo[j] = 0;
 
-  // Segment of slab g; a plain loop so the segment table is read on demand, not held.
-  auto seg_of = [&](uint32_t g) {
+  // Segment of slab g; a plain loop so the segment table is read on demand, not held. A
+  // one-segment call (FUSED = false) reads its fields at fixed offsets, without a chain of
+  // dependent argument loads.
+  auto seg_of = [&](uint32_t g) -> uint32_t {
+    if constexpr (!FUSED) return 0u;
     uint32_t s = 0;
     for (uint32_t i = 1; i < d.nseg; ++i)
       if (g >= d.seg[i].blk_begin) s = i;
@@ -479,10 +482,17 @@ hipError_t launch_t(GemmDesc d, const DecodeConfig& c, void* ws, hipStream_t str
   }
   const size_t lds = lds_bytes(d, c, pl.np_max);
   if (lds > kLdsLimit) return hipErrorInvalidConfiguration;
-  static const hipError_t attr = hipFuncSetAttribute(reinterpret_cast<const void*>(&hq_decode_kernel<FMT, DT, T, U>),
-                                                     hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsLimit);
+  static const hipError_t attr =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&hq_decode_kernel<FMT, DT, T, U, false>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsLimit) != hipSuccess
+          ? hipErrorInvalidConfiguration
+          : hipFuncSetAttribute(reinterpret_cast<const void*>(&hq_decode_kernel<FMT, DT, T, U, true>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsLimit);
   if (attr != hipSuccess) return attr;
-  hipLaunchKernelGGL((hq_decode_kernel<FMT, DT, T, U>), dim3(pl.P), dim3(64 * c.WK), lds, stream, d, pl);
+  if (d.nseg > 1)
+    hipLaunchKernelGGL((hq_decode_kernel<FMT, DT, T, U, true>), dim3(pl.P), dim3(64 * c.WK), lds, stream, d, pl);
+  else
+    hipLaunchKernelGGL((hq_decode_kernel<FMT, DT, T, U, false>), dim3(pl.P), dim3(64 * c.WK), lds, stream, d, pl);
   return hipGetLastError();
 }
 
