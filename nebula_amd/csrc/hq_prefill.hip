@@ -28,6 +28,15 @@ namespace hq {
 namespace {
 
 constexpr int kTilesPerWave = 4;  // 64 columns per wavefront, 256 per workgroup
+// fp16 128-row tiles order each k-block's instructions explicitly (see step()): the LDS
+// read of A fragment i + kReadAhead issues before the MFMAs of fragment i, and the next
+// chunk's dequantisation is spread between the MFMAs, kValuPerFrag VALU instructions after
+// each fragment's four (the first chunk's, kValuFirst of them, come first). Measured on
+// MI355X against the compiler's own order (which waits on each LDS read right after it):
+// 3-7% faster at M = 512..4096, N = 27648.
+constexpr int kReadAhead = 3;
+constexpr int kValuFirst = 32;
+constexpr int kValuPerFrag = 7;
 
 // Dequantised B fragment with the group scale applied. s2 holds the fp16 scale twice.
 template <int FMT, int DT>
@@ -109,6 +118,10 @@ __global__ void __launch_bounds__(256 * WM, WM == 1 && RT == 8 ? 2 : 1) hq_prefi
   constexpr uint32_t kStageBytes = BM * 256u;        // BM rows x 128 fp16
   constexpr uint32_t kPartBytes = BM * 256u * 4u;    // one fp32 partial tile
   constexpr uint32_t kWavePart = RT * kTilesPerWave * 1024u;  // one wavefront's share of it
+  // The explicit order holds more values live; the fp16 128-row kernels make room for it with
+  // a weight ring of two k-blocks (one ahead: a k-block's MFMAs outlast a load's latency).
+  constexpr bool kOrdered = DT == HQ_DTYPE_F16 && RT == 8;
+  constexpr int kRing = kOrdered ? 2 : 3;
   // Partial tiles are stored and loaded with the sc1 cache policy: agent-coherent, so a
   // store that has completed is visible to loads from any XCD.
   constexpr int kCoherent = 16;
@@ -198,10 +211,11 @@ __global__ void __launch_bounds__(256 * WM, WM == 1 && RT == 8 ? 2 : 1) hq_prefi
     uint32_t soff[kTilesPerWave];
 #pragma unroll
     for (int t = 0; t < kTilesPerWave; ++t) soff[t] = min((ct0 + t) * 16u + c16, sg.N - 1u) * 2u;
-    // Weights and scales: a register ring of 3 k-blocks, two ahead of the one computed.
+    // Weights and scales: a register ring of kRing k-blocks, kRing - 1 ahead of the one
+    // computed.
     // Column tiles past the segment have an empty descriptor and read zero.
-    u4 wr[3][kTilesPerWave];
-    uint32_t sr[3][kTilesPerWave];
+    u4 wr[kRing][kTilesPerWave];
+    uint32_t sr[kRing][kTilesPerWave];
     auto load_b = [&](int slot, uint32_t kb) {
       const uint32_t kc = min(kb, kz - 1u);
       const uint32_t so = kc / d.gkb * sg.lds * 2u;
@@ -222,13 +236,14 @@ __global__ void __launch_bounds__(256 * WM, WM == 1 && RT == 8 ? 2 : 1) hq_prefi
 #pragma unroll
       for (int t = 0; t < kTilesPerWave; ++t) acc[r][t] = f4{0.f, 0.f, 0.f, 0.f};
 
-    // One k-block. Issue order per step: A(kb + 1) to LDS, then B(kb + 2) to registers, so
-    // at the top of the next step vmcnt(2 * kTilesPerWave) leaves only B(kb + 2) in flight.
+    // One k-block. Issue order per step: A(kb + 1) to LDS, then B(kb + kRing - 1) to
+    // registers, so at the top of the next step vmcnt((kRing - 2) * 2 * kTilesPerWave) leaves
+    // only the B loads of later k-blocks in flight (none with a ring of two).
     auto step = [&](uint32_t kb, int slot) {
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * kTilesPerWave));  // A(kb), B(kb) landed for this wave
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm((kRing - 2) * 2 * kTilesPerWave));  // A(kb), B(kb) landed for this wave
       __syncthreads();                                            // ... for every wave; stage (kb+1)&1 is free
       load_a((kb + 1) & 1u, kb + 1);
-      load_b((slot + 2) % 3, kb + 2);
+      load_b((slot + kRing - 1) % kRing, kb + kRing - 1);
       // Keep this step's loads ahead of its compute: vmcnt retires in issue order, so a load
       // sunk below the first use of this step's weights would be waited for with them.
       __builtin_amdgcn_sched_barrier(0);
@@ -251,22 +266,36 @@ __global__ void __launch_bounds__(256 * WM, WM == 1 && RT == 8 ? 2 : 1) hq_prefi
             for (int t = 0; t < kTilesPerWave; ++t) acc[r][t] = mfma16x16x32<DT>(a, b[t], acc[r][t]);
           }
         }
+        if constexpr (kOrdered) {
+          // Instruction order of the k-block (fragment i = c * RT + r): the first kReadAhead
+          // LDS reads and the first chunk's dequantisation, then per fragment the LDS read of
+          // fragment i + kReadAhead, the four MFMAs of fragment i and a share of the next
+          // chunk's dequantisation, so that no LDS round trip stands between MFMAs.
+          // (Masks: 0x100 LDS reads, 0x008 MFMA, 0x002 VALU.)
+          __builtin_amdgcn_sched_group_barrier(0x100, kReadAhead, 0);
+          __builtin_amdgcn_sched_group_barrier(0x002, kValuFirst, 0);
+#pragma unroll
+          for (int i = 0; i < 4 * RT; ++i) {
+            if (i + kReadAhead < 4 * RT) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, kTilesPerWave, 0);
+            __builtin_amdgcn_sched_group_barrier(0x002, kValuPerFrag, 0);
+          }
+        }
       }
     };
 
     // Every wave is past the previous piece's last reads of both LDS stages.
     __syncthreads();
     // Prologue in ring order (no reordering across the barriers): the loop header's wait
-    // counts assume slot 1 holds the youngest loads, as at the loop latch.
+    // counts assume slot kRing - 2 holds the youngest loads, as at the loop latch.
     load_a(ka & 1u, ka);
     load_b(0, ka);
     __builtin_amdgcn_sched_barrier(0);
-    load_b(1, ka + 1);
+    if constexpr (kRing == 3) load_b(1, ka + 1);
     __builtin_amdgcn_sched_barrier(0);
-    for (uint32_t kb = ka; kb < kz; kb += 3) {
-      step(kb, 0);
-      step(kb + 1, 1);
-      step(kb + 2, 2);
+    for (uint32_t kb = ka; kb < kz; kb += kRing) {
+#pragma unroll
+      for (int s = 0; s < kRing; ++s) step(kb + s, s);
     }
     __builtin_amdgcn_s_waitcnt(0);  // drain the prefetches past the piece
   };
