@@ -86,6 +86,14 @@ __device__ __forceinline__ uint32_t ls_bpermute(uint32_t byte_lane, uint32_t v) 
   return r;
 }
 
+// Biased fp16 int4 fragment (words 1024 + q, 64 + q, 1024 + q, 64 + q) -> exact q - 8.
+__device__ __forceinline__ u4 unbias_f16(const u4& f) {
+  const h2 c1032 = {(_Float16)-1032.0f, (_Float16)-1032.0f};
+  const h2 c72 = {(_Float16)-72.0f, (_Float16)-72.0f};
+  return u4{h2_bits(bits_h2(f[0]) + c1032), h2_bits(bits_h2(f[1]) + c72), h2_bits(bits_h2(f[2]) + c1032),
+            h2_bits(bits_h2(f[3]) + c72)};
+}
+
 template <int FMT>
 struct LsW;
 template <>
@@ -114,7 +122,8 @@ __device__ __forceinline__ void ls_tie(u2& a) { asm volatile("" : "+v"(a)); }
 __device__ __forceinline__ void ls_tie(uint32_t& a) { asm volatile("" : "+v"(a)); }
 
 template <int FMT, int DT, int KG, int GW, int T, int U, int MT, bool FUSED>
-__global__ void __launch_bounds__(64 * KG * GW) hq_decode_ls_kernel(const GemmDesc d, const LsPlan pl) {
+__global__ void __launch_bounds__(64 * KG * GW, KG == 1 && MT > 1 ? 2 : 1)
+    hq_decode_ls_kernel(const GemmDesc d, const LsPlan pl) {
   static_assert(KG == 1 || KG == 2 || KG == 4, "one, two or four k-groups");
   static_assert(GW == 2 || GW == 4, "k-groups of two or four wavefronts");
   static_assert(T >= 1 && T <= 4, "the scale load covers at most four tiles");
@@ -123,6 +132,12 @@ __global__ void __launch_bounds__(64 * KG * GW) hq_decode_ls_kernel(const GemmDe
   constexpr uint32_t kLaneBytes = LsW<FMT>::kLaneBytes;
   constexpr uint32_t kBlockBytes = 64u * kLaneBytes;  // one tile x one k-block
   constexpr bool kInt4 = FMT == HQ_FORMAT_INT4;
+  // Several row tiles with fp16 activations: int4 fragments are dequantised exactly to q - 8
+  // (four v_pk_add_f16 per fragment) instead of carrying the bias into a correction MFMA,
+  // which would be a third of the MFMAs of a row tile. Measured on MI355X (5120 x 27648 and
+  // 27648 x 5120, M = 24..80): 5-11% faster. One row tile keeps the biased form (fewer VALU
+  // instructions in the memory-bound case); bf16 has no packed add on gfx950.
+  constexpr bool kUnbiased = kInt4 && DT == HQ_DTYPE_F16 && MT > 1;
   // The register ring holds U steps in flight plus the one being consumed. Activations
   // are staged through two LDS stages: a stage is written just before the barrier of its
   // step and rewritten two steps later, after every wavefront has passed the next barrier
@@ -249,6 +264,7 @@ __global__ void __launch_bounds__(64 * KG * GW) hq_decode_ls_kernel(const GemmDe
       for (int t = 0; t < T; ++t) {
         if constexpr (kInt4) {
           bf[c][t] = dq_int4_biased<DT>(wring[slot][t][c], dqb);
+          if constexpr (kUnbiased) bf[c][t] = unbias_f16(bf[c][t]);
         } else {
           const uint32_t word = wring[slot][t][c >> 1];
           bf[c][t] = (c & 1) ? dq_tern2<1>(word) : dq_tern2<0>(word);
@@ -278,7 +294,7 @@ __global__ void __launch_bounds__(64 * KG * GW) hq_decode_ls_kernel(const GemmDe
       for (int t = 0; t < T; ++t) gs[t] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        if constexpr (kInt4) corr = mfma16x16x32<DT>(xf[c], corr_b, corr);
+        if constexpr (kInt4 && !kUnbiased) corr = mfma16x16x32<DT>(xf[c], corr_b, corr);
 #pragma unroll
         for (int t = 0; t < T; ++t) gs[t] = mfma16x16x32<DT>(xf[c], bf[c][t], gs[t]);
       }
@@ -286,7 +302,7 @@ __global__ void __launch_bounds__(64 * KG * GW) hq_decode_ls_kernel(const GemmDe
       for (int t = 0; t < T; ++t)
 #pragma unroll
         for (int v = 0; v < 4; ++v)
-          acc[r][t][v] = __builtin_fmaf(kInt4 ? gs[t][v] + corr[v] : gs[t][v], sc[t], acc[r][t][v]);
+          acc[r][t][v] = __builtin_fmaf(kInt4 && !kUnbiased ? gs[t][v] + corr[v] : gs[t][v], sc[t], acc[r][t][v]);
     }
   };
 
@@ -509,6 +525,16 @@ hipError_t ls_launch_t(GemmDesc d, const LsConfig& c, void* ws, hipStream_t stre
 
 template <int FMT, int DT>
 hipError_t ls_launch_fd(const GemmDesc& d, const LsConfig& c, void* ws, hipStream_t stream) {
+  if (c.MT > 1 && c.KG == 1) {  // one k-group, two workgroups per CU
+    if (c.GW * 1000 + c.KG * 100 + c.T * 10 + c.U != 4122) return hipErrorInvalidConfiguration;
+    switch (c.MT) {
+      case 2: return ls_launch_t<FMT, DT, 1, 4, 2, 2, 2>(d, c, ws, stream);
+      case 3: return ls_launch_t<FMT, DT, 1, 4, 2, 2, 3>(d, c, ws, stream);
+      case 4: return ls_launch_t<FMT, DT, 1, 4, 2, 2, 4>(d, c, ws, stream);
+      case 5: return ls_launch_t<FMT, DT, 1, 4, 2, 2, 5>(d, c, ws, stream);
+      default: return hipErrorInvalidConfiguration;
+    }
+  }
   if (c.MT > 1) {  // several row tiles: two k-groups of four wavefronts, two tiles each, two steps in flight
     if (c.GW * 1000 + c.KG * 100 + c.T * 10 + c.U != 4222) return hipErrorInvalidConfiguration;
     switch (c.MT) {
@@ -549,13 +575,14 @@ LsConfig choose_decode_ls(int fmt, const GemmDesc& d) {
   if (eT == 1 || eT == 2 || eT == 4) c.T = eT;
   const int eU = ls_env("HQ_DECODE_LS_U", 0);
   if (eU >= 2 && eU <= 4) c.U = eU;
-  // Snap to an instantiated (KG, T, U); several row tiles have one configuration.
-  if (c.MT > 1) { c.KG = 2; c.T = 2; c.U = 2; }
+  // Snap to an instantiated (KG, T, U); several row tiles have two configurations (one or
+  // two k-groups of four wavefronts, two tiles each, two steps in flight).
   if (c.KG == 1) { c.T = 2; c.U = 4; }
   if (c.KG == 2 && c.T == 1) c.U = 4;
   if (c.KG == 2 && c.T == 2) c.U = std::min(c.U, 3);
   if (c.KG == 2 && c.T == 4) c.U = 2;
   if (c.KG == 4) { c.T = std::min(c.T, 2); c.U = c.T == 1 ? 3 : std::min(c.U, 3); }
+  if (c.MT > 1) { c.KG = eKG == 1 ? 1 : 2; c.T = 2; c.U = 2; }
   GemmDesc x = d;
   c.SW = c.GW * c.T;
   const uint32_t G = ls_assign_slabs(x, (uint32_t)c.SW);
@@ -573,6 +600,12 @@ LsConfig choose_decode_ls(int fmt, const GemmDesc& d) {
       c.U = steps4 >= 8u ? 3 : 2;
     }
   }
+  // Several row tiles: one workgroup per CU (two k-groups of four wavefronts near 256 VGPRs
+  // each), so a grid of more slabs than CUs would run a second, nearly empty round. One k-group
+  // per workgroup lets two workgroups share a CU and the whole grid run at once. Measured on
+  // MI355X (ternary 5120 x 34816, 272 slabs): M = 48 47 -> 41.5 us, M = 80 63 -> 60 us; with
+  // slabs for every CU already (216-240) one k-group is 5-20% slower.
+  if (c.MT > 1 && eKG == 0 && (uint64_t)G * (uint32_t)c.S > cus && (uint64_t)G * (uint32_t)c.S <= 2ull * cus) c.KG = 1;
   // Narrower slabs that would cover every CU measured slower (5120 x 27648, M = 1..16:
   // 247 slabs of 7 tiles 2-15% behind 216 of 8), so slabs stay GW * T tiles wide.
   const int eSW = ls_env("HQ_DECODE_LS_SW", 0);

@@ -603,6 +603,28 @@ def test_lockstep_row_tiles_split(cuda, M, S):
     check(y, P.reference(), O.F16, f"row tiles split S={S} M={M}", P)
 
 
+@pytest.mark.parametrize("fmt,xdt,M", [(O.INT4, O.F16, 40), (O.INT4, O.BF16, 80), (O.TERNARY2, O.F16, 64), (O.TERNARY2, O.BF16, 17)])
+def test_lockstep_row_tiles_one_kgroup(cuda, fmt, xdt, M):
+    # One k-group per workgroup (two workgroups per CU), forced.
+    P = O.Problem(fmt, M, 1536, 700, 128, xdt, seed=3800 + M)
+    D = DeviceProblem(P)
+    with decode_env(LS_KG=1):
+        y = D.run()
+        assert torch_equal(y, D.run())
+    check(y, P.reference(), xdt, f"row tiles one k-group fmt={fmt} M={M}", P)
+
+
+def test_lockstep_row_tiles_wide_grid(cuda):
+    # More 8-tile slabs than CUs (260 on 256 CUs): the planner takes one k-group per workgroup.
+    N = 16 * 8 * 260
+    P = O.Problem(O.INT4, 40, 512, N, 128, O.F16, seed=3900)
+    D = DeviceProblem(P)
+    y = D.run()
+    check(y, P.reference(), O.F16, f"row tiles wide grid N={N}", P)
+    with decode_env(LS_KG=2):  # two rounds of one-per-CU workgroups: the same products
+        check(D.run(), P.reference(), O.F16, f"row tiles wide grid, two k-groups, N={N}", P)
+
+
 def test_lockstep_row_tiles_fused_and_vs_prefill(cuda):
     Ns, K, M = [600, 130, 1000], 1024, 70
     probs = [O.Problem(O.INT4, M, K, n, 128, O.F16, seed=3700 + i) for i, n in enumerate(Ns)]
