@@ -239,7 +239,7 @@ def run_gpu(args):
                                 "frac_mfma_f16": round(tf / MFMA_F16_PEAK_TFLOPS, 4)}
             log(f"prefill M={M}: {us:.1f} us, {tf:.1f} TFLOP/s")
             del Xp, Yp
-        # config 4: 1008 prefill rows + 16 decode rows, fused QKV (int4) and gate||up (ternary)
+        # mixed split-fuse batch: 1008 prefill rows + 16 decode rows, fused QKV (int4) and gate||up (ternary)
         M = 1024
         Xm = torch.randn((M, 5120), device="cuda").to(torch.float16)
         qkv, gu = [], []

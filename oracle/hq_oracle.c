@@ -1,7 +1,7 @@
 /*
  * hq_oracle.c — CPU restatement of hydrogen's weight-only quantized GEMM path.
  *
- * TEST INFRASTRUCTURE ONLY (the checker). See hq_oracle.h for the function-by-
+ * TEST INFRASTRUCTURE ONLY (the oracle). See hq_oracle.h for the function-by-
  * function map to the reference. Build with -ffp-contract=off: the reference's
  * host dequantisation (marlin_gemm.cu:506) is a separate multiply and add, and
  * the only fused multiply-adds are the explicit fmaf() calls of the matmul,

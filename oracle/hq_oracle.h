@@ -1,7 +1,7 @@
 /*
  * hq_oracle.h — CPU restatement of hydrogen's weight-only quantized GEMM path.
  *
- * TEST INFRASTRUCTURE ONLY. This library is the checker: tests, the smoke
+ * TEST INFRASTRUCTURE ONLY. This library is the oracle: tests, the smoke
  * check and the CPU-baseline leg of the benchmark call it. Nothing in the
  * product library (nebula_amd/) links or loads it.
  *

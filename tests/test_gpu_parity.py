@@ -1,6 +1,6 @@
 """GPU parity of the HIP qGEMM against the CPU oracle, called through the C ABI.
 
-Bar (north star): max relative error <= 1e-2 with fp32 accumulation on both sides,
+Bar of the target operator: max relative error <= 1e-2 with fp32 accumulation on both sides,
 measured normwise (max |y - r| / max |r|); the integer/byte work (repacks) is bit-exact.
 Two tighter checks stop a bug from hiding under that bar:
   * normwise error <= OUT_TOL[dtype] (output rounding: fp16 2^-11, bf16 2^-8, plus slack);
@@ -44,8 +44,8 @@ def check(y, ref, xdtype, label, P=None):
     return err
 
 
-def test_config0_w4a16_m16_4096(cuda):
-    # Config 0: M=16, K=N=4096, int4 zero point 8, g=128, fp16 in/out.
+def test_w4a16_m16_4096(cuda):
+    # The single W4A16 GEMM: M=16, K=N=4096, int4 zero point 8, g=128, fp16 in/out.
     P = O.Problem(O.INT4, 16, 4096, 4096, 128, O.F16, seed=42)
     D = DeviceProblem(P)
     check(D.run(), P.reference(), O.F16, "c0", P)
@@ -64,8 +64,8 @@ def test_decode_int4_bf16(cuda, M):
 
 
 @pytest.mark.parametrize("M", [1, 8])
-def test_config2_ternary_bf16(cuda, M):
-    # Config 2: ternary {-1,0,1} p={.25,.5,.25}, K=5120, N=27648, bf16 activations.
+def test_ternary_bf16_decode_27b(cuda, M):
+    # Ternary decode GEMV: ternary {-1,0,1} p={.25,.5,.25}, K=5120, N=27648, bf16 activations.
     P = O.Problem(O.TERNARY2, M, 5120, 27648, 128, O.BF16, seed=300 + M)
     check(DeviceProblem(P).run(), P.reference(), O.BF16, f"ternary bf16 M={M}", P)
 
@@ -77,9 +77,9 @@ def test_decode_ternary_f16(cuda, M):
 
 
 @pytest.mark.parametrize("K,N", [(5120, 27648), (27648, 5120)])
-def test_config1_large_shapes_m16(cuda, K, N):
+def test_w4a16_27b_shapes_m16(cuda, K, N):
     P = O.Problem(O.INT4, 16, K, N, 128, O.F16, seed=400)
-    check(DeviceProblem(P).run(), P.reference(threads=16), O.F16, f"c1 {K}x{N}")
+    check(DeviceProblem(P).run(), P.reference(threads=16), O.F16, f"w4a16 {K}x{N} M=16")
 
 
 @pytest.mark.parametrize("fmt,xdt", [(O.INT4, O.F16), (O.INT4, O.BF16), (O.TERNARY2, O.F16), (O.TERNARY2, O.BF16)])
@@ -182,15 +182,15 @@ def test_prefill_group_256(cuda):
 
 
 @pytest.mark.parametrize("M", [512, 2048])
-def test_config3_prefill_rows_subset(cuda, M):
-    # Config 3 shape (K=5120, N=27648). Rows are independent, so a random subset of rows
+def test_prefill_27b_rows_subset(cuda, M):
+    # The prefill shape (K=5120, N=27648). Rows are independent, so a random subset of rows
     # is compared against the oracle at full size.
     P = O.Problem(O.INT4, M, 5120, 27648, 128, O.F16, seed=880 + M)
     y = to_host_f32(DeviceProblem(P).run())
     rows = np.sort(np.random.default_rng(M).choice(M, size=24, replace=False))
     ref = P.reference(rows=rows, threads=16)
     err = O.normwise_error(y[rows], ref)
-    assert err <= OUT_TOL[O.F16], f"config 3 M={M}: {err:.3e}"
+    assert err <= OUT_TOL[O.F16], f"prefill K=5120 N=27648 M={M}: {err:.3e}"
 
 
 def test_rows_independent_and_deterministic(cuda):
