@@ -15,9 +15,9 @@ projections that share an input run as one fused call over all rows of a step:
 
 Rows are independent, so a step's rows may be any mix of decode tokens and prefill tokens
 (the split-fuse batch of hydrogen/src/batcher/split_fuse.cpp:110-159: the decode streams'
-tokens first, then one prefill chunk); the library picks its decode kernels for up to 16 rows
-and its prefill kernels above. `StepRows` builds such a batch's activation matrix and splits
-the outputs back per chunk. Normalisation, attention, the SSM step and SwiGLU stay with the
+tokens first, then one prefill chunk); the library picks its streaming (decode) kernels for
+up to 80 rows and its prefill kernels above. `StepRows` builds such a batch's activation
+matrix and splits the outputs back per chunk. Normalisation, attention, the SSM step and SwiGLU stay with the
 caller: they are not projections.
 
 Activations are fp16 or bf16 (the reference's are fp32); the ternary weights and their
