@@ -118,11 +118,12 @@ hq_status get_internal_ws(hipStream_t stream, size_t need, void** out) {
   return HQ_OK;
 }
 
-// Streaming kernel family. With at most three activation rows the activation traffic is
-// negligible and the per-wavefront kernel (hq_decode.hip) is as fast or faster; from four
-// rows on, the lockstep kernel (hq_decode_ls.hip), which fetches each activation k-block
-// once per workgroup, is (measured on MI355X over the 27B-class decode shapes), and above
-// 16 rows only the lockstep kernel takes them. With ternary weights the lockstep kernel's
+// Streaming kernel family. With at most four activation rows the activation traffic is
+// small and the per-wavefront kernel (hq_decode.hip) is as fast or faster (M = 4, same-run
+// order-swapped timings on MI355X: 5120 x 5120 7.7 against 8.1 us, 5120 x 27648 15.9 against
+// 16.15 us, 27648 x 5120 even); from five rows on, the lockstep kernel (hq_decode_ls.hip),
+// which fetches each activation k-block once per workgroup, is, and above 16 rows only the
+// lockstep kernel takes them. With ternary weights the lockstep kernel's
 // four-k-group configuration is faster from one row on (5120 x 27648 at M = 1: 12.8 us
 // against 14.7 us), so it is taken whenever the lockstep planner picks it.
 // HQ_DECODE_KERNEL=0 / 1 forces one of them for M <= 16 (tuning and tests).
@@ -130,7 +131,7 @@ bool use_lockstep(int fmt, const hq::GemmDesc& d) {
   if (d.M > 16) return true;  // only the lockstep kernel takes several row tiles
   const char* v = std::getenv("HQ_DECODE_KERNEL");
   if (v && *v) return std::atoi(v) != 0;
-  if (d.M >= 4) return true;
+  if (d.M >= 5) return true;
   return fmt == HQ_FORMAT_TERNARY2 && hq::choose_decode_ls(fmt, d).KG == 4;
 }
 

@@ -249,7 +249,7 @@ def test_device_repack_matches_host(cuda, fmt):
 
 # ---------------------------------------------------------------- decode work decomposition
 # Keys of the per-wavefront kernel's decomposition; forcing any of them also selects that
-# kernel (HQ_DECODE_KERNEL=0), which otherwise serves only M <= 3.
+# kernel (HQ_DECODE_KERNEL=0), which otherwise serves only M <= 4.
 _PW_KEYS = {"T", "WK", "P", "G", "U", "CONTIG"}
 
 
