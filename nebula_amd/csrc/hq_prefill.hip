@@ -615,13 +615,25 @@ PrefillConfig choose_prefill(int fmt, const GemmDesc& d) {
     if (split >= 2u && d.nkb / split < 64u) {
       RT = 4;
     } else if (split < 2u) {
-      // Whole tiles either way: compare rounds. A part-empty last round costs about 0.65 of a
-      // full one (its lone workgroups run faster), and a round of 64-row tiles about 0.6 of a
-      // 128-row round (measured on MI355X; e.g. 544 tiles of 128 rows, ternary K = 5120,
-      // N = 34816, M = 512: 64-row tiles 10% faster).
+      // Whole tiles either way: compare rounds, in units of a full 128-row round. A part-empty
+      // last round that leaves at most one workgroup per CU costs 0.35 + 0.45 x its fill (its
+      // lone workgroups run faster); a fuller one 0.35 + 0.65 x its fill with 128-row tiles
+      // and a whole round with 64-row tiles (several per CU). A 64-row tile computes its
+      // rows at 0.76 (int4: its dequantisation is shared by half as many rows) or 0.915
+      // (ternary) of a 128-row tile's rate, so a round of s64 64-row tiles costs
+      // (s64 * 64) / (s128 * 128) / rate. Measured on MI355X (K = 5120; ternary N = 27648,
+      // 34816, 55296 and int4 N = 27648, 55296 at M = 384..2048): this picks the faster
+      // height in every case, e.g. ternary N = 34816 at M = 512 (544 128-row tiles) 64-row
+      // tiles 7% faster, at M = 2048 128-row tiles 10% faster; int4 N = 27648 at M = 384
+      // 128-row tiles 12% faster.
       const uint32_t t64 = make_launch(4, 1, d).tiles, s64 = (uint32_t)prefill_slots(fmt, 4, 1);
-      auto rounds = [](uint32_t t, uint32_t sl) { return (double)(t / sl) + (t % sl ? 0.65 : 0.0); };
-      if (0.6 * rounds(t64, s64) < rounds(t128, s128)) RT = 4;
+      const double rate64 = fmt == HQ_FORMAT_INT4 ? 0.76 : 0.915;
+      const double round64 = (double)s64 * 64.0 / ((double)s128 * 128.0) / rate64;
+      auto rounds = [](uint32_t t, uint32_t sl, double full) {
+        const double f = (double)(t % sl) / (double)sl;
+        return (double)(t / sl) + (t % sl ? (f <= 0.5 ? 0.35 + 0.45 * f : full * (0.35 + 0.65 * f) + (1.0 - full)) : 0.0);
+      };
+      if (round64 * rounds(t64, s64, 0.0) < rounds(t128, s128, 1.0)) RT = 4;
     }
   }
   c.n = 1;
