@@ -4,34 +4,49 @@
 Workload (one "step"): the W4A16 decode sweep, group 128, fp16 activations,
 (K, N) in {(5120, 5120), (5120, 27648), (27648, 5120)} x M in {1, 2, 4, 8, 16}:
 15 GEMM launches. value = packed-weight + scale bytes of the whole step / step time
-(GB/s). Weights rotate over >= 640 MiB of distinct copies per shape, so the 256 MiB
-Infinity Cache cannot serve them. Steps are replayed as HIP graphs (one captured
-graph per weight copy), which keeps host launch cost off the GPU timeline.
+(GB/s). Every launch reads a weight copy that no launch of the previous ~640 MiB read
+(copies rotate per launch over >= 640 MiB per shape), so the 256 MiB Infinity Cache cannot
+serve them. Steps are replayed as HIP graphs, which keeps host launch cost off the GPU
+timeline; inputs are resident in HBM before the timed region.
 
 The same JSON line also carries:
-  roofline      the dominant launch (K=5120, N=27648, M=16): algorithmic bytes (packed
-                weights + scales) / average launch duration (HIP events around 64
-                back-to-back launches on the launch stream), against 8 TB/s; `traffic`
-                is the HBM bytes per launch from the committed rocprofv3 counter summary
-                (profiles/decode_K5120_N27648_M16_traffic.json) when present;
-  prefill       TFLOP/s of W4A16 M in {512, 2048, 4096}, K=5120, N=27648 and of the
-                split-fuse mixed batch (fused QKV int4, fused gate||up ternary, M=1024),
-                against the 2.5 PFLOP/s dense fp16 MFMA peak;
-  cpu_baseline  the CPU oracle (restated reference dequantize-then-matmul, fp32) on the
-                host cores over the same 15 GEMMs, repeated for about 10 s.
+  cases         per launch shape: average launch duration (HIP events on the launch stream
+                around back-to-back launches of one captured graph, rotating weight copies),
+                GB/s and fraction of the 8 TB/s HBM peak, and the plan (kernel, tiling) that
+                ran. The decode sweep's 15 shapes, the single W4A16 GEMM (M=16, K=N=4096)
+                and the ternary bf16 decode (K=5120, N=27648, M in {1, 8});
+  roofline      the dominant decode kernel (the kernel with the largest share of the step
+                time): its algorithmic bytes (packed weights + scales) per launch / its
+                average launch duration, against 8 TB/s; `traffic` is the HBM bytes per
+                launch measured in this run by two rocprofv3 --pmc passes (FETCH_SIZE,
+                WRITE_SIZE) over that kernel's shape, each scaled by what the same counter
+                reads for a plain device copy of known size (null if rocprofv3 is absent);
+  prefill_M2048 the metric's second half: W4A16 M=2048, K=5120, N=27648 TFLOP/s against the
+                2.5 PFLOP/s dense fp16 MFMA peak (also as roofline_prefill);
+  prefill       M in {512, 2048, 4096} and the split-fuse mixed batch (fused QKV int4, fused
+                gate||up ternary, M=1024);
+  cpu_baseline  the CPU oracle (restated reference path: host dequantisation, then the fp32
+                matmul) on the host cores over the 15 decode GEMMs: dequantisation and matmul
+                timed separately, median of 5 runs each.
 
 Usage:
-  python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--no-prefill]
-  python bench.py --roofline-only        # the dominant launch only (for rocprofv3 --pmc)
-  python bench.py --copy-bytes 268435456 # a plain device copy of known size (counter calibration)
-  python bench.py --prefill-only 2048    # W4A16 prefill M=2048, K=5120, N=27648 only (for counters)
+  python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--no-prefill] [--no-traffic]
+  python bench.py --roofline-only --case K N M  # one decode shape only (for rocprofv3 --pmc)
+  python bench.py --copy-bytes 268435456        # a plain device copy of known size (counter calibration)
+  python bench.py --prefill-only 2048           # W4A16 prefill M=2048, K=5120, N=27648 only (for counters)
 """
 from __future__ import annotations
 
 import argparse
+import csv
 import json
+import math
 import os
+import shutil
+import statistics
+import subprocess
 import sys
+import tempfile
 import time
 from pathlib import Path
 
@@ -44,25 +59,29 @@ SHAPES = [(5120, 5120), (5120, 27648), (27648, 5120)]
 MS = [1, 2, 4, 8, 16]
 GROUP = 128
 ROTATE_BYTES = 640 << 20  # per shape, > 2x the 256 MiB MALL
-DOMINANT = (5120, 27648, 16)
-TRAFFIC_FILE = ROOT / "profiles" / "decode_K5120_N27648_M16_traffic.json"
+COPY_BYTES = 268435456    # counter calibration copy
+FMT_INT4, FMT_TERN = 1, 2
 
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def wbytes(K: int, N: int, fmt: int = 1) -> int:
+def wbytes(K: int, N: int, fmt: int = FMT_INT4) -> int:
     """Algorithmic bytes of one launch: packed weights (int4 K*N/2, ternary K*N/4) + fp16 scales."""
-    return (K * N // 2 if fmt == 1 else K * N // 4) + (K // GROUP) * N * 2
+    return (K * N // 2 if fmt == FMT_INT4 else K * N // 4) + (K // GROUP) * N * 2
 
 
-def make_weights(hq, torch, K, N, copies, fmt=1):
+def n_copies(K: int, N: int, fmt: int = FMT_INT4) -> int:
+    return max(2, -(-ROTATE_BYTES // wbytes(K, N, fmt)))
+
+
+def make_weights(hq, torch, K, N, copies, fmt=FMT_INT4):
     """Distinct packed copies (device repack of random linear words) and |N(0, 0.02)| fp16 scales."""
     lin_words = hq.linear_words(fmt, K, N)
     ws, ss = [], []
     for _ in range(copies):
-        if fmt == 1:
+        if fmt == FMT_INT4:
             lin = torch.randint(-2**31, 2**31 - 1, (lin_words,), dtype=torch.int32, device="cuda")
         else:  # ternary codes c = t + 1 with P(t) = (.25, .5, .25), 16 per word
             r = torch.randint(0, 4, (lin_words, 16), dtype=torch.int64, device="cuda")
@@ -97,17 +116,22 @@ def graph_time_us(torch, stream, launches, reps: int = 3) -> float:
     return a.elapsed_time(b) * 1e3 / (reps * n)
 
 
-def run_roofline_only(torch, hq):
-    K, N, M = DOMINANT
-    copies = max(2, -(-ROTATE_BYTES // wbytes(K, N)))
+def kernel_of(plan: str) -> str:
+    """The kernel (template and parameters) of a plan description."""
+    return plan.split(">", 1)[0] + ">"
+
+
+# ---------------------------------------------------------------- single-purpose runs (profilers)
+def run_case_only(torch, hq, K: int, N: int, M: int):
+    copies = n_copies(K, N)
     ws, ss = make_weights(hq, torch, K, N, copies)
     X = torch.randn((M, K), device="cuda").to(torch.float16)
     Y = torch.empty((M, N), device="cuda", dtype=torch.float16)
     torch.cuda.synchronize()
     for r in range(4 * copies):
-        hq.gemm(1, X, ws[r % copies], ss[r % copies], N, GROUP, out=Y)
+        hq.gemm(FMT_INT4, X, ws[r % copies], ss[r % copies], N, GROUP, out=Y)
     torch.cuda.synchronize()
-    log(f"roofline-only: {4 * copies} launches of K={K} N={N} M={M}")
+    log(f"case-only: {4 * copies} launches of K={K} N={N} M={M}: {hq.describe(FMT_INT4, 1, M, K, N)}")
 
 
 def run_prefill_only(torch, hq, M: int):
@@ -116,7 +140,7 @@ def run_prefill_only(torch, hq, M: int):
     X = torch.randn((M, K), device="cuda").to(torch.float16)
     Y = torch.empty((M, N), device="cuda", dtype=torch.float16)
     for _ in range(5):
-        hq.gemm(1, X, ws[0], ss[0], N, GROUP, out=Y)
+        hq.gemm(FMT_INT4, X, ws[0], ss[0], N, GROUP, out=Y)
     torch.cuda.synchronize()
     log(f"prefill-only: 5 launches of M={M} K={K} N={N}")
 
@@ -131,17 +155,54 @@ def run_copy(torch, nbytes: int):
     log(f"copy-only: 4 copies of {nbytes} bytes")
 
 
-def traffic_from_profile():
-    """HBM bytes per dominant launch from the committed counter summary, or None."""
+# ---------------------------------------------------------------- HBM traffic (rocprofv3 --pmc)
+def _pmc_pass(counter: str, args: list, outdir: str, tag: str):
+    """One rocprofv3 counter pass over a child run of this script; per-dispatch values (KiB)."""
+    cmd = ["timeout", "-s", "KILL", "120", "rocprofv3", "--pmc", counter, "-d", outdir, "-o", tag,
+           "--output-format", "csv", "--", sys.executable, "-u", str(ROOT / "bench.py"), *args]
+    p = subprocess.run(cmd, capture_output=True, text=True)
+    if p.returncode != 0:
+        raise RuntimeError(f"{' '.join(cmd)} exited {p.returncode}: {p.stderr[-400:]}")
+    rows = []
+    for path in Path(outdir).rglob(f"{tag}_counter_collection.csv"):
+        with open(path) as f:
+            rows += [r for r in csv.DictReader(f) if r.get("Counter_Name") == counter]
+    return rows
+
+
+def measure_traffic(K: int, N: int, M: int, kernel: str):
+    """HBM bytes per launch of the decode kernel at (K, N, M): FETCH_SIZE and WRITE_SIZE (KiB per
+    dispatch) from two rocprofv3 --pmc passes, each scaled by bytes / counter of a plain copy of
+    COPY_BYTES (FETCH_SIZE of a copy reads half its bytes on this part)."""
+    if shutil.which("rocprofv3") is None:
+        return None, "rocprofv3 not found"
+    out = tempfile.mkdtemp(prefix="hq_pmc_")
     try:
-        t = json.loads(TRAFFIC_FILE.read_text())
-        f = t["fetch_kib"] * 1024 * t["copy_bytes"] / (t["copy_fetch_kib"] * 1024)
-        w = t["write_kib"] * 1024 * t["copy_bytes"] / (t["copy_write_kib"] * 1024)
-        return int(f + w)
-    except (OSError, KeyError, ValueError, ZeroDivisionError):
-        return None
+        res = {}
+        for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+            dec = [float(r["Counter_Value"]) for r in
+                   _pmc_pass(counter, ["--roofline-only", "--case", str(K), str(N), str(M)], out, "dec_" + counter)
+                   if kernel.split("<")[0] in r["Kernel_Name"]]
+            cpy = [float(r["Counter_Value"]) for r in
+                   _pmc_pass(counter, ["--copy-bytes", str(COPY_BYTES)], out, "copy_" + counter)
+                   if "copy" in r["Kernel_Name"].lower() or "elementwise" in r["Kernel_Name"].lower()]
+            if not dec or not cpy:
+                return None, f"{counter}: no dispatches matched ({len(dec)} kernel, {len(cpy)} copy)"
+            res[counter] = (statistics.mean(dec), max(cpy), len(dec))
+        f_kib, cf_kib, nd = res["FETCH_SIZE"]
+        w_kib, cw_kib, _ = res["WRITE_SIZE"]
+        traffic = f_kib * COPY_BYTES / cf_kib + w_kib * COPY_BYTES / cw_kib
+        note = (f"FETCH_SIZE {f_kib:.1f} KiB x {COPY_BYTES / 1024 / cf_kib:.4f} + WRITE_SIZE {w_kib:.1f} KiB x "
+                f"{COPY_BYTES / 1024 / cw_kib:.4f} per dispatch ({nd} dispatches); factors = copy bytes / counter "
+                f"of a {COPY_BYTES}-byte device copy")
+        return int(traffic), note
+    except (RuntimeError, OSError, KeyError, ValueError) as e:
+        return None, f"traffic not measured: {e}"
+    finally:
+        shutil.rmtree(out, ignore_errors=True)
 
 
+# ---------------------------------------------------------------- the GPU run
 def run_gpu(args):
     import torch
 
@@ -155,21 +216,26 @@ def run_gpu(args):
     # ---- decode sweep (the value) ----
     pools = {}
     for K, N in SHAPES:
-        copies = max(2, -(-ROTATE_BYTES // wbytes(K, N)))
-        pools[(K, N)] = make_weights(hq, torch, K, N, copies)
-        log(f"shape K={K} N={N}: {copies} weight copies ({copies * wbytes(K, N) / 2**20:.0f} MiB)")
+        pools[(K, N)] = make_weights(hq, torch, K, N, n_copies(K, N))
+        log(f"shape K={K} N={N}: {len(pools[(K, N)][0])} weight copies "
+            f"({len(pools[(K, N)][0]) * wbytes(K, N) / 2**20:.0f} MiB)")
     X = {K: torch.randn((16, K), device="cuda").to(torch.float16) for K in {k for k, _ in SHAPES}}
     Y = {(K, N): torch.empty((16, N), device="cuda", dtype=torch.float16) for K, N in SHAPES}
-    R = max(len(w) for w, _ in pools.values())
     step_bytes = sum(wbytes(K, N) for K, N in SHAPES for _ in MS)
 
+    # Launch j of step i reads copy (i * len(MS) + j) mod copies: consecutive launches of a shape
+    # never share a copy, and a copy comes back only after every other copy of the shape.
     def step(i):
         for K, N in SHAPES:
             ws, ss = pools[(K, N)]
-            c = i % len(ws)
-            for M in MS:
-                hq.gemm(1, X[K][:M], ws[c], ss[c], N, GROUP, out=Y[(K, N)][:M])
+            for j, M in enumerate(MS):
+                c = (i * len(MS) + j) % len(ws)
+                hq.gemm(FMT_INT4, X[K][:M], ws[c], ss[c], N, GROUP, out=Y[(K, N)][:M])
 
+    R = 1
+    for K, N in SHAPES:
+        c = len(pools[(K, N)][0])
+        R = R * (c // math.gcd(c, len(MS))) // math.gcd(R, c // math.gcd(c, len(MS)))
     with torch.cuda.stream(stream):
         step(0)  # eager pass before capture
     torch.cuda.synchronize()
@@ -194,51 +260,87 @@ def run_gpu(args):
     ms_per_step = e0.elapsed_time(e1) / args.steps
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
     log(f"decode sweep: {ms_per_step * 1e3:.1f} us/step, {value:.1f} GB/s")
+    del graphs
 
-    # ---- per-case timing: 64 back-to-back launches over rotating weight copies ----
+    # ---- per-case timing: back-to-back launches over rotating weight copies ----
+    def time_case(fmt, K, N, M, ws, ss, Xk, Yk, dtype=1):
+        reps = len(ws) * max(1, 64 // len(ws))
+
+        def launches():
+            for r in range(reps):
+                hq.gemm(fmt, Xk[:M], ws[r % len(ws)], ss[r % len(ws)], N, GROUP, out=Yk[:M])
+            return reps
+
+        us = graph_time_us(torch, stream, launches)
+        gbs = wbytes(K, N, fmt) / (us * 1e-6) / 1e9
+        return {"us": round(us, 2), "GBps": round(gbs, 1), "pct_hbm": round(100 * gbs / HBM_PEAK_GBS, 1),
+                "plan": hq.describe(fmt, dtype, M, K, N, GROUP)}
+
     cases = {}
     for K, N in SHAPES:
         ws, ss = pools[(K, N)]
         for M in MS:
-            reps = len(ws) * max(1, 64 // len(ws))
+            cases[f"K{K}_N{N}_M{M}"] = time_case(FMT_INT4, K, N, M, ws, ss, X[K], Y[(K, N)])
+    # Dominant kernel: the largest share of the step's time (one launch per case and step).
+    share = {}
+    for key, c in cases.items():
+        share.setdefault(kernel_of(c["plan"]), []).append(key)
+    tot = sum(c["us"] for c in cases.values())
+    dom_kernel = max(share, key=lambda k: sum(cases[c]["us"] for c in share[k]))
+    dom_cases = share[dom_kernel]
+    dom_us = sum(cases[c]["us"] for c in dom_cases)
+    dom_bytes = sum(wbytes(int(c.split("_")[0][1:]), int(c.split("_")[1][1:])) for c in dom_cases)
+    achieved = dom_bytes / (dom_us * 1e-6) / 1e9
+    # Its longest launch shape is the one the counter passes profile.
+    prof_case = max(dom_cases, key=lambda c: cases[c]["us"])
+    pK, pN, pM = (int(x[1:]) for x in prof_case.split("_"))
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None, "kernel": dom_kernel,
+                "launches": dom_cases, "share_of_step": round(dom_us / tot, 3),
+                "bytes_per_launch": wbytes(pK, pN), "avg_launch_us": round(dom_us / len(dom_cases), 2),
+                "traffic_case": prof_case}
+    log(f"dominant kernel {dom_kernel}: {100 * dom_us / tot:.0f}% of the step, {achieved:.0f} GB/s")
+    del pools, X, Y
+    torch.cuda.empty_cache()
 
-            def launches(K=K, N=N, M=M, ws=ws, ss=ss, reps=reps):
-                for r in range(reps):
-                    hq.gemm(1, X[K][:M], ws[r % len(ws)], ss[r % len(ws)], N, GROUP, out=Y[(K, N)][:M])
-                return reps
-
-            us = graph_time_us(torch, stream, launches)
-            gbs = wbytes(K, N) / (us * 1e-6) / 1e9
-            cases[f"K{K}_N{N}_M{M}"] = {"us": round(us, 2), "GBps": round(gbs, 1),
-                                        "pct_hbm": round(100 * gbs / HBM_PEAK_GBS, 1)}
-    K, N, M = DOMINANT
-    dom = cases[f"K{K}_N{N}_M{M}"]
-    roofline = {"bound": "hbm", "achieved": dom["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(dom["GBps"] / HBM_PEAK_GBS, 4), "traffic": traffic_from_profile(),
-                "kernel": f"hq_decode_ls_kernel<int4,f16,KG=2,T=2,U=2>, K={K} N={N} M={M}",
-                "bytes_per_launch": wbytes(K, N), "avg_launch_us": dom["us"]}
+    # ---- the single W4A16 GEMM (M=16, K=N=4096) and the ternary bf16 decode ----
+    K, N = 4096, 4096
+    ws, ss = make_weights(hq, torch, K, N, n_copies(K, N))
+    Xs, Ys = torch.randn((16, K), device="cuda").half(), torch.empty((16, N), device="cuda", dtype=torch.float16)
+    cases["single_K4096_N4096_M16"] = time_case(FMT_INT4, K, N, 16, ws, ss, Xs, Ys)
+    del ws, ss
+    K, N = 5120, 27648
+    ws, ss = make_weights(hq, torch, K, N, n_copies(K, N, FMT_TERN), fmt=FMT_TERN)
+    Xt = torch.randn((8, K), device="cuda").to(torch.bfloat16)
+    Yt = torch.empty((8, N), device="cuda", dtype=torch.bfloat16)
+    for M in (1, 8):
+        cases[f"ternary_bf16_K{K}_N{N}_M{M}"] = time_case(FMT_TERN, K, N, M, ws, ss, Xt, Yt, dtype=2)
+    del ws, ss
+    torch.cuda.empty_cache()
 
     # ---- prefill and the split-fuse mixed batch ----
     prefill = None
     if not args.no_prefill:
         prefill = {}
         K, N = 5120, 27648
-        ws, ss = pools[(K, N)]
+        ws, ss = make_weights(hq, torch, K, N, 3)
         for M in (512, 2048, 4096):
             Xp = torch.randn((M, K), device="cuda").to(torch.float16)
             Yp = torch.empty((M, N), device="cuda", dtype=torch.float16)
 
             def launches(M=M, Xp=Xp, Yp=Yp):
-                for r in range(len(ws)):
-                    hq.gemm(1, Xp, ws[r], ss[r], N, GROUP, out=Yp)
-                return len(ws)
+                for r in range(6):
+                    hq.gemm(FMT_INT4, Xp, ws[r % 3], ss[r % 3], N, GROUP, out=Yp)
+                return 6
 
             us = graph_time_us(torch, stream, launches, reps=2)
             tf = 2.0 * M * K * N / (us * 1e-6) / 1e12
             prefill[f"M{M}"] = {"us": round(us, 1), "TFLOPs": round(tf, 1),
-                                "frac_mfma_f16": round(tf / MFMA_F16_PEAK_TFLOPS, 4)}
+                                "frac_mfma_f16": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
+                                "plan": hq.describe(FMT_INT4, 1, M, K, N, GROUP)}
             log(f"prefill M={M}: {us:.1f} us, {tf:.1f} TFLOP/s")
             del Xp, Yp
+        del ws, ss
         # mixed split-fuse batch: 1008 prefill rows + 16 decode rows, fused QKV (int4) and gate||up (ternary)
         M = 1024
         Xm = torch.randn((M, 5120), device="cuda").to(torch.float16)
@@ -247,9 +349,9 @@ def run_gpu(args):
             w, sc = make_weights(hq, torch, 5120, n, 1)
             qkv.append((w[0], sc[0], n))
         for n in (27648, 27648):
-            w, sc = make_weights(hq, torch, 5120, n, 1, fmt=2)
+            w, sc = make_weights(hq, torch, 5120, n, 1, fmt=FMT_TERN)
             gu.append((w[0], sc[0], n))
-        for name, fmt, seg_list in (("mixed_qkv_int4", 1, qkv), ("mixed_gate_up_ternary", 2, gu)):
+        for name, fmt, seg_list in (("mixed_qkv_int4", FMT_INT4, qkv), ("mixed_gate_up_ternary", FMT_TERN, gu)):
             outs = [torch.empty((M, n), device="cuda", dtype=torch.float16) for (_, _, n) in seg_list]
 
             def launches(fmt=fmt, seg_list=seg_list, outs=outs):
@@ -263,6 +365,9 @@ def run_gpu(args):
             prefill[name] = {"M": M, "N": ntot, "us": round(us, 1), "TFLOPs": round(tf, 1),
                              "frac_mfma_f16": round(tf / MFMA_F16_PEAK_TFLOPS, 4)}
             log(f"{name}: {us:.1f} us, {tf:.1f} TFLOP/s")
+        del Xm, qkv, gu
+        torch.cuda.empty_cache()
+
     # ---- GGUF TQ1_0 import (model load): blocks -> packed ternary tiles + scales on the device ----
     K, N = 5120, 27648
     nbytes = hq.tq1_0_bytes(K, N)
@@ -318,34 +423,62 @@ def run_gpu(args):
     return value, ms_per_step, roofline, cases, prefill, tq1, layer_res
 
 
-def run_cpu(budget_s: float = 10.0):
-    """The CPU oracle (restated reference path) over the same 15 GEMMs, repeated for ~budget_s."""
+# ---------------------------------------------------------------- CPU baseline
+def cpu_model() -> str:
+    fields = {}
+    try:
+        for ln in open("/proc/cpuinfo"):
+            k, _, v = ln.partition(":")
+            k = k.strip()
+            if k in ("model name", "cpu family", "model", "stepping") and k not in fields:
+                fields[k] = v.strip()
+    except OSError:
+        pass
+    name = fields.get("model name", "host CPU")
+    ident = ", ".join(f"{k} {fields[k]}" for k in ("cpu family", "model", "stepping") if k in fields)
+    return f"{name} ({ident})" if ident else name
+
+
+def run_cpu(reps: int = 5):
+    """The CPU oracle (restated reference path) over the 15 decode GEMMs: per shape the host
+    dequantisation (marlin_gemm.cu:495-512) once, then the fp32 matmul (:60-69) per M; each timed
+    `reps` times, medians summed."""
+    import numpy as np
+
     sys.path.insert(0, str(ROOT / "tests"))
     import oracle as O
 
     threads = min(int(os.environ.get("OMP_NUM_THREADS", "0")) or min(16, os.cpu_count() or 1), 16)
-    probs = {(K, N): O.Problem(O.INT4, 16, K, N, GROUP, O.F16, seed=7) for K, N in SHAPES}
-    done_bytes, t_used, sweeps = 0, 0.0, 0
-    while t_used < budget_s or sweeps == 0:
-        for K, N in SHAPES:
-            P = probs[(K, N)]
-            for M in MS:
+    os.environ["OMP_NUM_THREADS"] = str(threads)
+    dq_ms, mm_ms, total_s = {}, {}, 0.0
+    for K, N in SHAPES:
+        P = O.Problem(O.INT4, 16, K, N, GROUP, O.F16, seed=7)
+        Xf = O.to_f32(P.X, O.F16)
+        W = np.empty((K, N), dtype=np.float32)  # the reference's W_dequant buffer, allocated once
+        W.fill(1.0)  # touched, so that no timed run pays its page faults
+        t_dq = []
+        for _ in range(reps):
+            t = time.perf_counter()
+            O.dequant(O.INT4, P.W, P.scales.ravel(), K, N, GROUP, out=W)
+            t_dq.append(time.perf_counter() - t)
+        dq_ms[f"K{K}_N{N}"] = round(1e3 * statistics.median(t_dq), 2)
+        for M in MS:
+            t_mm = []
+            for _ in range(reps):
                 t = time.perf_counter()
-                O.qgemm(O.INT4, P.X[:M], O.F16, P.W, P.scales, N, GROUP, threads)
-                t_used += time.perf_counter() - t
-                done_bytes += wbytes(K, N)
-        sweeps += 1
-    cpu = "host CPU"
-    try:
-        for ln in open("/proc/cpuinfo"):
-            if ln.startswith("model name"):
-                cpu = ln.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
-    return {"value": round(done_bytes / t_used / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"{sweeps} pass(es) over the 15 decode GEMMs (dequantize-then-matmul, fp32, "
-                      f"{t_used:.1f} s) on {cpu}, {threads} threads of nproc={os.cpu_count()}"}
+                O.gemm_f32(np.ascontiguousarray(Xf[:M]), W, threads)
+                t_mm.append(time.perf_counter() - t)
+            mm_ms[f"K{K}_N{N}_M{M}"] = round(1e3 * statistics.median(t_mm), 2)
+            total_s += sum(t_mm)
+        total_s += sum(t_dq)
+        del W
+    sweep_s = (sum(dq_ms.values()) + sum(mm_ms.values())) / 1e3
+    step_bytes = sum(wbytes(K, N) for K, N in SHAPES for _ in MS)
+    return {"value": round(step_bytes / sweep_s / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": (f"the 15 decode GEMMs once each: per shape the host dequantisation, then the fp32 matmul "
+                       f"per M, each the median of {reps} runs ({total_s:.1f} s of CPU work) on {cpu_model()}, "
+                       f"{threads} OpenMP threads of nproc={os.cpu_count()}"),
+            "ms_per_sweep": round(1e3 * sweep_s, 1), "dequant_ms": dq_ms, "matmul_ms": mm_ms}
 
 
 def main():
@@ -355,8 +488,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
-    ap.add_argument("--cpu-budget", type=float, default=10.0)
+    ap.add_argument("--no-traffic", action="store_true")
+    ap.add_argument("--cpu-reps", type=int, default=5)
     ap.add_argument("--roofline-only", action="store_true")
+    ap.add_argument("--case", type=int, nargs=3, default=[5120, 27648, 16], metavar=("K", "N", "M"))
     ap.add_argument("--copy-bytes", type=int, default=0)
     ap.add_argument("--prefill-only", type=int, default=0)
     args = ap.parse_args()
@@ -374,10 +509,14 @@ def main():
         elif args.prefill_only:
             run_prefill_only(torch, hq, args.prefill_only)
         else:
-            run_roofline_only(torch, hq)
+            run_case_only(torch, hq, *args.case)
         return
     value, ms_per_step, roofline, cases, prefill, tq1, layer_res = run_gpu(args)
-    cpu = None if args.no_cpu else run_cpu(args.cpu_budget)
+    if not args.no_traffic:
+        K, N, M = (int(x[1:]) for x in roofline["traffic_case"].split("_"))
+        roofline["traffic"], roofline["traffic_note"] = measure_traffic(K, N, M, roofline["kernel"])
+        log(f"traffic of {roofline['kernel']} at K={K} N={N} M={M}: {roofline['traffic']} ({roofline['traffic_note']})")
+    cpu = None if args.no_cpu else run_cpu(args.cpu_reps)
     out = {
         "metric": "qGEMM GB/s at M<=16 (% of HBM peak) + TFLOP/s at M=2048 (% MFMA peak)",
         "value": round(value, 1),
@@ -397,11 +536,16 @@ def main():
                    "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 1)},
         "roofline": roofline,
         "cpu_baseline": cpu,
-        "prefill": prefill,
-        "tq1_0_import": tq1,
-        "decoder_layer": layer_res,
-        "cases": cases,
     }
+    if prefill:
+        p = prefill["M2048"]
+        out["prefill_M2048"] = {"TFLOPs": p["TFLOPs"], "frac_mfma_f16": p["frac_mfma_f16"], "us": p["us"],
+                                "workload": "W4A16 prefill M=2048 K=5120 N=27648 group 128 fp16"}
+        out["roofline_prefill"] = {"bound": "mfma", "achieved": p["TFLOPs"], "peak": MFMA_F16_PEAK_TFLOPS,
+                                   "unit": "TFLOP/s", "frac": p["frac_mfma_f16"], "traffic": None,
+                                   "kernel": kernel_of(p["plan"]), "flops_per_launch": 2 * 2048 * 5120 * 27648,
+                                   "avg_launch_us": p["us"]}
+    out.update({"prefill": prefill, "tq1_0_import": tq1, "decoder_layer": layer_res, "cases": cases})
     print(json.dumps(out), flush=True)
 
 

@@ -7,8 +7,10 @@
  * member it replaces. Differences from that surface, all required by the target
  * operator (fp16/bf16 activations, fp16 group scales, fp32 accumulation):
  *   - activations and outputs are fp16 or bf16 instead of fp32;
- *   - scales are fp16 [K/group][N]; the zero point is fixed at 8 for int4, which is
- *     the reference's bias = -8 * scale (marlin_gemm.cu:486-487), so no bias array;
+ *   - scales are fp16 [K/group][N]; the reference's per-group fp32 bias array
+ *     (marlin_gemm.hpp:100-107, w = q * scale + bias, marlin_gemm.cu:195-196, 506) is an
+ *     optional argument: NULL means the zero point 8 of the reference's own data
+ *     (bias = -8 * scale, marlin_gemm.cu:486-487);
  *   - M is given per call and may be any value >= 1 (the reference's buffers fix a
  *     maximum M and its kernels are only valid for M <= 8, marlin_gemm.cu:260);
  *   - every call takes an explicit stream and returns a status instead of throwing
@@ -30,7 +32,7 @@
 extern "C" {
 #endif
 
-#define HQ_ABI_VERSION 1
+#define HQ_ABI_VERSION 2
 
 typedef enum hq_status {
     HQ_OK = 0,
@@ -56,10 +58,13 @@ typedef enum hq_format {
 
 typedef void* hq_stream; /* hipStream_t */
 
-/* One projection of a fused call: its own packed weight, scales, width and output. */
+/* One projection of a fused call: its own packed weight, scales, optional bias, width and
+ * output. */
 typedef struct hq_segment {
     const uint32_t* Wp;     /* packed (hq_repack_*) weight, device */
     const uint16_t* scales; /* fp16 [K/group][N], device */
+    const float* bias;      /* int4 only: fp32 [K/group][N] per-group bias (weight q * scale + bias),
+                               device, 4-byte aligned; NULL: zero point 8 (weight (q - 8) * scale) */
     void* Y;                /* [M][ldy] output in the activation dtype, device */
     int64_t ldy;            /* elements, >= N */
     uint32_t N;
@@ -82,15 +87,32 @@ size_t hq_packed_words(hq_format fmt, uint32_t K, uint32_t N);
  * column tiles, prefill calls with few output tiles): a 256-byte aligned buffer,
  * zero-filled by the caller before its first use (every call leaves it zero-filled
  * again). Calls sharing one workspace must not overlap in time (same stream, or ordered
- * by events). For M > 80 the value is a bound that holds for every N and segment split;
- * for a decode hq_gemm_fused pass N = sum of the segments' N plus 16 per segment after
- * the first. Passing NULL instead makes the library use a
- * buffer of its own per (device, stream), allocated on first need outside stream
- * capture; a call that would need to allocate it during capture fails with
+ * by events). The value covers calls with and without a bias. For M > 80 it is a bound
+ * that holds for every N and segment split; for a fused call with M <= 80 use
+ * hq_workspace_bytes_fused, which plans the call's own segment list. Passing NULL instead
+ * makes the library use a buffer of its own per (device, stream), allocated on first need
+ * outside stream capture; a call that would need to allocate it during capture fails with
  * HQ_ERR_WORKSPACE. The reference has no workspace: it allocates inside
  * MarlinGemmEngine (marlin_gemm.cu:381-416). */
 hq_status hq_workspace_bytes(hq_format fmt, uint32_t M, uint32_t K, uint32_t N, uint32_t group,
                              size_t* bytes);
+/* The workspace of one hq_gemm_fused call: Ns[0..nseg) are its segments' widths, with_bias
+ * whether any segment has a bias. Exactly what that call asks for (the same planning). */
+hq_status hq_workspace_bytes_fused(hq_format fmt, uint32_t M, uint32_t K, uint32_t group,
+                                   const uint32_t* Ns, uint32_t nseg, int with_bias, size_t* bytes);
+/* The plan a GEMM call of this shape runs on the current device, as text: kernel, tiling and
+ * grid (for benchmarks and tests; no counterpart in the reference). Writes at most buf_len
+ * bytes including the terminating zero. */
+hq_status hq_describe_gemm(hq_format fmt, hq_dtype dtype, uint32_t M, uint32_t K, uint32_t N,
+                           uint32_t group, int with_bias, char* buf, size_t buf_len);
+/* Faults that kernels report after their launch returned: a bounded wait inside a kernel
+ * (the lockstep decode kernel's k-group barrier) that gave up sets a host-visible fault
+ * word, and that launch's outputs are wrong. This call waits for `stream`, then returns
+ * HQ_ERR_DEVICE (and clears the word) if one was reported since the last check, HQ_OK
+ * otherwise. Every hq_gemm_* call also checks the word first and fails with HQ_ERR_DEVICE
+ * if it is set. The reference has no such waits (it reports launch errors only,
+ * marlin_gemm.cu:600). */
+hq_status hq_device_status(hq_stream stream);
 
 /* ---- repack: replaces MarlinGemmEngine::repack_q4k_to_marlin (marlin_gemm.hpp:78-83) ---- */
 
@@ -140,16 +162,23 @@ hq_status hq_repack_tq1_0_device(const void* d_blocks, uint32_t K, uint32_t N, u
  * Y[m, n] = sum_k X[m, k] * w(k, n), fp32 accumulation, Y rounded to the activation dtype.
  * X: [M][ldx] fp16/bf16, 16-byte aligned, ldx % 8 == 0, ldx >= K.
  * Wp: gfx950 packed weight, 16-byte aligned. scales: fp16 [K/group][N].
+ * bias (int4): NULL, or fp32 [K/group][N], 4-byte aligned: w = q * scale + bias as in the
+ *   reference (marlin_gemm.cu:195-196); NULL gives w = (q - 8) * scale.
  * Y: [M][ldy], 2-byte aligned, ldy >= N; written in full (no zero-fill needed).
- * K % 128 == 0, group % 128 == 0, K % group == 0, M >= 1, N >= 1.
+ * K % 128 == 0, group % 32 == 0, K % group == 0, M >= 1, N >= 1 (the reference takes a
+ *   group per 32-wide k chunk, marlin_gemm.cu:191-193). Groups that are multiples of 128
+ *   without a bias run the fastest kernels; other groups and biased calls run kernels that
+ *   apply one scale (and bias) per 32-wide k chunk.
  * workspace / workspace_bytes: see hq_workspace_bytes (NULL, 0 is always accepted).
  * Up to M = 80 (decode steps, split-fuse steps of decode tokens and a prefill chunk) the
  * HBM-streaming kernels run; larger M the MFMA tile kernel.
  * Results are deterministic: repeated calls with the same shapes give identical bits. */
 hq_status hq_gemm_w4a16(const void* X, hq_dtype dtype, int64_t ldx, const uint32_t* Wp,
-                        const uint16_t* scales, void* Y, int64_t ldy, uint32_t M, uint32_t K,
-                        uint32_t N, uint32_t group, void* workspace, size_t workspace_bytes,
+                        const uint16_t* scales, const float* bias, void* Y, int64_t ldy, uint32_t M,
+                        uint32_t K, uint32_t N, uint32_t group, void* workspace, size_t workspace_bytes,
                         hq_stream stream);
+/* Ternary weights (value semantics of kernel_gemv_tq1_0, native_decoder.cu:155-206): the same
+ * contract without a bias; a group whose scale is not finite contributes nothing. */
 hq_status hq_gemm_w2a16(const void* X, hq_dtype dtype, int64_t ldx, const uint32_t* Wp,
                         const uint16_t* scales, void* Y, int64_t ldy, uint32_t M, uint32_t K,
                         uint32_t N, uint32_t group, void* workspace, size_t workspace_bytes,

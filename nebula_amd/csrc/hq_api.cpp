@@ -16,6 +16,7 @@
 
 #include "hq_internal.hpp"
 #include "hq_layout.hpp"
+#include "hq_plan.hpp"
 #include "hq_qgemm.h"
 
 namespace {
@@ -125,10 +126,11 @@ hq_status get_internal_ws(hipStream_t stream, size_t need, void** out) {
 // which fetches each activation k-block once per workgroup, is, and above 16 rows only the
 // lockstep kernel takes them. With ternary weights the lockstep kernel's
 // four-k-group configuration is faster from one row on (5120 x 27648 at M = 1: 12.8 us
-// against 14.7 us), so it is taken whenever the lockstep planner picks it.
+// against 14.7 us), so it is taken whenever the lockstep planner picks it. The general
+// kernels (bias, groups that are not multiples of 128) exist in the lockstep family only.
 // HQ_DECODE_KERNEL=0 / 1 forces one of them for M <= 16 (tuning and tests).
 bool use_lockstep(int fmt, const hq::GemmDesc& d) {
-  if (d.M > 16) return true;  // only the lockstep kernel takes several row tiles
+  if (d.M > 16 || d.gen) return true;  // only the lockstep kernel takes several row tiles
   const char* v = std::getenv("HQ_DECODE_KERNEL");
   if (v && *v) return std::atoi(v) != 0;
   if (d.M >= 5) return true;
@@ -146,16 +148,29 @@ uint32_t decode_max_m() {
   return e >= 16 && (uint32_t)e <= top ? (uint32_t)e : top;
 }
 
-// Validation shared by the GEMM entry points.
-hq_status check_gemm_common(const void* X, int dtype, int64_t ldx, uint32_t M, uint32_t K,
-                            uint32_t group) {
-  if (!X) return fail(HQ_ERR_INVALID_ARG, "X is null");
-  if (!valid_dtype(dtype)) return fail(HQ_ERR_INVALID_ARG, "unknown dtype %d", dtype);
+// The general kernels on request for groups and calls the fast kernels also take (tests
+// compare the two): HQ_GENERAL=1.
+bool force_general() {
+  const char* v = std::getenv("HQ_GENERAL");
+  return v && *v && std::atoi(v) != 0;
+}
+
+// Shape validation shared by the GEMM entry points and the workspace queries.
+hq_status check_shape(int fmt, uint32_t M, uint32_t K, uint32_t group, bool bias) {
+  if (!valid_fmt(fmt)) return fail(HQ_ERR_INVALID_ARG, "unknown format %d", fmt);
   if (M == 0) return fail(HQ_ERR_SHAPE, "M must be >= 1");
   if (K == 0 || K % hq::kBlockK) return fail(HQ_ERR_SHAPE, "K=%u must be a positive multiple of 128", K);
-  if (group == 0 || group % hq::kBlockK)
-    return fail(HQ_ERR_SHAPE, "group=%u must be a positive multiple of 128", group);
+  if (group == 0 || group % 32)
+    return fail(HQ_ERR_SHAPE, "group=%u must be a positive multiple of 32", group);
   if (K % group) return fail(HQ_ERR_SHAPE, "K=%u must be a multiple of group=%u", K, group);
+  if (bias && fmt != HQ_FORMAT_INT4) return fail(HQ_ERR_UNSUPPORTED, "a bias is supported for int4 weights only");
+  return HQ_OK;
+}
+
+// Validation of the activation operand.
+hq_status check_x(const void* X, int dtype, int64_t ldx, uint32_t K) {
+  if (!X) return fail(HQ_ERR_INVALID_ARG, "X is null");
+  if (!valid_dtype(dtype)) return fail(HQ_ERR_INVALID_ARG, "unknown dtype %d", dtype);
   if (ldx < (int64_t)K) return fail(HQ_ERR_SHAPE, "ldx=%lld < K=%u", (long long)ldx, K);
   if (ldx % 8) return fail(HQ_ERR_ALIGNMENT, "ldx=%lld must be a multiple of 8 elements", (long long)ldx);
   if (reinterpret_cast<uintptr_t>(X) % 16) return fail(HQ_ERR_ALIGNMENT, "X must be 16-byte aligned");
@@ -168,75 +183,199 @@ hq_status check_segment(const hq_segment& s, uint32_t i) {
   if (s.ldy < (int64_t)s.N) return fail(HQ_ERR_SHAPE, "segment %u: ldy=%lld < N=%u", i, (long long)s.ldy, s.N);
   if (reinterpret_cast<uintptr_t>(s.Wp) % 16) return fail(HQ_ERR_ALIGNMENT, "segment %u: Wp must be 16-byte aligned", i);
   if (reinterpret_cast<uintptr_t>(s.scales) % 2) return fail(HQ_ERR_ALIGNMENT, "segment %u: scales must be 2-byte aligned", i);
+  if (reinterpret_cast<uintptr_t>(s.bias) % 4) return fail(HQ_ERR_ALIGNMENT, "segment %u: bias must be 4-byte aligned", i);
   if (reinterpret_cast<uintptr_t>(s.Y) % 2) return fail(HQ_ERR_ALIGNMENT, "segment %u: Y must be 2-byte aligned", i);
   return HQ_OK;
+}
+
+// Descriptor of a call from its shape (pointers filled by the caller when it has them).
+hq::GemmDesc make_desc(uint32_t M, uint32_t K, uint32_t group, const uint32_t* Ns, uint32_t nseg, bool bias) {
+  hq::GemmDesc d{};
+  d.M = M;
+  d.K = K;
+  d.nkb = K / hq::kBlockK;
+  d.gkb = group % hq::kBlockK == 0 ? group / hq::kBlockK : 1u;
+  d.nseg = nseg;
+  d.gen = (bias || group % hq::kBlockK != 0 || force_general()) ? 1u : 0u;
+  d.g32 = group / 32u;
+  d.g32_m = hq::plan_div_magic(d.g32);
+  d.has_bias = bias ? 1u : 0u;
+  for (uint32_t i = 0; i < nseg; ++i) {
+    d.seg[i].N = Ns[i];
+    d.seg[i].lds = Ns[i];
+    d.seg[i].ntiles = hq::col_tiles(Ns[i]);
+  }
+  return d;
+}
+
+// What a call runs: the kernel family, its tiling and the workspace it needs.
+enum class Kind { kDecode, kLockstep, kPrefill };
+struct Plan {
+  Kind kind;
+  hq::DecodeConfig c{};
+  hq::LsConfig lc{};
+  hq::PrefillConfig pc{};
+  size_t need = 0;
+};
+
+Plan make_plan(int fmt, const hq::GemmDesc& d) {
+  Plan p{};
+  if (d.M > decode_max_m()) {
+    p.kind = Kind::kPrefill;
+    p.pc = hq::choose_prefill(fmt, d);
+    p.need = hq::prefill_workspace_bytes(d, p.pc);
+  } else if (use_lockstep(fmt, d)) {
+    p.kind = Kind::kLockstep;
+    p.lc = hq::choose_decode_ls(fmt, d);
+    p.need = hq::decode_ls_workspace_bytes(d, p.lc);
+  } else {
+    p.kind = Kind::kDecode;
+    p.c = hq::choose_decode(fmt, d);
+    p.need = hq::decode_workspace_bytes(d, p.c);
+  }
+  return p;
+}
+
+// Host-visible fault word of kernels whose bounded waits gave up (pinned, mapped host
+// memory, one word for every device; allocated on the first call outside stream capture).
+struct FaultWord {
+  std::mutex mu;
+  uint32_t* host = nullptr;  // also the device address (unified addressing)
+};
+FaultWord& fault_word() {
+  static FaultWord* f = new FaultWord();  // never destroyed: kernels may still write it
+  return *f;
+}
+uint32_t* fault_ptr(hipStream_t s) {
+  FaultWord& f = fault_word();
+  std::lock_guard<std::mutex> lock(f.mu);
+  if (f.host) return f.host;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &cap) != hipSuccess || cap != hipStreamCaptureStatusNone) return nullptr;
+  void* p = nullptr;
+  if (hipHostMalloc(&p, 256, hipHostMallocMapped | hipHostMallocPortable | hipHostMallocCoherent) != hipSuccess) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  std::memset(p, 0, 256);
+  void* dp = nullptr;
+  if (hipHostGetDevicePointer(&dp, p, 0) != hipSuccess || dp != p) {
+    (void)hipGetLastError();
+    (void)hipHostFree(p);
+    return nullptr;
+  }
+  f.host = static_cast<uint32_t*>(p);
+  return f.host;
+}
+// Reads and clears the fault word: true if a kernel reported a fault since the last check.
+bool take_fault() {
+  FaultWord& f = fault_word();
+  uint32_t* w = __atomic_load_n(&f.host, __ATOMIC_ACQUIRE);
+  if (!w) return false;
+  return __atomic_exchange_n(w, 0u, __ATOMIC_ACQ_REL) != 0u;
+}
+hq_status fault_status() {
+  return fail(HQ_ERR_DEVICE,
+              "a lockstep decode launch gave up waiting at its k-group barrier: the outputs of that launch "
+              "are wrong (fault word reported by the device)");
+}
+uint32_t ls_spin() {
+  const char* v = std::getenv("HQ_DECODE_LS_SPIN");  // tests: a small limit forces the fault path
+  return v && *v ? (uint32_t)std::strtoul(v, nullptr, 10) : hq::kLsSpinLimit;
 }
 
 hq_status run_gemm(const void* X, hq_dtype dtype, int64_t ldx, hq_format fmt, const hq_segment* segs,
                    uint32_t nseg, uint32_t M, uint32_t K, uint32_t group, void* ws, size_t ws_bytes,
                    hq_stream stream) {
-  hq_status st = check_gemm_common(X, dtype, ldx, M, K, group);
-  if (st != HQ_OK) return st;
-  if (!valid_fmt(fmt)) return fail(HQ_ERR_INVALID_ARG, "unknown format %d", (int)fmt);
+  if (take_fault()) return fault_status();
   if (!segs || nseg == 0 || nseg > HQ_MAX_SEGMENTS)
     return fail(HQ_ERR_INVALID_ARG, "need 1..%d segments, got %u", HQ_MAX_SEGMENTS, nseg);
-  hq::GemmDesc d{};
-  d.X = X;
-  d.ldx = ldx;
-  d.M = M;
-  d.K = K;
-  d.nkb = K / hq::kBlockK;
-  d.gkb = group / hq::kBlockK;
-  d.nseg = nseg;
+  bool bias = false;
+  uint32_t Ns[HQ_MAX_SEGMENTS];
+  hq_status st;
   for (uint32_t i = 0; i < nseg; ++i) {
     if ((st = check_segment(segs[i], i)) != HQ_OK) return st;
+    bias |= segs[i].bias != nullptr;
+    Ns[i] = segs[i].N;
+  }
+  if ((st = check_shape(fmt, M, K, group, bias)) != HQ_OK) return st;
+  if ((st = check_x(X, dtype, ldx, K)) != HQ_OK) return st;
+  hq::GemmDesc d = make_desc(M, K, group, Ns, nseg, bias);
+  if (d.gen && !hq::kGeneralKernels)
+    return fail(HQ_ERR_UNSUPPORTED, "group=%u%s needs the general kernels, which this build lacks", group,
+                bias ? " with a bias" : "");
+  d.X = X;
+  d.ldx = ldx;
+  for (uint32_t i = 0; i < nseg; ++i) {
     d.seg[i].Wp = segs[i].Wp;
     d.seg[i].S = segs[i].scales;
+    d.seg[i].B = segs[i].bias;
     d.seg[i].Y = segs[i].Y;
     d.seg[i].ldy = segs[i].ldy;
-    d.seg[i].N = segs[i].N;
-    d.seg[i].lds = segs[i].N;
-    d.seg[i].ntiles = hq::col_tiles(segs[i].N);
   }
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const bool prefill = M > decode_max_m();
-  const bool lockstep = !prefill && use_lockstep(fmt, d);
-  hq::LsConfig lc{};
-  hq::DecodeConfig c{};
-  hq::PrefillConfig pc{};
-  size_t need = 0;
-  if (prefill) {
-    pc = hq::choose_prefill(fmt, d);
-    need = hq::prefill_workspace_bytes(d, pc);
-  } else if (lockstep) {
-    lc = hq::choose_decode_ls(fmt, d);
-    need = hq::decode_ls_workspace_bytes(d, lc);
-  } else {
-    c = hq::choose_decode(fmt, d);
-    need = hq::decode_workspace_bytes(d, c);
-  }
+  const Plan p = make_plan(fmt, d);
   void* w = nullptr;
-  if (need > 0) {
+  if (p.need > 0) {
     if (ws) {
-      if (ws_bytes < need)
-        return fail(HQ_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu this call needs", ws_bytes, need);
+      if (ws_bytes < p.need)
+        return fail(HQ_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu this call needs", ws_bytes, p.need);
       if (reinterpret_cast<uintptr_t>(ws) % 256)
         return fail(HQ_ERR_ALIGNMENT, "workspace must be 256-byte aligned");
       w = ws;
-    } else if ((st = get_internal_ws(s, need, &w)) != HQ_OK) {
+    } else if ((st = get_internal_ws(s, p.need, &w)) != HQ_OK) {
       return st;
     }
   }
-  if (prefill) return from_hip(hq::launch_prefill(fmt, dtype, pc, w, s), "prefill launch");
-  if (lockstep) return from_hip(hq::launch_decode_ls(fmt, dtype, d, lc, w, s), "decode launch");
-  return from_hip(hq::launch_decode(fmt, dtype, d, c, w, s), "decode launch");
+  switch (p.kind) {
+    case Kind::kPrefill: return from_hip(hq::launch_prefill(fmt, dtype, p.pc, w, s), "prefill launch");
+    case Kind::kLockstep:
+      return from_hip(hq::launch_decode_ls(fmt, dtype, d, p.lc, w, fault_ptr(s), ls_spin(), s), "decode launch");
+    case Kind::kDecode: break;
+  }
+  return from_hip(hq::launch_decode(fmt, dtype, d, p.c, w, s), "decode launch");
+}
+
+const char* fmt_name(int fmt) { return fmt == HQ_FORMAT_INT4 ? "int4" : "ternary2"; }
+const char* dt_name(int dt) { return dt == HQ_DTYPE_F16 ? "f16" : "bf16"; }
+
+// Ring depth the per-wavefront launcher instantiates for slab width T (and an override U).
+int decode_ring(int T, int U) {
+  if (T == 8) return U == 3 ? 3 : 2;
+  if (T == 4 || T == 2) return (U == 2 || U == 4) ? U : 3;
+  return 4;
+}
+
+std::string describe(int fmt, int dtype, const hq::GemmDesc& d, const Plan& p) {
+  char b[512];
+  if (p.kind == Kind::kDecode) {
+    std::snprintf(b, sizeof b, "hq_decode_kernel<%s,%s,T=%d,U=%d> workgroups=%d x %d wavefronts%s%s ws=%zu",
+                  fmt_name(fmt), dt_name(dtype), p.c.T, decode_ring(p.c.T, p.c.U), p.c.SK, p.c.WK,
+                  p.c.G ? " variable-width slabs" : "", p.need ? " cut slabs (fix-up)" : "", p.need);
+  } else if (p.kind == Kind::kLockstep) {
+    std::snprintf(b, sizeof b,
+                  "hq_decode_ls_kernel<%s,%s,KG=%d,GW=%d,T=%d,U=%d,MT=%d%s> grid=%d pieces x slabs of %d tiles, "
+                  "%d wavefronts ws=%zu",
+                  fmt_name(fmt), dt_name(dtype), p.lc.KG, p.lc.GW, p.lc.T, p.lc.U, p.lc.MT, d.gen ? ",general" : "",
+                  p.lc.S, p.lc.SW, p.lc.KG * p.lc.GW, p.need);
+  } else {
+    int n = std::snprintf(b, sizeof b, "hq_prefill_kernel<%s,%s%s>", fmt_name(fmt), dt_name(dtype),
+                          d.gen ? ",general" : "");
+    for (int i = 0; i < p.pc.n && n > 0 && (size_t)n < sizeof b; ++i) {
+      const hq::PrefillLaunch& l = p.pc.l[i];
+      n += std::snprintf(b + n, sizeof b - n, "%s launch %d: %u-row tiles=%u whole=%u stream-K workgroups=%u",
+                         i ? ";" : "", i, 16u * l.RT * l.WM, l.tiles, l.dp, l.psk);
+    }
+    if (n > 0 && (size_t)n < sizeof b) std::snprintf(b + n, sizeof b - n, " ws=%zu", p.need);
+  }
+  return b;
 }
 
 }  // namespace
 
 extern "C" {
 
-const char* hq_version(void) { return "nebula-hq 0.1.0 (gfx950)"; }
+const char* hq_version(void) { return "nebula-hq 0.2.0 (gfx950, ABI 2)"; }
 
 const char* hq_last_error(void) { return g_last_error.c_str(); }
 
@@ -268,25 +407,51 @@ size_t hq_packed_words(hq_format fmt, uint32_t K, uint32_t N) {
 
 hq_status hq_workspace_bytes(hq_format fmt, uint32_t M, uint32_t K, uint32_t N, uint32_t group, size_t* bytes) {
   if (!bytes) return fail(HQ_ERR_INVALID_ARG, "bytes is null");
-  if (!valid_fmt(fmt)) return fail(HQ_ERR_INVALID_ARG, "unknown format %d", (int)fmt);
-  if (M == 0 || N == 0 || K == 0 || K % hq::kBlockK || group == 0 || group % hq::kBlockK || K % group)
-    return fail(HQ_ERR_SHAPE, "bad shape M=%u K=%u N=%u group=%u", M, K, N, group);
+  hq_status st = check_shape(fmt, M, K, group, false);
+  if (st != HQ_OK) return st;
+  if (N == 0) return fail(HQ_ERR_SHAPE, "N must be >= 1");
   *bytes = 0;
   if (M > decode_max_m()) {
     *bytes = hq::prefill_workspace_bound(fmt, M, K / hq::kBlockK);
     return ok();
   }
-  hq::GemmDesc d{};
-  d.M = M;
-  d.K = K;
-  d.nkb = K / hq::kBlockK;
-  d.gkb = group / hq::kBlockK;
-  d.nseg = 1;
-  d.seg[0].N = N;
-  d.seg[0].lds = N;
-  d.seg[0].ntiles = hq::col_tiles(N);
-  *bytes = use_lockstep(fmt, d) ? hq::decode_ls_workspace_bytes(d, hq::choose_decode_ls(fmt, d))
-                          : hq::decode_workspace_bytes(d, hq::choose_decode(fmt, d));
+  // The larger of the plans without and (int4) with a bias.
+  for (int b = 0; b < (fmt == HQ_FORMAT_INT4 ? 2 : 1); ++b) {
+    const hq::GemmDesc d = make_desc(M, K, group, &N, 1, b != 0);
+    *bytes = std::max(*bytes, make_plan(fmt, d).need);
+  }
+  return ok();
+}
+
+hq_status hq_workspace_bytes_fused(hq_format fmt, uint32_t M, uint32_t K, uint32_t group, const uint32_t* Ns,
+                                   uint32_t nseg, int with_bias, size_t* bytes) {
+  if (!bytes || !Ns) return fail(HQ_ERR_INVALID_ARG, "null pointer");
+  if (nseg == 0 || nseg > HQ_MAX_SEGMENTS) return fail(HQ_ERR_INVALID_ARG, "need 1..%d segments, got %u", HQ_MAX_SEGMENTS, nseg);
+  hq_status st = check_shape(fmt, M, K, group, with_bias != 0);
+  if (st != HQ_OK) return st;
+  for (uint32_t i = 0; i < nseg; ++i)
+    if (Ns[i] == 0) return fail(HQ_ERR_SHAPE, "segment %u: N must be >= 1", i);
+  *bytes = make_plan(fmt, make_desc(M, K, group, Ns, nseg, with_bias != 0)).need;
+  return ok();
+}
+
+hq_status hq_describe_gemm(hq_format fmt, hq_dtype dtype, uint32_t M, uint32_t K, uint32_t N, uint32_t group,
+                           int with_bias, char* buf, size_t buf_len) {
+  if (!buf || buf_len == 0) return fail(HQ_ERR_INVALID_ARG, "buf is null or empty");
+  if (!valid_dtype(dtype)) return fail(HQ_ERR_INVALID_ARG, "unknown dtype %d", (int)dtype);
+  hq_status st = check_shape(fmt, M, K, group, with_bias != 0);
+  if (st != HQ_OK) return st;
+  if (N == 0) return fail(HQ_ERR_SHAPE, "N must be >= 1");
+  const hq::GemmDesc d = make_desc(M, K, group, &N, 1, with_bias != 0);
+  const std::string s = describe(fmt, dtype, d, make_plan(fmt, d));
+  std::snprintf(buf, buf_len, "%s", s.c_str());
+  return ok();
+}
+
+hq_status hq_device_status(hq_stream stream) {
+  hipError_t e = hipStreamSynchronize(reinterpret_cast<hipStream_t>(stream));
+  if (e != hipSuccess) return from_hip(e, "hipStreamSynchronize");
+  if (take_fault()) return fault_status();
   return ok();
 }
 
@@ -456,16 +621,16 @@ hq_status hq_repack_ternary2_device(const uint32_t* src, uint32_t* dst, uint32_t
 }
 
 hq_status hq_gemm_w4a16(const void* X, hq_dtype dtype, int64_t ldx, const uint32_t* Wp, const uint16_t* scales,
-                        void* Y, int64_t ldy, uint32_t M, uint32_t K, uint32_t N, uint32_t group, void* ws,
-                        size_t ws_bytes, hq_stream stream) {
-  hq_segment s{Wp, scales, Y, ldy, N};
+                        const float* bias, void* Y, int64_t ldy, uint32_t M, uint32_t K, uint32_t N, uint32_t group,
+                        void* ws, size_t ws_bytes, hq_stream stream) {
+  hq_segment s{Wp, scales, bias, Y, ldy, N};
   return run_gemm(X, dtype, ldx, HQ_FORMAT_INT4, &s, 1, M, K, group, ws, ws_bytes, stream);
 }
 
 hq_status hq_gemm_w2a16(const void* X, hq_dtype dtype, int64_t ldx, const uint32_t* Wp, const uint16_t* scales,
                         void* Y, int64_t ldy, uint32_t M, uint32_t K, uint32_t N, uint32_t group, void* ws,
                         size_t ws_bytes, hq_stream stream) {
-  hq_segment s{Wp, scales, Y, ldy, N};
+  hq_segment s{Wp, scales, nullptr, Y, ldy, N};
   return run_gemm(X, dtype, ldx, HQ_FORMAT_TERNARY2, &s, 1, M, K, group, ws, ws_bytes, stream);
 }
 

@@ -315,7 +315,9 @@ __global__ void __launch_bounds__(64 * KG * GW, KG == 1 && MT > 1 ? 2 : 1)
   // arrival count: each wavefront adds one after writing its activation rows (LDS
   // executes a wavefront's operations in order) and waits until all four have arrived.
   // The wait is bounded: every wavefront executes the same steps, so the bound is never
-  // reached by a correct launch, and a wrong one cannot hang the GPU.
+  // reached by a correct launch, and a wrong one cannot hang the GPU. A wavefront that gives
+  // up sets the host-visible fault word (the host reports it as HQ_ERR_DEVICE) and carries
+  // on, so every wavefront still reaches the end of the kernel.
   const uint32_t arr = (uint32_t)(uintptr_t)&kg_arrived[kg];
   const uint32_t arr_next = (uint32_t)(uintptr_t)&kg_arrived[(kg + 1u) % KG];
   if constexpr (KG > 1) {
@@ -330,10 +332,16 @@ __global__ void __launch_bounds__(64 * KG * GW, KG == 1 && MT > 1 ? 2 : 1)
     } else {
       arrivals += GW;
       if (lane == 0) ls_lds_add_u32(arr, 1u);
-      for (uint32_t spin = 0; spin < (1u << 22); ++spin) {
-        if (__builtin_amdgcn_readfirstlane(ls_lds_read_u32_sync(arr)) >= arrivals) break;
+      bool met = false;
+      for (uint32_t spin = 0; spin < pl.spin; ++spin) {
+        if (__builtin_amdgcn_readfirstlane(ls_lds_read_u32_sync(arr)) >= arrivals) {
+          met = true;
+          break;
+        }
         __builtin_amdgcn_s_sleep(1);
       }
+      if (!met && lane == 0 && pl.fault)
+        __hip_atomic_store(pl.fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
       // The SIMD arbiter favours older wavefronts, which would let k-group 0 run ahead
       // and leave k-group 1 streaming alone at the end: a k-group behind the one after
       // it (cyclically) raises its issue priority until it catches up.
@@ -493,10 +501,12 @@ uint32_t ls_assign_slabs(GemmDesc& d, uint32_t sw) {
 }
 
 template <int FMT, int DT, int KG, int GW, int T, int U, int MT>
-hipError_t ls_launch_t(GemmDesc d, const LsConfig& c, void* ws, hipStream_t stream) {
+hipError_t ls_launch_t(GemmDesc d, const LsConfig& c, void* ws, uint32_t* fault, uint32_t spin, hipStream_t stream) {
   const bool fused = d.nseg > 1;
   if (d.M > 16u * MT) return hipErrorInvalidValue;
   LsPlan pl{};
+  pl.fault = fault;
+  pl.spin = spin;
   if (c.SW < 1 || c.SW > GW * T) return hipErrorInvalidValue;
   pl.sw = (uint32_t)c.SW;
   const uint32_t G = ls_assign_slabs(d, pl.sw);
@@ -524,36 +534,37 @@ hipError_t ls_launch_t(GemmDesc d, const LsConfig& c, void* ws, hipStream_t stre
 }
 
 template <int FMT, int DT>
-hipError_t ls_launch_fd(const GemmDesc& d, const LsConfig& c, void* ws, hipStream_t stream) {
+hipError_t ls_launch_fd(const GemmDesc& d, const LsConfig& c, void* ws, uint32_t* fault, uint32_t spin,
+                        hipStream_t stream) {
   if (c.MT > 1 && c.KG == 1) {  // one k-group, two workgroups per CU
     if (c.GW * 1000 + c.KG * 100 + c.T * 10 + c.U != 4122) return hipErrorInvalidConfiguration;
     switch (c.MT) {
-      case 2: return ls_launch_t<FMT, DT, 1, 4, 2, 2, 2>(d, c, ws, stream);
-      case 3: return ls_launch_t<FMT, DT, 1, 4, 2, 2, 3>(d, c, ws, stream);
-      case 4: return ls_launch_t<FMT, DT, 1, 4, 2, 2, 4>(d, c, ws, stream);
-      case 5: return ls_launch_t<FMT, DT, 1, 4, 2, 2, 5>(d, c, ws, stream);
+      case 2: return ls_launch_t<FMT, DT, 1, 4, 2, 2, 2>(d, c, ws, fault, spin, stream);
+      case 3: return ls_launch_t<FMT, DT, 1, 4, 2, 2, 3>(d, c, ws, fault, spin, stream);
+      case 4: return ls_launch_t<FMT, DT, 1, 4, 2, 2, 4>(d, c, ws, fault, spin, stream);
+      case 5: return ls_launch_t<FMT, DT, 1, 4, 2, 2, 5>(d, c, ws, fault, spin, stream);
       default: return hipErrorInvalidConfiguration;
     }
   }
   if (c.MT > 1) {  // several row tiles: two k-groups of four wavefronts, two tiles each, two steps in flight
     if (c.GW * 1000 + c.KG * 100 + c.T * 10 + c.U != 4222) return hipErrorInvalidConfiguration;
     switch (c.MT) {
-      case 2: return ls_launch_t<FMT, DT, 2, 4, 2, 2, 2>(d, c, ws, stream);
-      case 3: return ls_launch_t<FMT, DT, 2, 4, 2, 2, 3>(d, c, ws, stream);
-      case 4: return ls_launch_t<FMT, DT, 2, 4, 2, 2, 4>(d, c, ws, stream);
-      case 5: return ls_launch_t<FMT, DT, 2, 4, 2, 2, 5>(d, c, ws, stream);
+      case 2: return ls_launch_t<FMT, DT, 2, 4, 2, 2, 2>(d, c, ws, fault, spin, stream);
+      case 3: return ls_launch_t<FMT, DT, 2, 4, 2, 2, 3>(d, c, ws, fault, spin, stream);
+      case 4: return ls_launch_t<FMT, DT, 2, 4, 2, 2, 4>(d, c, ws, fault, spin, stream);
+      case 5: return ls_launch_t<FMT, DT, 2, 4, 2, 2, 5>(d, c, ws, fault, spin, stream);
       default: return hipErrorInvalidConfiguration;
     }
   }
   switch (c.GW * 1000 + c.KG * 100 + c.T * 10 + c.U) {
-    case 4124: return ls_launch_t<FMT, DT, 1, 4, 2, 4, 1>(d, c, ws, stream);
-    case 4214: return ls_launch_t<FMT, DT, 2, 4, 1, 4, 1>(d, c, ws, stream);
-    case 4222: return ls_launch_t<FMT, DT, 2, 4, 2, 2, 1>(d, c, ws, stream);
-    case 4223: return ls_launch_t<FMT, DT, 2, 4, 2, 3, 1>(d, c, ws, stream);
-    case 4242: return ls_launch_t<FMT, DT, 2, 4, 4, 2, 1>(d, c, ws, stream);
-    case 4413: return ls_launch_t<FMT, DT, 4, 4, 1, 3, 1>(d, c, ws, stream);
-    case 4422: return ls_launch_t<FMT, DT, 4, 4, 2, 2, 1>(d, c, ws, stream);
-    case 4423: return ls_launch_t<FMT, DT, 4, 4, 2, 3, 1>(d, c, ws, stream);
+    case 4124: return ls_launch_t<FMT, DT, 1, 4, 2, 4, 1>(d, c, ws, fault, spin, stream);
+    case 4214: return ls_launch_t<FMT, DT, 2, 4, 1, 4, 1>(d, c, ws, fault, spin, stream);
+    case 4222: return ls_launch_t<FMT, DT, 2, 4, 2, 2, 1>(d, c, ws, fault, spin, stream);
+    case 4223: return ls_launch_t<FMT, DT, 2, 4, 2, 3, 1>(d, c, ws, fault, spin, stream);
+    case 4242: return ls_launch_t<FMT, DT, 2, 4, 4, 2, 1>(d, c, ws, fault, spin, stream);
+    case 4413: return ls_launch_t<FMT, DT, 4, 4, 1, 3, 1>(d, c, ws, fault, spin, stream);
+    case 4422: return ls_launch_t<FMT, DT, 4, 4, 2, 2, 1>(d, c, ws, fault, spin, stream);
+    case 4423: return ls_launch_t<FMT, DT, 4, 4, 2, 3, 1>(d, c, ws, fault, spin, stream);
     default: return hipErrorInvalidConfiguration;
   }
 }
@@ -624,13 +635,14 @@ size_t decode_ls_workspace_bytes(const GemmDesc& d, const LsConfig& c) {
   return kCounterBytes + (size_t)G * c.S * c.GW * c.T * c.MT * 1024u;
 }
 
-hipError_t launch_decode_ls(int fmt, int dtype, GemmDesc d, const LsConfig& c, void* ws, hipStream_t stream) {
+hipError_t launch_decode_ls(int fmt, int dtype, GemmDesc d, const LsConfig& c, void* ws, uint32_t* fault,
+                            uint32_t spin, hipStream_t stream) {
   if (fmt == HQ_FORMAT_INT4) {
-    return dtype == HQ_DTYPE_F16 ? ls_launch_fd<HQ_FORMAT_INT4, HQ_DTYPE_F16>(d, c, ws, stream)
-                                 : ls_launch_fd<HQ_FORMAT_INT4, HQ_DTYPE_BF16>(d, c, ws, stream);
+    return dtype == HQ_DTYPE_F16 ? ls_launch_fd<HQ_FORMAT_INT4, HQ_DTYPE_F16>(d, c, ws, fault, spin, stream)
+                                 : ls_launch_fd<HQ_FORMAT_INT4, HQ_DTYPE_BF16>(d, c, ws, fault, spin, stream);
   }
-  return dtype == HQ_DTYPE_F16 ? ls_launch_fd<HQ_FORMAT_TERNARY2, HQ_DTYPE_F16>(d, c, ws, stream)
-                               : ls_launch_fd<HQ_FORMAT_TERNARY2, HQ_DTYPE_BF16>(d, c, ws, stream);
+  return dtype == HQ_DTYPE_F16 ? ls_launch_fd<HQ_FORMAT_TERNARY2, HQ_DTYPE_F16>(d, c, ws, fault, spin, stream)
+                               : ls_launch_fd<HQ_FORMAT_TERNARY2, HQ_DTYPE_BF16>(d, c, ws, fault, spin, stream);
 }
 
 }  // namespace hq

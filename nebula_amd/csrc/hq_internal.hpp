@@ -12,6 +12,7 @@ namespace hq {
 struct SegDesc {
   const uint32_t* Wp;
   const uint16_t* S;
+  const float* B;      // fp32 per-group bias [K/group][lds] (int4, general kernels only) or null
   void* Y;
   int64_t ldy;
   uint32_t N;
@@ -28,8 +29,14 @@ struct GemmDesc {
   int64_t ldx;
   uint32_t M, K;
   uint32_t nkb;  // K / 128
-  uint32_t gkb;  // group / 128
+  uint32_t gkb;  // group / 128 (fast kernels: group % 128 == 0)
   uint32_t nseg;
+  // General kernels (a bias, or a group that is not a multiple of 128): one scale (and bias)
+  // per 32-wide k chunk, scale row (4 kb + c) / g32 of chunk c of k-block kb.
+  uint32_t gen;       // 1: run the general kernels
+  uint32_t g32;       // group / 32
+  uint32_t g32_m;     // plan_div_magic(g32)
+  uint32_t has_bias;  // some segment has a bias (the others read it as 0 and add nothing)
   uint32_t pad;
   SegDesc seg[HQ_MAX_SEGMENTS];
 };
@@ -75,10 +82,16 @@ struct LsPlan {
   uint32_t gmul;    // plan_gmul(gkb)
   uint32_t* cnt;    // [G] arrival counters, zero between launches (S > 1)
   float* part;      // [G][S][GW * T * MT tiles][64 lanes] f4 partial tiles (S > 1)
+  uint32_t* fault;  // host-visible word set to 1 when a k-group barrier gives up (may be null)
+  uint32_t spin;    // polls before a k-group barrier gives up
 };
+// Polls of the lockstep k-group barrier before it gives up (each poll sleeps ~64 cycles):
+// far beyond any correct launch, whose k-groups stay within one step of each other.
+constexpr uint32_t kLsSpinLimit = 1u << 22;
 LsConfig choose_decode_ls(int fmt, const GemmDesc& d);
 size_t decode_ls_workspace_bytes(const GemmDesc& d, const LsConfig& c);
-hipError_t launch_decode_ls(int fmt, int dtype, GemmDesc d, const LsConfig& c, void* ws, hipStream_t stream);
+hipError_t launch_decode_ls(int fmt, int dtype, GemmDesc d, const LsConfig& c, void* ws, uint32_t* fault,
+                            uint32_t spin, hipStream_t stream);
 
 // One prefill launch: (16 * RT * WM)-row x 256-column tiles over the columns of d; psk
 // stream-K workgroups share the last tiles - dp tiles along K, dp workgroups own one tile
@@ -106,6 +119,10 @@ size_t prefill_workspace_bytes(const GemmDesc& d, const PrefillConfig& c);
 size_t prefill_workspace_bound(int fmt, uint32_t M, uint32_t nkb);
 // Prefill (M > 16): MFMA tile kernel.
 hipError_t launch_prefill(int fmt, int dtype, const PrefillConfig& c, void* ws, hipStream_t stream);
+
+// Whether this build has the general kernels (a bias, groups that are multiples of 32 but
+// not of 128); without them such calls fail with HQ_ERR_UNSUPPORTED.
+constexpr bool kGeneralKernels = false;
 
 // Counter area at the start of every workspace, the same for all shapes and both kernels
 // so that one workspace can serve calls of different shapes (the counters stay zero

@@ -564,6 +564,7 @@ GemmDesc column_range(int fmt, const GemmDesc& d, uint32_t cb0, uint32_t cb1) {
       const uint32_t c0 = lo * 256u;
       t.Wp = g.Wp + (size_t)lo * 16u * tile_words;
       t.S = g.S + c0;
+      t.B = g.B ? g.B + c0 : nullptr;
       t.Y = static_cast<char*>(g.Y) + (size_t)c0 * 2u;
       t.N = std::min<uint32_t>(g.N, (hi - cb) * 256u) - c0;
       t.ntiles = col_tiles(t.N);

@@ -1,6 +1,6 @@
 // hq_repack.hip — device repack of linear int4 / ternary weights into the gfx950 tile
 // layout (hq_layout.hpp). One thread per packed output word; the host variants in
-// hq_host.cpp produce the same words.
+// hq_api.cpp (hq_repack_int4, hq_repack_ternary2, hq_convert_tq1_0) produce the same words.
 #include <hip/hip_runtime.h>
 
 #include "hq_internal.hpp"

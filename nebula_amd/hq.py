@@ -35,7 +35,7 @@ MAX_SEGMENTS = 8
 # Every symbol include/hq_qgemm.h declares.
 EXPORTS = (
     "hq_version", "hq_last_error", "hq_status_string", "hq_linear_words", "hq_packed_words",
-    "hq_workspace_bytes", "hq_repack_int4_ref", "hq_repack_int4", "hq_repack_ternary2",
+    "hq_workspace_bytes", "hq_workspace_bytes_fused", "hq_describe_gemm", "hq_device_status", "hq_repack_int4_ref", "hq_repack_int4", "hq_repack_ternary2",
     "hq_unpack_int4", "hq_unpack_ternary2", "hq_repack_int4_device", "hq_repack_ternary2_device",
     "hq_gemm_w4a16", "hq_gemm_w2a16", "hq_gemm_fused", "hq_tq1_0_bytes", "hq_convert_tq1_0",
     "hq_repack_tq1_0_device",
@@ -53,6 +53,7 @@ class Segment(ctypes.Structure):
     _fields_ = [
         ("Wp", ctypes.c_void_p),
         ("scales", ctypes.c_void_p),
+        ("bias", ctypes.c_void_p),
         ("Y", ctypes.c_void_p),
         ("ldy", ctypes.c_int64),
         ("N", ctypes.c_uint32),
@@ -81,6 +82,12 @@ def lib() -> ctypes.CDLL:
     L.hq_packed_words.argtypes = [i32, u32, u32]
     L.hq_workspace_bytes.restype = i32
     L.hq_workspace_bytes.argtypes = [i32, u32, u32, u32, u32, ctypes.POINTER(sz)]
+    L.hq_workspace_bytes_fused.restype = i32
+    L.hq_workspace_bytes_fused.argtypes = [i32, u32, u32, u32, ctypes.POINTER(u32), u32, i32, ctypes.POINTER(sz)]
+    L.hq_describe_gemm.restype = i32
+    L.hq_describe_gemm.argtypes = [i32, i32, u32, u32, u32, u32, i32, ctypes.c_char_p, sz]
+    L.hq_device_status.restype = i32
+    L.hq_device_status.argtypes = [vp]
     for name in ("hq_repack_int4_ref", "hq_repack_int4", "hq_repack_ternary2", "hq_unpack_int4", "hq_unpack_ternary2"):
         f = getattr(L, name)
         f.restype = i32
@@ -89,10 +96,10 @@ def lib() -> ctypes.CDLL:
     L.hq_repack_int4_device.argtypes = [vp, vp, u32, u32, vp]
     L.hq_repack_ternary2_device.restype = i32
     L.hq_repack_ternary2_device.argtypes = [vp, vp, u32, u32, vp, vp]
-    for name in ("hq_gemm_w4a16", "hq_gemm_w2a16"):
-        f = getattr(L, name)
-        f.restype = i32
-        f.argtypes = [vp, i32, i64, vp, vp, vp, i64, u32, u32, u32, u32, vp, sz, vp]
+    L.hq_gemm_w4a16.restype = i32
+    L.hq_gemm_w4a16.argtypes = [vp, i32, i64, vp, vp, vp, vp, i64, u32, u32, u32, u32, vp, sz, vp]
+    L.hq_gemm_w2a16.restype = i32
+    L.hq_gemm_w2a16.argtypes = [vp, i32, i64, vp, vp, vp, i64, u32, u32, u32, u32, vp, sz, vp]
     L.hq_tq1_0_bytes.restype = sz
     L.hq_tq1_0_bytes.argtypes = [u32, u32]
     L.hq_convert_tq1_0.restype = i32
@@ -132,6 +139,8 @@ def _u32(a: np.ndarray) -> np.ndarray:
 # ---------------------------------------------------------------- host repacks
 def repack_int4_ref(linear: np.ndarray, K: int, N: int) -> np.ndarray:
     src = _u32(linear)
+    if src.size != (K // 8) * N:
+        raise ValueError(f"linear weight has {src.size} words, expected {(K // 8) * N}")
     dst = np.empty((K // 8) * N, dtype=np.uint32)
     check(lib().hq_repack_int4_ref(src.ctypes.data, dst.ctypes.data, K, N))
     return dst
@@ -149,6 +158,8 @@ def repack(fmt: int, linear: np.ndarray, K: int, N: int) -> np.ndarray:
 
 def unpack(fmt: int, packed: np.ndarray, K: int, N: int) -> np.ndarray:
     src = _u32(packed)
+    if src.size < packed_words(fmt, K, N):
+        raise ValueError(f"packed weight has {src.size} words, expected {packed_words(fmt, K, N)}")
     dst = np.empty(linear_words(fmt, K, N), dtype=np.uint32)
     f = lib().hq_unpack_int4 if fmt == FORMAT_INT4 else lib().hq_unpack_ternary2
     check(f(src.ctypes.data, dst.ctypes.data, K, N))
@@ -193,6 +204,10 @@ def repack_device(fmt: int, linear, K: int, N: int, stream=None, bad_flag=None):
     """Repack a device tensor of linear words (int32/uint32 view) into a new device tensor."""
     import torch
 
+    if not linear.is_cuda or not linear.is_contiguous() or linear.element_size() != 4:
+        raise ValueError("linear weight must be a contiguous 32-bit device tensor")
+    if linear.numel() != linear_words(fmt, K, N):
+        raise ValueError(f"linear weight has {linear.numel()} words, expected {linear_words(fmt, K, N)}")
     out = torch.empty(packed_words(fmt, K, N), dtype=torch.int32, device=linear.device)
     sp = _stream_ptr(stream)
     if fmt == FORMAT_INT4:
@@ -225,46 +240,142 @@ def repack_tq1_0_device(blocks, K: int, N: int, stream=None, out=None):
 
 
 def workspace_bytes(fmt: int, M: int, K: int, N: int, group: int = 128) -> int:
-    """Bytes of the decode fix-up workspace for this shape on the current device (0: none)."""
+    """Bytes of the fix-up workspace for this shape on the current device (0: none); covers calls
+    with and without a bias."""
     b = ctypes.c_size_t(0)
     check(lib().hq_workspace_bytes(fmt, M, K, N, group, ctypes.byref(b)))
     return int(b.value)
+
+
+def workspace_bytes_fused(fmt: int, M: int, K: int, Ns: Sequence[int], group: int = 128, with_bias: bool = False) -> int:
+    """Exactly the workspace one fused call over segments of widths Ns asks for."""
+    arr = (ctypes.c_uint32 * len(Ns))(*Ns)
+    b = ctypes.c_size_t(0)
+    check(lib().hq_workspace_bytes_fused(fmt, M, K, group, arr, len(Ns), int(with_bias), ctypes.byref(b)))
+    return int(b.value)
+
+
+def describe(fmt: int, dtype: int, M: int, K: int, N: int, group: int = 128, with_bias: bool = False) -> str:
+    """The plan (kernel, tiling, grid) a call of this shape runs on the current device."""
+    buf = ctypes.create_string_buffer(512)
+    check(lib().hq_describe_gemm(fmt, dtype, M, K, N, group, int(with_bias), buf, len(buf)))
+    return buf.value.decode()
+
+
+def device_status(stream=None) -> None:
+    """Wait for the stream, then raise HQError if a kernel reported a fault (a bounded wait that
+    gave up) since the last check."""
+    check(lib().hq_device_status(_stream_ptr(stream)))
 
 
 def _ws(workspace):
     """(pointer, bytes) of a caller workspace tensor (zero-filled before first use), or (None, 0)."""
     if workspace is None:
         return None, 0
+    if not workspace.is_cuda or not workspace.is_contiguous():
+        raise ValueError("workspace must be a contiguous device tensor")
     return workspace.data_ptr(), workspace.numel() * workspace.element_size()
 
 
-def gemm(fmt: int, X, Wp, scales, N: int, group: int = 128, out=None, stream=None, workspace=None):
+def _nbytes(t) -> int:
+    return t.numel() * t.element_size()
+
+
+def _check_rows(name: str, t, rows: int, cols: int, dtype) -> None:
+    """t must be a device matrix of at least rows x cols elements of dtype, unit column stride."""
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor")
+    if t.dim() != 2:
+        raise ValueError(f"{name} must be 2-D, got shape {tuple(t.shape)}")
+    if t.dtype != dtype:
+        raise ValueError(f"{name} has dtype {t.dtype}, expected {dtype}")
+    if t.shape[0] < rows or t.shape[1] < cols:
+        raise ValueError(f"{name} has shape {tuple(t.shape)}, needs at least ({rows}, {cols})")
+    if t.stride(1) != 1 and t.shape[1] > 1:
+        raise ValueError(f"{name} must have unit stride along its last dimension, got strides {t.stride()}")
+    if t.shape[0] > 1 and t.stride(0) < cols:
+        raise ValueError(f"{name} rows overlap: stride {t.stride(0)} < {cols}")
+
+
+def _check_weight(fmt: int, Wp, scales, bias, K: int, N: int, group: int, X) -> None:
+    import torch
+
+    if not (Wp.is_cuda and scales.is_cuda) or Wp.device != X.device or scales.device != X.device:
+        raise ValueError("Wp and scales must be device tensors on X's device")
+    if not (Wp.is_contiguous() and scales.is_contiguous()):
+        raise ValueError("Wp and scales must be contiguous")
+    if group <= 0 or K % group:
+        raise ValueError(f"K={K} must be a multiple of group={group}")
+    need_w = 4 * packed_words(fmt, K, N)
+    if _nbytes(Wp) < need_w:
+        raise ValueError(f"packed weight has {_nbytes(Wp)} bytes, K={K} N={N} needs {need_w}")
+    if scales.element_size() != 2 or scales.numel() < (K // group) * N:
+        raise ValueError(f"scales must hold at least {(K // group) * N} fp16 values")
+    if bias is not None:
+        if fmt != FORMAT_INT4:
+            raise ValueError("a bias is supported for int4 weights only")
+        if not bias.is_cuda or bias.device != X.device or bias.dtype != torch.float32 or not bias.is_contiguous():
+            raise ValueError("bias must be a contiguous float32 device tensor on X's device")
+        if bias.numel() < (K // group) * N:
+            raise ValueError(f"bias must hold at least {(K // group) * N} values")
+
+
+def gemm(fmt: int, X, Wp, scales, N: int, group: int = 128, out=None, stream=None, workspace=None, bias=None):
     """Y[M, N] = X[M, K] @ dequant(Wp) with fp32 accumulation (Y in X's dtype).
 
-    workspace: optional device tensor of at least workspace_bytes() bytes, zero-filled
-    before its first use; by default the library's own per-stream buffer is used."""
+    dequant: int4 (q - 8) * scale, or q * scale + bias with a float32 bias [K/group, N];
+    ternary t * scale. workspace: optional device tensor of at least workspace_bytes() bytes,
+    zero-filled before its first use; by default the library's own per-stream buffer is used.
+    Shapes, dtypes, devices and strides are checked here: the kernels size their buffer
+    descriptors from the shape, not from the allocations."""
     import torch
 
     M, K = X.shape
+    _check_rows("X", X, M, K, X.dtype)
+    _dt(X)
+    _check_weight(fmt, Wp, scales, bias, K, N, group, X)
     if out is None:
         out = torch.empty((M, N), dtype=X.dtype, device=X.device)
-    f = lib().hq_gemm_w4a16 if fmt == FORMAT_INT4 else lib().hq_gemm_w2a16
+    _check_rows("out", out, M, N, X.dtype)
+    if out.device != X.device:
+        raise ValueError("out must be on X's device")
     wp, wb = _ws(workspace)
-    check(f(X.data_ptr(), _dt(X), X.stride(0), Wp.data_ptr(), scales.data_ptr(), out.data_ptr(), out.stride(0),
-            M, K, N, group, wp, wb, _stream_ptr(stream)))
+    L = lib()
+    if fmt == FORMAT_INT4:
+        st = L.hq_gemm_w4a16(X.data_ptr(), _dt(X), X.stride(0), Wp.data_ptr(), scales.data_ptr(),
+                             bias.data_ptr() if bias is not None else None, out.data_ptr(), out.stride(0),
+                             M, K, N, group, wp, wb, _stream_ptr(stream))
+    else:
+        if bias is not None:
+            raise ValueError("a bias is supported for int4 weights only")
+        st = L.hq_gemm_w2a16(X.data_ptr(), _dt(X), X.stride(0), Wp.data_ptr(), scales.data_ptr(), out.data_ptr(),
+                             out.stride(0), M, K, N, group, wp, wb, _stream_ptr(stream))
+    check(st)
     return out
 
 
 def gemm_fused(fmt: int, X, segments: Sequence[tuple], group: int = 128, outs=None, stream=None, workspace=None):
-    """segments: (Wp, scales, N) per projection; returns one output per segment."""
+    """segments: (Wp, scales, N) or (Wp, scales, N, bias) per projection; returns one output per
+    segment."""
     import torch
 
     M, K = X.shape
+    _check_rows("X", X, M, K, X.dtype)
+    _dt(X)
+    if not 1 <= len(segments) <= MAX_SEGMENTS:
+        raise ValueError(f"need 1..{MAX_SEGMENTS} segments, got {len(segments)}")
     if outs is None:
-        outs = [torch.empty((M, n), dtype=X.dtype, device=X.device) for (_, _, n) in segments]
+        outs = [torch.empty((M, seg[2]), dtype=X.dtype, device=X.device) for seg in segments]
+    if len(outs) != len(segments):
+        raise ValueError("one output per segment")
     arr = (Segment * len(segments))()
-    for i, ((wp, sc, n), y) in enumerate(zip(segments, outs)):
-        arr[i] = Segment(wp.data_ptr(), sc.data_ptr(), y.data_ptr(), y.stride(0), n)
+    for i, (seg, y) in enumerate(zip(segments, outs)):
+        wp, sc, n = seg[:3]
+        b = seg[3] if len(seg) > 3 else None
+        _check_weight(fmt, wp, sc, b, K, n, group, X)
+        _check_rows(f"outs[{i}]", y, M, n, X.dtype)
+        arr[i] = Segment(wp.data_ptr(), sc.data_ptr(), b.data_ptr() if b is not None else None, y.data_ptr(),
+                         y.stride(0), n)
     wp, wb = _ws(workspace)
     check(lib().hq_gemm_fused(X.data_ptr(), _dt(X), X.stride(0), fmt, arr, len(segments), M, K, group, wp, wb,
                               _stream_ptr(stream)))

@@ -280,8 +280,10 @@ int main(int argc, char** argv) {
   HIP_OK(hipEventCreate(&e1));
 
   auto gemm = [&](uint32_t M, int c) {
-    auto f = fmt == HQ_FORMAT_INT4 ? hq_gemm_w4a16 : hq_gemm_w2a16;
-    HQ_OK(f(dX, dt, K, dWp[c], dS[c], dY, N, M, K, N, group, dWs, ws_bytes, stream));
+    if (fmt == HQ_FORMAT_INT4)
+      HQ_OK(hq_gemm_w4a16(dX, dt, K, dWp[c], dS[c], nullptr, dY, N, M, K, N, group, dWs, ws_bytes, stream));
+    else
+      HQ_OK(hq_gemm_w2a16(dX, dt, K, dWp[c], dS[c], dY, N, M, K, N, group, dWs, ws_bytes, stream));
   };
   auto baseline = [&](uint32_t M, int c) {
     (void)c;

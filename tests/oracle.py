@@ -105,10 +105,13 @@ def repack_ref(linear: np.ndarray, K: int, N: int) -> np.ndarray:
     return dst
 
 
-def dequant(fmt: int, linear: np.ndarray, scales: np.ndarray, K: int, N: int, group: int) -> np.ndarray:
+def dequant(fmt: int, linear: np.ndarray, scales: np.ndarray, K: int, N: int, group: int,
+            out: np.ndarray | None = None) -> np.ndarray:
     w = np.ascontiguousarray(linear, dtype=np.uint32)
     s = np.ascontiguousarray(scales, dtype=np.uint16)
-    out = np.empty((K, N), dtype=np.float32)
+    if out is None:
+        out = np.empty((K, N), dtype=np.float32)
+    assert out.shape == (K, N) and out.dtype == np.float32 and out.flags["C_CONTIGUOUS"]
     if fmt == INT4:
         lib().hqo_dequant_int4(_p(w), _p(s), K, N, group, _p(out))
     else:

@@ -51,14 +51,25 @@ def workspace_bytes(fmt, M, K, N, group=128):
     return st, b.value
 
 
+def workspace_bytes_fused(fmt, M, K, Ns, group=128, bias=0):
+    arr = (ctypes.c_uint32 * len(Ns))(*Ns)
+    b = ctypes.c_size_t(99)
+    st = hq.lib().hq_workspace_bytes_fused(fmt, M, K, group, arr, len(Ns), bias, ctypes.byref(b))
+    return st, b.value
+
+
 def test_workspace_bytes():
     # Large decode shapes with few column tiles cut their slabs along K and need a fix-up
     # workspace: a fixed counter area plus fp32 partial tiles that scale with M.
-    st, b16 = workspace_bytes(hq.FORMAT_INT4, 16, 27648, 5120)
-    st1, b1 = workspace_bytes(hq.FORMAT_INT4, 1, 27648, 5120)
+    st, b16 = workspace_bytes_fused(hq.FORMAT_INT4, 16, 27648, [5120])
+    st1, b1 = workspace_bytes_fused(hq.FORMAT_INT4, 1, 27648, [5120])
     assert st == st1 == hq.HQ_OK
     assert b16 > b1 > 0 and b16 % 256 == 0 and b1 % 256 == 0
-    assert (b16 - 65536) == 16 * (b1 - 65536)  # fixed 64 KiB counter area, then M-row partial tiles
+    # hq_workspace_bytes covers the call with and without a bias.
+    for M in (1, 16):
+        plain = workspace_bytes_fused(hq.FORMAT_INT4, M, 27648, [5120])[1]
+        biased = workspace_bytes_fused(hq.FORMAT_INT4, M, 27648, [5120], bias=1)[1]
+        assert workspace_bytes(hq.FORMAT_INT4, M, 27648, 5120) == (hq.HQ_OK, max(plain, biased))
     # Up to M = 80 the streaming kernel runs (row tiles of 16): its partials grow with the
     # row tiles. Prefill shapes (M > 80) report one bound for every N: the counter area plus
     # two fp32 tiles of 128 rows per concurrent workgroup (or 64-row ones, whichever is
@@ -72,17 +83,64 @@ def test_workspace_bytes():
     assert p2048 == p81 and (p2048 - 65536) % (2 * 128 * 256 * 4) == 0
     assert workspace_bytes(hq.FORMAT_TERNARY2, 2048, 5120, 16) == (hq.HQ_OK, p2048)
     assert workspace_bytes(hq.FORMAT_INT4, 2048, 896, 4096) == (hq.HQ_OK, 0)
-    # Bad shapes are reported, not sized.
+    # Groups that are multiples of 32 are sized (the general kernels), bad shapes reported.
+    assert workspace_bytes(hq.FORMAT_INT4, 16, 4096, 4096, group=64)[0] == hq.HQ_OK
     assert workspace_bytes(hq.FORMAT_INT4, 16, 4000, 4096)[0] == hq.HQ_ERR_SHAPE
-    assert workspace_bytes(hq.FORMAT_INT4, 16, 4096, 4096, group=64)[0] == hq.HQ_ERR_SHAPE
+    assert workspace_bytes(hq.FORMAT_INT4, 16, 4096, 4096, group=48)[0] == hq.HQ_ERR_SHAPE
+    assert workspace_bytes(hq.FORMAT_INT4, 16, 4096, 4096, group=96)[0] == hq.HQ_ERR_SHAPE  # K % group
     assert workspace_bytes(hq.FORMAT_INT4, 0, 4096, 4096)[0] == hq.HQ_ERR_SHAPE
     assert workspace_bytes(7, 16, 4096, 4096)[0] == hq.HQ_ERR_INVALID_ARG
+
+
+def test_workspace_bytes_fused_is_what_the_call_asks_for():
+    # A fused call needs exactly hq_workspace_bytes_fused bytes: one byte less is rejected
+    # with HQ_ERR_WORKSPACE before any launch, the exact size passes validation (and would
+    # launch, so the check stops at the size by giving it a misaligned buffer).
+    L = hq.lib()
+    cases = [(hq.FORMAT_INT4, 8, 1024, [16] * 8), (hq.FORMAT_INT4, 3, 27648, [5120, 1024]),
+             (hq.FORMAT_TERNARY2, 16, 5120, [5120, 1024, 1024]), (hq.FORMAT_INT4, 80, 4096, [600, 130, 1000]),
+             (hq.FORMAT_INT4, 40, 2048, [16, 32, 48, 64]), (hq.FORMAT_TERNARY2, 1, 17408, [5120])]
+    for fmt, M, K, Ns in cases:
+        st, need = workspace_bytes_fused(fmt, M, K, Ns)
+        assert st == hq.HQ_OK
+        if need == 0:
+            continue
+        segs = (hq.Segment * len(Ns))()
+        for i, n in enumerate(Ns):
+            segs[i] = hq.Segment(0x2000, 0x3000, None, 0x4000, n, n)
+        assert L.hq_gemm_fused(0x1000, 1, K, fmt, segs, len(Ns), M, K, 128, 0x10000, need - 1, None) == \
+            hq.HQ_ERR_WORKSPACE, (fmt, M, K, Ns)
+        assert L.hq_gemm_fused(0x1000, 1, K, fmt, segs, len(Ns), M, K, 128, 0x10010, need, None) == \
+            hq.HQ_ERR_ALIGNMENT, (fmt, M, K, Ns)
+    # The case the single-shape rule under-sized: eight 16-column int4 segments at M = 8.
+    need8 = workspace_bytes_fused(hq.FORMAT_INT4, 8, 1024, [16] * 8)[1]
+    assert need8 >= workspace_bytes(hq.FORMAT_INT4, 8, 1024, 16 * 8)[1]
+    assert workspace_bytes_fused(hq.FORMAT_INT4, 8, 1024, [])[0] == hq.HQ_ERR_INVALID_ARG
+    assert workspace_bytes_fused(hq.FORMAT_INT4, 8, 1024, [0])[0] == hq.HQ_ERR_SHAPE
+    assert workspace_bytes_fused(hq.FORMAT_TERNARY2, 8, 1024, [64], bias=1)[0] == hq.HQ_ERR_UNSUPPORTED
+
+
+def test_describe_gemm_names_the_kernel_families():
+    assert hq.describe(hq.FORMAT_INT4, hq.DTYPE_F16, 1, 27648, 5120).startswith("hq_decode_kernel<int4,f16,")
+    assert hq.describe(hq.FORMAT_INT4, hq.DTYPE_F16, 16, 5120, 27648).startswith("hq_decode_ls_kernel<int4,f16,")
+    assert hq.describe(hq.FORMAT_TERNARY2, hq.DTYPE_BF16, 2048, 5120, 27648).startswith(
+        "hq_prefill_kernel<ternary2,bf16")
+    assert "general" in hq.describe(hq.FORMAT_INT4, hq.DTYPE_F16, 4, 4096, 4096, group=32)
+    assert "general" in hq.describe(hq.FORMAT_INT4, hq.DTYPE_BF16, 300, 4096, 4096, with_bias=True)
+    with pytest.raises(hq.HQError):
+        hq.describe(hq.FORMAT_TERNARY2, hq.DTYPE_F16, 4, 4096, 4096, with_bias=True)
+
+
+def test_device_status_without_faults():
+    # No kernel has run: the fault word was never set (nor allocated).
+    assert hq.lib().hq_last_error() is not None
 
 
 def test_workspace_checked_before_launch():
     L = hq.lib()
     _, need = workspace_bytes(hq.FORMAT_INT4, 16, 27648, 5120)
-    args = (0x1000, 1, 27648, 0x2000, 0x3000, 0x4000, 5120, 16, 27648, 5120, 128)
+    need = workspace_bytes_fused(hq.FORMAT_INT4, 16, 27648, [5120])[1]
+    args = (0x1000, 1, 27648, 0x2000, 0x3000, None, 0x4000, 5120, 16, 27648, 5120, 128)
     assert L.hq_gemm_w4a16(*args, 0x10000, need - 1, None) == hq.HQ_ERR_WORKSPACE
     assert b"smaller" in L.hq_last_error()
     assert L.hq_gemm_w4a16(*args, 0x10010, need, None) == hq.HQ_ERR_ALIGNMENT
@@ -90,7 +148,9 @@ def test_workspace_checked_before_launch():
 
 # ---------------------------------------------------------------- validation (no device work)
 def call_gemm(X=0x1000, dtype=1, ldx=4096, Wp=0x2000, S=0x3000, Y=0x4000, ldy=4096, M=16, K=4096, N=4096, g=128,
-              fn="hq_gemm_w4a16"):
+              fn="hq_gemm_w4a16", bias=None):
+    if fn == "hq_gemm_w4a16":
+        return hq.lib().hq_gemm_w4a16(X, dtype, ldx, Wp, S, bias, Y, ldy, M, K, N, g, None, 0, None)
     return getattr(hq.lib(), fn)(X, dtype, ldx, Wp, S, Y, ldy, M, K, N, g, None, 0, None)
 
 
@@ -103,7 +163,7 @@ def call_gemm(X=0x1000, dtype=1, ldx=4096, Wp=0x2000, S=0x3000, Y=0x4000, ldy=40
     (dict(M=0), hq.HQ_ERR_SHAPE),
     (dict(N=0), hq.HQ_ERR_SHAPE),
     (dict(K=4000, ldx=4000), hq.HQ_ERR_SHAPE),
-    (dict(g=64), hq.HQ_ERR_SHAPE),
+    (dict(g=48), hq.HQ_ERR_SHAPE),
     (dict(g=96), hq.HQ_ERR_SHAPE),
     (dict(K=384, ldx=384, g=256), hq.HQ_ERR_SHAPE),
     (dict(ldx=4000), hq.HQ_ERR_SHAPE),
@@ -120,15 +180,23 @@ def test_gemm_rejects_bad_arguments(kw, status):
         assert hq.lib().hq_last_error().decode()
 
 
+def test_bias_validation():
+    assert call_gemm(bias=0x5002) == hq.HQ_ERR_ALIGNMENT
+    segs = (hq.Segment * 1)()
+    segs[0] = hq.Segment(0x2000, 0x3000, 0x5000, 0x4000, 64, 64)
+    assert hq.lib().hq_gemm_fused(0x1000, 1, 4096, 2, segs, 1, 16, 4096, 128, None, 0, None) == hq.HQ_ERR_UNSUPPORTED
+    assert "int4" in hq.lib().hq_last_error().decode()
+
+
 def test_fused_rejects_bad_segments():
     L = hq.lib()
     segs = (hq.Segment * 9)()
     for i in range(9):
-        segs[i] = hq.Segment(0x2000, 0x3000, 0x4000, 64, 64)
+        segs[i] = hq.Segment(0x2000, 0x3000, None, 0x4000, 64, 64)
     assert L.hq_gemm_fused(0x1000, 1, 4096, 1, segs, 0, 16, 4096, 128, None, 0, None) == hq.HQ_ERR_INVALID_ARG
     assert L.hq_gemm_fused(0x1000, 1, 4096, 1, segs, 9, 16, 4096, 128, None, 0, None) == hq.HQ_ERR_INVALID_ARG
     assert L.hq_gemm_fused(0x1000, 1, 4096, 7, segs, 2, 16, 4096, 128, None, 0, None) == hq.HQ_ERR_INVALID_ARG
-    segs[1] = hq.Segment(0x2000, 0x3000, 0x4000, 10, 64)
+    segs[1] = hq.Segment(0x2000, 0x3000, None, 0x4000, 10, 64)
     assert L.hq_gemm_fused(0x1000, 1, 4096, 1, segs, 2, 16, 4096, 128, None, 0, None) == hq.HQ_ERR_SHAPE
     assert "segment 1" in L.hq_last_error().decode()
 
