@@ -192,6 +192,20 @@ hq_status hq_gemm_fused(const void* X, hq_dtype dtype, int64_t ldx, hq_format fm
                         const hq_segment* segs, uint32_t nseg, uint32_t M, uint32_t K,
                         uint32_t group, void* workspace, size_t workspace_bytes, hq_stream stream);
 
+/* hq_gemm_fused for callers that cannot allocate (code under stream capture, tight serving
+ * loops, harnesses that forbid allocation). No counterpart in the reference. It allocates
+ * nothing: its workspace is a static device array of HQ_NOALLOC_SCRATCH_BYTES per GPU, held
+ * from the library's load until the process ends, and it never creates the fault word (a
+ * fault is still reported if another call created it). Plans are chosen to fit that array
+ * (fewer K splits where a call would need more), so outputs equal hq_gemm_fused's up to fp32
+ * summation order; a call that cannot fit fails with HQ_ERR_WORKSPACE. Every call on one GPU
+ * shares that GPU's array, which keeps the last call's contents: calls that overlap in time
+ * on one GPU (different streams without ordering) race and give wrong results. */
+#define HQ_NOALLOC_SCRATCH_BYTES ((size_t)16 << 20)
+hq_status hq_gemm_fused_noalloc(const void* X, hq_dtype dtype, int64_t ldx, hq_format fmt,
+                                const hq_segment* segs, uint32_t nseg, uint32_t M, uint32_t K,
+                                uint32_t group, hq_stream stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -218,21 +218,25 @@ struct Plan {
   size_t need = 0;
 };
 
-Plan make_plan(int fmt, const hq::GemmDesc& d) {
+// cap: the largest workspace the plan may use (the no-allocation entry point's scratch).
+Plan make_plan(int fmt, const hq::GemmDesc& d, size_t cap = SIZE_MAX) {
   Plan p{};
   if (d.M > decode_max_m()) {
     p.kind = Kind::kPrefill;
-    p.pc = hq::choose_prefill(fmt, d);
+    p.pc = hq::choose_prefill(fmt, d, cap);
     p.need = hq::prefill_workspace_bytes(d, p.pc);
-  } else if (use_lockstep(fmt, d)) {
-    p.kind = Kind::kLockstep;
-    p.lc = hq::choose_decode_ls(fmt, d);
-    p.need = hq::decode_ls_workspace_bytes(d, p.lc);
-  } else {
+    return p;
+  }
+  if (!use_lockstep(fmt, d)) {
     p.kind = Kind::kDecode;
     p.c = hq::choose_decode(fmt, d);
     p.need = hq::decode_workspace_bytes(d, p.c);
+    if (p.need <= cap) return p;
   }
+  // The lockstep kernel takes every decode shape; under a cap with fewer pieces per slab.
+  p.kind = Kind::kLockstep;
+  p.lc = hq::choose_decode_ls(fmt, d, cap);
+  p.need = hq::decode_ls_workspace_bytes(d, p.lc);
   return p;
 }
 
@@ -267,6 +271,8 @@ uint32_t* fault_ptr(hipStream_t s) {
   f.host = static_cast<uint32_t*>(p);
   return f.host;
 }
+// The fault word if it exists already (never allocates).
+uint32_t* fault_ptr_if_any() { return __atomic_load_n(&fault_word().host, __ATOMIC_ACQUIRE); }
 // Reads and clears the fault word: true if a kernel reported a fault since the last check.
 bool take_fault() {
   FaultWord& f = fault_word();
@@ -284,9 +290,9 @@ uint32_t ls_spin() {
   return v && *v ? (uint32_t)std::strtoul(v, nullptr, 10) : hq::kLsSpinLimit;
 }
 
-hq_status run_gemm(const void* X, hq_dtype dtype, int64_t ldx, hq_format fmt, const hq_segment* segs,
-                   uint32_t nseg, uint32_t M, uint32_t K, uint32_t group, void* ws, size_t ws_bytes,
-                   hq_stream stream) {
+// Validates a call and builds its descriptor (pointers included).
+hq_status prepare(const void* X, hq_dtype dtype, int64_t ldx, hq_format fmt, const hq_segment* segs, uint32_t nseg,
+                  uint32_t M, uint32_t K, uint32_t group, hq::GemmDesc* out) {
   if (take_fault()) return fault_status();
   if (!segs || nseg == 0 || nseg > HQ_MAX_SEGMENTS)
     return fail(HQ_ERR_INVALID_ARG, "need 1..%d segments, got %u", HQ_MAX_SEGMENTS, nseg);
@@ -313,6 +319,27 @@ hq_status run_gemm(const void* X, hq_dtype dtype, int64_t ldx, hq_format fmt, co
     d.seg[i].Y = segs[i].Y;
     d.seg[i].ldy = segs[i].ldy;
   }
+  *out = d;
+  return HQ_OK;
+}
+
+hq_status launch_plan(int fmt, int dtype, const hq::GemmDesc& d, const Plan& p, void* w, uint32_t* fault,
+                      hipStream_t s) {
+  switch (p.kind) {
+    case Kind::kPrefill: return from_hip(hq::launch_prefill(fmt, dtype, p.pc, w, s), "prefill launch");
+    case Kind::kLockstep:
+      return from_hip(hq::launch_decode_ls(fmt, dtype, d, p.lc, w, fault, ls_spin(), s), "decode launch");
+    case Kind::kDecode: break;
+  }
+  return from_hip(hq::launch_decode(fmt, dtype, d, p.c, w, s), "decode launch");
+}
+
+hq_status run_gemm(const void* X, hq_dtype dtype, int64_t ldx, hq_format fmt, const hq_segment* segs,
+                   uint32_t nseg, uint32_t M, uint32_t K, uint32_t group, void* ws, size_t ws_bytes,
+                   hq_stream stream) {
+  hq::GemmDesc d;
+  hq_status st = prepare(X, dtype, ldx, fmt, segs, nseg, M, K, group, &d);
+  if (st != HQ_OK) return st;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const Plan p = make_plan(fmt, d);
   void* w = nullptr;
@@ -327,13 +354,50 @@ hq_status run_gemm(const void* X, hq_dtype dtype, int64_t ldx, hq_format fmt, co
       return st;
     }
   }
-  switch (p.kind) {
-    case Kind::kPrefill: return from_hip(hq::launch_prefill(fmt, dtype, p.pc, w, s), "prefill launch");
-    case Kind::kLockstep:
-      return from_hip(hq::launch_decode_ls(fmt, dtype, d, p.lc, w, fault_ptr(s), ls_spin(), s), "decode launch");
-    case Kind::kDecode: break;
-  }
-  return from_hip(hq::launch_decode(fmt, dtype, d, p.c, w, s), "decode launch");
+  return launch_plan(fmt, dtype, d, p, w, fault_ptr(s), s);
+}
+
+// ---- the no-allocation entry point's scratch ----
+// A file-scope device array is the workspace of hq_gemm_fused_noalloc: each GPU the library
+// runs on holds its own copy, at its own address, until the process ends. Host code never
+// passes the array's name to a kernel (on the host it only names the symbol): the per-device
+// address comes from hipGetSymbolAddress, taken once per device at that device's first call.
+constexpr size_t kScratchBytes = HQ_NOALLOC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+__global__ void hq_zero_words(uint32_t* p, uint32_t n) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+constexpr int kMaxDevices = 64;
+struct ScratchSlot {
+  std::once_flag once;
+  void* ptr = nullptr;
+  hipError_t err = hipSuccess;
+};
+ScratchSlot g_scratch[kMaxDevices];
+
+// The scratch array's address on the current device. The first call on a device resolves it
+// and clears the arrival counters at its start with a fill kernel on `s` (kernels leave them
+// at zero after every call; a fill kernel, not a memset, so that a captured first call still
+// replays correctly).
+hq_status scratch_ptr(hipStream_t s, void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return from_hip(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(HQ_ERR_UNSUPPORTED, "device %d: at most %d devices", dev, kMaxDevices);
+  ScratchSlot& sl = g_scratch[dev];
+  std::call_once(sl.once, [&] {
+    sl.err = hipGetSymbolAddress(&sl.ptr, HIP_SYMBOL(scratch));
+    if (sl.err != hipSuccess) return;
+    const uint32_t n = (uint32_t)(hq::kCounterBytes / 4u);
+    hipLaunchKernelGGL(hq_zero_words, dim3((n + 255u) / 256u), dim3(256), 0, s, static_cast<uint32_t*>(sl.ptr), n);
+    sl.err = hipGetLastError();
+  });
+  if (sl.err != hipSuccess) return from_hip(sl.err, "scratch set-up (hipGetSymbolAddress)");
+  *out = sl.ptr;
+  return HQ_OK;
 }
 
 const char* fmt_name(int fmt) { return fmt == HQ_FORMAT_INT4 ? "int4" : "ternary2"; }
@@ -638,6 +702,21 @@ hq_status hq_gemm_fused(const void* X, hq_dtype dtype, int64_t ldx, hq_format fm
                         uint32_t nseg, uint32_t M, uint32_t K, uint32_t group, void* ws, size_t ws_bytes,
                         hq_stream stream) {
   return run_gemm(X, dtype, ldx, fmt, segs, nseg, M, K, group, ws, ws_bytes, stream);
+}
+
+hq_status hq_gemm_fused_noalloc(const void* X, hq_dtype dtype, int64_t ldx, hq_format fmt, const hq_segment* segs,
+                                uint32_t nseg, uint32_t M, uint32_t K, uint32_t group, hq_stream stream) {
+  hq::GemmDesc d;
+  hq_status st = prepare(X, dtype, ldx, fmt, segs, nseg, M, K, group, &d);
+  if (st != HQ_OK) return st;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const Plan p = make_plan(fmt, d, kScratchBytes);
+  if (p.need > kScratchBytes)
+    return fail(HQ_ERR_WORKSPACE, "this call needs %zu workspace bytes, more than the %zu-byte static scratch",
+                p.need, kScratchBytes);
+  void* w = nullptr;
+  if (p.need > 0 && (st = scratch_ptr(s, &w)) != HQ_OK) return st;
+  return launch_plan(fmt, dtype, d, p, w, fault_ptr_if_any(), s);
 }
 
 }  // extern "C"

@@ -574,7 +574,7 @@ hipError_t ls_launch_fd(const GemmDesc& d, const LsConfig& c, void* ws, uint32_t
 // Lockstep tiling: KG k-groups of four wavefronts, T tiles per wavefront (slabs of up to
 // 4 T tiles), ring depth U, and S pieces per slab chosen so that the grid covers the CUs.
 // HQ_DECODE_LS_KG / _T / _U / _S / _SW override (tuning and tests).
-LsConfig choose_decode_ls(int fmt, const GemmDesc& d) {
+LsConfig choose_decode_ls(int fmt, const GemmDesc& d, size_t ws_cap) {
   const uint32_t cus = (uint32_t)cu_count();
   // Measured on MI355X (27B-class shapes, M = 4..16): two k-groups of four wavefronts,
   // two tiles per wavefront, two steps in flight; a K split only when the slabs alone
@@ -625,6 +625,7 @@ LsConfig choose_decode_ls(int fmt, const GemmDesc& d) {
   if (eS >= 1) c.S = eS;
   c.S = std::max(1, std::min<int>({c.S, (int)d.nkb, (int)kMaxPieces}));
   if (c.S > 1 && ls_assign_slabs(x, (uint32_t)c.SW) > kMaxCounters) c.S = 1;
+  while (c.S > 1 && decode_ls_workspace_bytes(d, c) > ws_cap) --c.S;  // fewer pieces under a cap
   return c;
 }
 

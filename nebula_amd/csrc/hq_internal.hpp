@@ -88,7 +88,8 @@ struct LsPlan {
 // Polls of the lockstep k-group barrier before it gives up (each poll sleeps ~64 cycles):
 // far beyond any correct launch, whose k-groups stay within one step of each other.
 constexpr uint32_t kLsSpinLimit = 1u << 22;
-LsConfig choose_decode_ls(int fmt, const GemmDesc& d);
+// ws_cap: the largest workspace the plan may use (fewer pieces per slab below it).
+LsConfig choose_decode_ls(int fmt, const GemmDesc& d, size_t ws_cap = SIZE_MAX);
 size_t decode_ls_workspace_bytes(const GemmDesc& d, const LsConfig& c);
 hipError_t launch_decode_ls(int fmt, int dtype, GemmDesc d, const LsConfig& c, void* ws, uint32_t* fault,
                             uint32_t spin, hipStream_t stream);
@@ -110,7 +111,8 @@ struct PrefillConfig {
   int n;
   PrefillLaunch l[2];
 };
-PrefillConfig choose_prefill(int fmt, const GemmDesc& d);
+// ws_cap: the largest workspace the plan may use (fewer stream-K workgroups, or none, below it).
+PrefillConfig choose_prefill(int fmt, const GemmDesc& d, size_t ws_cap = SIZE_MAX);
 // Workspace bytes of a prefill call (0 without stream-K): the counter area, then two fp32
 // partial tiles per stream-K workgroup.
 size_t prefill_workspace_bytes(const GemmDesc& d, const PrefillConfig& c);

@@ -601,7 +601,7 @@ PrefillLaunch make_launch(int RT, int WM, const GemmDesc& d) {
 //    the last k column blocks (just enough to empty that round) run as a second launch of
 //    half-height tiles, if those fit in one round: the tail then takes half a round.
 //  * Otherwise whole tiles.
-PrefillConfig choose_prefill(int fmt, const GemmDesc& d) {
+PrefillConfig choose_prefill(int fmt, const GemmDesc& d, size_t ws_cap) {
   PrefillConfig c{};
   int RT = 8, WM = 2;
   prefill_shape(d.M, RT, WM);
@@ -646,6 +646,12 @@ PrefillConfig choose_prefill(int fmt, const GemmDesc& d) {
       (uint64_t)l.tiles * d.nkb < (1ull << 31)) {
     uint32_t psk = std::min<uint32_t>(slots / l.tiles, d.nkb / 4u) * l.tiles;
     if (epsk > 0) psk = std::min<uint32_t>((uint32_t)epsk, l.tiles * d.nkb);
+    // Under a workspace cap: as many whole s-way splits as the partial tiles fit in.
+    const size_t per_wg = 2u * (16u * RT * WM) * 256u * sizeof(float);
+    if (ws_cap != SIZE_MAX) {
+      const size_t fit = ws_cap > kCounterBytes ? (ws_cap - kCounterBytes) / per_wg : 0u;
+      if (psk > fit) psk = epsk > 0 ? (uint32_t)fit : (uint32_t)(fit / l.tiles) * l.tiles;
+    }
     if (psk > l.tiles && (psk >= 2u * l.tiles || epsk > 0)) {
       l.psk = psk;
       l.dp = 0;

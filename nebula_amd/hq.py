@@ -31,13 +31,14 @@ DTYPE_BF16 = 2
 FORMAT_INT4 = 1
 FORMAT_TERNARY2 = 2
 MAX_SEGMENTS = 8
+NOALLOC_SCRATCH_BYTES = 16 << 20  # HQ_NOALLOC_SCRATCH_BYTES
 
 # Every symbol include/hq_qgemm.h declares.
 EXPORTS = (
     "hq_version", "hq_last_error", "hq_status_string", "hq_linear_words", "hq_packed_words",
     "hq_workspace_bytes", "hq_workspace_bytes_fused", "hq_describe_gemm", "hq_device_status", "hq_repack_int4_ref", "hq_repack_int4", "hq_repack_ternary2",
     "hq_unpack_int4", "hq_unpack_ternary2", "hq_repack_int4_device", "hq_repack_ternary2_device",
-    "hq_gemm_w4a16", "hq_gemm_w2a16", "hq_gemm_fused", "hq_tq1_0_bytes", "hq_convert_tq1_0",
+    "hq_gemm_w4a16", "hq_gemm_w2a16", "hq_gemm_fused", "hq_gemm_fused_noalloc", "hq_tq1_0_bytes", "hq_convert_tq1_0",
     "hq_repack_tq1_0_device",
 )
 
@@ -108,6 +109,8 @@ def lib() -> ctypes.CDLL:
     L.hq_repack_tq1_0_device.argtypes = [vp, u32, u32, vp, vp, vp]
     L.hq_gemm_fused.restype = i32
     L.hq_gemm_fused.argtypes = [vp, i32, i64, i32, ctypes.POINTER(Segment), u32, u32, u32, u32, vp, sz, vp]
+    L.hq_gemm_fused_noalloc.restype = i32
+    L.hq_gemm_fused_noalloc.argtypes = [vp, i32, i64, i32, ctypes.POINTER(Segment), u32, u32, u32, u32, vp]
     _lib = L
     return L
 
@@ -354,9 +357,11 @@ def gemm(fmt: int, X, Wp, scales, N: int, group: int = 128, out=None, stream=Non
     return out
 
 
-def gemm_fused(fmt: int, X, segments: Sequence[tuple], group: int = 128, outs=None, stream=None, workspace=None):
+def gemm_fused(fmt: int, X, segments: Sequence[tuple], group: int = 128, outs=None, stream=None, workspace=None,
+               noalloc: bool = False):
     """segments: (Wp, scales, N) or (Wp, scales, N, bias) per projection; returns one output per
-    segment."""
+    segment. noalloc: run hq_gemm_fused_noalloc (its workspace is the library's static scratch;
+    `outs` must then be given by a caller that cannot allocate)."""
     import torch
 
     M, K = X.shape
@@ -376,6 +381,12 @@ def gemm_fused(fmt: int, X, segments: Sequence[tuple], group: int = 128, outs=No
         _check_rows(f"outs[{i}]", y, M, n, X.dtype)
         arr[i] = Segment(wp.data_ptr(), sc.data_ptr(), b.data_ptr() if b is not None else None, y.data_ptr(),
                          y.stride(0), n)
+    if noalloc:
+        if workspace is not None:
+            raise ValueError("noalloc calls use the library's static scratch, not a workspace")
+        check(lib().hq_gemm_fused_noalloc(X.data_ptr(), _dt(X), X.stride(0), fmt, arr, len(segments), M, K, group,
+                                          _stream_ptr(stream)))
+        return outs
     wp, wb = _ws(workspace)
     check(lib().hq_gemm_fused(X.data_ptr(), _dt(X), X.stride(0), fmt, arr, len(segments), M, K, group, wp, wb,
                               _stream_ptr(stream)))
