@@ -31,6 +31,13 @@
 // removed by a correction MFMA that seeds every tile's k-block sum; the fp16 group scale
 // multiplies the fp32 k-block sum. Pieces of a split slab are summed in piece order by
 // the last workgroup to finish (arrival counter), so results are deterministic.
+//
+// General kernels (GEN): one scale per 32-wide k chunk (groups that are multiples of 32, not
+// of 128) and an optional fp32 per-group bias, the reference's w = q * s + b
+// (marlin_gemm.cu:195-196). With e = 8 s + b (the weight of code 8) the chunk's contribution
+// is s * sum x (q - 8) + e * sum x: the first term is the fast kernels' (per chunk), the
+// second a row sum of the chunk (one MFMA against a fragment of ones) times e. Without a bias
+// e is 0, and so is e for a bias of exactly -8 s: such calls give the same bits.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -52,6 +59,11 @@ __device__ __forceinline__ u4 ls_load_b128_nt(__amdgpu_buffer_rsrc_t r, uint32_t
 __device__ __forceinline__ u2 ls_load_b64_nt(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
   u2 v;
   asm volatile("buffer_load_dwordx2 %0, %1, %2, %3 offen nt" : "=v"(v) : "v"(voff), "s"(r), "s"(soff));
+  return v;
+}
+__device__ __forceinline__ uint32_t ls_load_b32(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  uint32_t v;
+  asm volatile("buffer_load_dword %0, %1, %2, %3 offen" : "=v"(v) : "v"(voff), "s"(r), "s"(soff));
   return v;
 }
 __device__ __forceinline__ uint32_t ls_load_u16(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
@@ -121,7 +133,7 @@ __device__ __forceinline__ void ls_tie(u4& a) { asm volatile("" : "+v"(a)); }
 __device__ __forceinline__ void ls_tie(u2& a) { asm volatile("" : "+v"(a)); }
 __device__ __forceinline__ void ls_tie(uint32_t& a) { asm volatile("" : "+v"(a)); }
 
-template <int FMT, int DT, int KG, int GW, int T, int U, int MT, bool FUSED>
+template <int FMT, int DT, int KG, int GW, int T, int U, int MT, bool FUSED, bool GEN>
 __global__ void __launch_bounds__(64 * KG * GW, KG == 1 && MT > 1 ? 2 : 1)
     hq_decode_ls_kernel(const GemmDesc d, const LsPlan pl) {
   static_assert(KG == 1 || KG == 2 || KG == 4, "one, two or four k-groups");
@@ -145,7 +157,8 @@ __global__ void __launch_bounds__(64 * KG * GW, KG == 1 && MT > 1 ? 2 : 1)
   constexpr int R = U + 1;
   constexpr int NS = 2;
   constexpr int XL = 4 * MT / GW;   // activation loads (four rows each) per wavefront and step
-  constexpr int PER = XL + T + 1;  // loads per wavefront and step: activation rows, T tiles, scales
+  // Loads per wavefront and step: activation rows, T tiles, scales (GEN: T scale and T bias loads).
+  constexpr int PER = XL + T + (GEN ? 2 * T : 1);
   constexpr uint32_t kXStage = MT * kStageBytes;  // one k-group's activation k-block: 16 MT rows
   constexpr uint32_t kStep = KG * kXStage;
   static_assert((KG - 1) * GW * T * MT * 1024 <= NS * kStep, "the k-group reduction reuses the activation stages");
@@ -167,6 +180,7 @@ __global__ void __launch_bounds__(64 * KG * GW, KG == 1 && MT > 1 ? 2 : 1)
   // call looks its segment up first.
   const uint32_t* sWp = d.seg[0].Wp;
   const uint16_t* sS = d.seg[0].S;
+  const float* sB = d.seg[0].B;
   void* sY = d.seg[0].Y;
   uint32_t sN = d.seg[0].N, sLds = d.seg[0].lds, sNt = d.seg[0].ntiles;
   uint32_t sLdy = (uint32_t)d.seg[0].ldy, sBegin = d.seg[0].blk_begin;
@@ -177,6 +191,7 @@ __global__ void __launch_bounds__(64 * KG * GW, KG == 1 && MT > 1 ? 2 : 1)
     si = __builtin_amdgcn_readfirstlane(si);
     sWp = d.seg[si].Wp;
     sS = d.seg[si].S;
+    sB = d.seg[si].B;
     sY = d.seg[si].Y;
     sN = d.seg[si].N;
     sLds = d.seg[si].lds;
@@ -201,9 +216,15 @@ __global__ void __launch_bounds__(64 * KG * GW, KG == 1 && MT > 1 ? 2 : 1)
   uint32_t wvo[T];
 #pragma unroll
   for (int t = 0; t < T; ++t) wvo[t] = lane * kLaneBytes + (uint32_t)t * nkb * kBlockBytes;
-  // Scales: lane l loads column 16 (ctw + l / 16) + l % 16 (clamped to N - 1).
-  const __amdgpu_buffer_rsrc_t srs = make_rsrc(sS, ((nkb / d.gkb - 1u) * sLds + sN) * 2u);
+  // Scales: lane l loads column 16 (ctw + l / 16) + l % 16 (clamped to N - 1). GEN: scale load
+  // t (and bias load t) gives lane l tile t's column 16 (ctw + t) + l % 16 in chunk l / 16.
+  const uint32_t srows = GEN ? 4u * nkb / d.g32 : nkb / d.gkb;  // scale (and bias) rows
+  const __amdgpu_buffer_rsrc_t srs = make_rsrc(sS, ((srows - 1u) * sLds + sN) * 2u);
   const uint32_t svo = min((ctw + min(g4, (uint32_t)T - 1u)) * 16u + c16, sN - 1u) * 2u;
+  const __amdgpu_buffer_rsrc_t brs = make_rsrc(sB, GEN && sB ? ((srows - 1u) * sLds + sN) * 4u : 0u);
+  uint32_t gvo[GEN ? T : 1];
+#pragma unroll
+  for (int t = 0; t < (GEN ? T : 1); ++t) gvo[t] = min((ctw + t) * 16u + c16, sN - 1u);
   // Activations: load x of this wavefront covers rows 4 (XL wi + x) + lane / 16 of its
   // k-group's k-block; lane l holds the 16-byte piece (l % 16) ^ row of its row's 256
   // bytes (rows >= M read zero) and writes it to LDS at row * 256 + 16 * (l % 16) of the
@@ -224,7 +245,8 @@ __global__ void __launch_bounds__(64 * KG * GW, KG == 1 && MT > 1 ? 2 : 1)
   for (int c = 0; c < 4; ++c) xro[c] = xs0 + c16 * 256u + 16u * ((4u * c + g4) ^ c16);
 
   WV wring[R][T];
-  uint32_t sring[R];
+  uint32_t sring[R][GEN ? T : 1];
+  uint32_t bring[R][GEN ? T : 1];
   u4 xring[R][XL];
   // Loads of ring slot `slot` for step q (past the piece: zero reads).
   auto issue = [&](int slot, uint32_t q) {
@@ -239,8 +261,18 @@ __global__ void __launch_bounds__(64 * KG * GW, KG == 1 && MT > 1 ? 2 : 1)
       if constexpr (kInt4) wring[slot][t] = ls_load_b128_nt(wr, live ? wvo[t] : kOutOfRange, kbo);
       else wring[slot][t] = ls_load_b64_nt(wr, live ? wvo[t] : kOutOfRange, kbo);
     }
-    sring[slot] = ls_load_u16(srs, live ? svo : kOutOfRange,
-                              __builtin_amdgcn_readfirstlane(plan_group_of_kb(kbu, pl.gmul) * srow2));
+    if constexpr (GEN) {
+      // Chunk g4 of k-block kb: scale row (4 kb + g4) / g32, per lane.
+      const uint32_t row = plan_div(4u * kbu + g4, d.g32, d.g32_m);
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        sring[slot][t] = ls_load_u16(srs, live ? row * srow2 + gvo[t] * 2u : kOutOfRange, 0u);
+        bring[slot][t] = ls_load_b32(brs, live ? row * (srow2 * 2u) + gvo[t] * 4u : kOutOfRange, 0u);
+      }
+    } else {
+      sring[slot][0] = ls_load_u16(srs, live ? svo : kOutOfRange,
+                                   __builtin_amdgcn_readfirstlane(plan_group_of_kb(kbu, pl.gmul) * srow2));
+    }
   };
 
   f4 acc[MT][T];
@@ -250,12 +282,26 @@ __global__ void __launch_bounds__(64 * KG * GW, KG == 1 && MT > 1 ? 2 : 1)
     for (int t = 0; t < T; ++t) acc[r][t] = f4{0.f, 0.f, 0.f, 0.f};
   const DqBiasConst dqb = DT == HQ_DTYPE_F16 ? dq_bias_const_f16() : dq_bias_const_bf16();
   const u4 corr_b = int4_corr_fragment<DT>();
+  const uint32_t one2 = DT == HQ_DTYPE_F16 ? 0x3C003C00u : 0x3F803F80u;  // 1.0 in both halves
+  const u4 ones = u4{one2, one2, one2, one2};
+  const bool has_bias = GEN && sB != nullptr;
 
   auto compute = [&](int slot, uint32_t stage) {
     const uint32_t so = stage * kStep;
     uint32_t sb[T];
+    uint32_t gsb[GEN ? T : 1][4], gbb[GEN ? T : 1][4];  // GEN: scale / bias bits of (tile, chunk)
+    if constexpr (GEN) {
 #pragma unroll
-    for (int t = 0; t < T; ++t) sb[t] = T == 1 ? sring[slot] : ls_bpermute((16u * t + c16) * 4u, sring[slot]);
+      for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          gsb[t][c] = ls_bpermute((16u * c + c16) * 4u, sring[slot][t]);
+          gbb[t][c] = ls_bpermute((16u * c + c16) * 4u, bring[slot][t]);
+        }
+    } else {
+#pragma unroll
+      for (int t = 0; t < T; ++t) sb[t] = T == 1 ? sring[slot][0] : ls_bpermute((16u * t + c16) * 4u, sring[slot][0]);
+    }
     // The weight fragments of the k-block, dequantised once and used by every row tile.
     u4 bf[4][T];
 #pragma unroll
@@ -271,6 +317,7 @@ __global__ void __launch_bounds__(64 * KG * GW, KG == 1 && MT > 1 ? 2 : 1)
         }
       }
     float sc[T];
+    float gs_[GEN ? T : 1][4], ge_[GEN ? T : 1][4];  // GEN: scale and e = 8 s + b of (tile, chunk)
 #pragma unroll
     for (int r = 0; r < MT; ++r) {
       u4 xf[4];
@@ -279,6 +326,38 @@ __global__ void __launch_bounds__(64 * KG * GW, KG == 1 && MT > 1 ? 2 : 1)
       ls_wait_lgkmcnt0();
 #pragma unroll
       for (int c = 0; c < 4; ++c) ls_tie(xf[c]);
+      if constexpr (GEN) {
+        if (r == 0) {
+#pragma unroll
+          for (int t = 0; t < T; ++t)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+              ls_tie(gsb[t][c]);
+              ls_tie(gbb[t][c]);
+              float sv = f16_to_f32((uint16_t)gsb[t][c]);
+              if constexpr (!kInt4) sv = __builtin_isfinite(sv) ? 0.5f * sv : 0.0f;  // fields hold 2t
+              gs_[t][c] = sv;
+              ge_[t][c] = has_bias ? __builtin_fmaf(8.0f, sv, __builtin_bit_cast(float, gbb[t][c])) : 0.0f;
+            }
+        }
+        // Per chunk: the tiles' sums x (q - 8) (or x 2t), scaled, and the row sum times e.
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          f4 cc = f4{0.f, 0.f, 0.f, 0.f};
+          if constexpr (kInt4 && !kUnbiased) cc = mfma16x16x32<DT>(xf[c], corr_b, cc);
+          const f4 rs = mfma16x16x32<DT>(xf[c], ones, f4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+          for (int t = 0; t < T; ++t) {
+            const f4 g = mfma16x16x32<DT>(xf[c], bf[c][t], f4{0.f, 0.f, 0.f, 0.f});
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+              acc[r][t][v] = __builtin_fmaf(kInt4 && !kUnbiased ? g[v] + cc[v] : g[v], gs_[t][c], acc[r][t][v]);
+              acc[r][t][v] = __builtin_fmaf(rs[v], ge_[t][c], acc[r][t][v]);
+            }
+          }
+        }
+        continue;
+      }
       if (r == 0) {
 #pragma unroll
         for (int t = 0; t < T; ++t) {
@@ -358,7 +437,11 @@ __global__ void __launch_bounds__(64 * KG * GW, KG == 1 && MT > 1 ? 2 : 1)
         ls_wait_vmcnt<(U - 1) * PER>();  // this wavefront's loads of step i + s have landed
 #pragma unroll
         for (int t = 0; t < T; ++t) ls_tie(wring[s][t]);
-        ls_tie(sring[s]);
+    #pragma unroll
+        for (int t = 0; t < (GEN ? T : 1); ++t) {
+          ls_tie(sring[s][t]);
+          if constexpr (GEN) ls_tie(bring[s][t]);
+        }
 #pragma unroll
         for (int x = 0; x < XL; ++x) ls_tie(xring[s][x]);
         issue((s + U) % R, i + s + U);
@@ -378,7 +461,11 @@ __global__ void __launch_bounds__(64 * KG * GW, KG == 1 && MT > 1 ? 2 : 1)
   for (int r = 0; r < R; ++r) {
 #pragma unroll
     for (int t = 0; t < T; ++t) ls_tie(wring[r][t]);
-    ls_tie(sring[r]);
+#pragma unroll
+    for (int t = 0; t < (GEN ? T : 1); ++t) {
+      ls_tie(sring[r][t]);
+      if constexpr (GEN) ls_tie(bring[r][t]);
+    }
 #pragma unroll
     for (int x = 0; x < XL; ++x) ls_tie(xring[r][x]);
   }
@@ -500,7 +587,7 @@ uint32_t ls_assign_slabs(GemmDesc& d, uint32_t sw) {
   return g;
 }
 
-template <int FMT, int DT, int KG, int GW, int T, int U, int MT>
+template <int FMT, int DT, int KG, int GW, int T, int U, int MT, bool GEN = false>
 hipError_t ls_launch_t(GemmDesc d, const LsConfig& c, void* ws, uint32_t* fault, uint32_t spin, hipStream_t stream) {
   const bool fused = d.nseg > 1;
   if (d.M > 16u * MT) return hipErrorInvalidValue;
@@ -524,18 +611,33 @@ hipError_t ls_launch_t(GemmDesc d, const LsConfig& c, void* ws, uint32_t* fault,
   bool fits = G >= 1 && G <= 65535 && xbytes < (1ull << 31) && (uint64_t)G * pl.S * GW * T * MT * 1024u < (1ull << 31);
   for (uint32_t i = 0; i < d.nseg; ++i) fits = fits && (uint64_t)d.M * (uint64_t)d.seg[i].ldy * 2u < (1ull << 31);
   if (!fits) return hipErrorInvalidValue;
-  if (fused)
-    hipLaunchKernelGGL((hq_decode_ls_kernel<FMT, DT, KG, GW, T, U, MT, true>), dim3(pl.S, G), dim3(64 * KG * GW), 0,
-                       stream, d, pl);
-  else
-    hipLaunchKernelGGL((hq_decode_ls_kernel<FMT, DT, KG, GW, T, U, MT, false>), dim3(pl.S, G), dim3(64 * KG * GW), 0,
-                       stream, d, pl);
+  if constexpr (GEN) {  // the general kernels always look their segment up
+    hipLaunchKernelGGL((hq_decode_ls_kernel<FMT, DT, KG, GW, T, U, MT, true, true>), dim3(pl.S, G), dim3(64 * KG * GW),
+                       0, stream, d, pl);
+  } else if (fused) {
+    hipLaunchKernelGGL((hq_decode_ls_kernel<FMT, DT, KG, GW, T, U, MT, true, false>), dim3(pl.S, G),
+                       dim3(64 * KG * GW), 0, stream, d, pl);
+  } else {
+    hipLaunchKernelGGL((hq_decode_ls_kernel<FMT, DT, KG, GW, T, U, MT, false, false>), dim3(pl.S, G),
+                       dim3(64 * KG * GW), 0, stream, d, pl);
+  }
   return hipGetLastError();
 }
 
 template <int FMT, int DT>
 hipError_t ls_launch_fd(const GemmDesc& d, const LsConfig& c, void* ws, uint32_t* fault, uint32_t spin,
                         hipStream_t stream) {
+  if (d.gen) {  // general kernels: two k-groups of four wavefronts, two tiles each, two steps in flight
+    if (c.GW * 1000 + c.KG * 100 + c.T * 10 + c.U != 4222) return hipErrorInvalidConfiguration;
+    switch (c.MT) {
+      case 1: return ls_launch_t<FMT, DT, 2, 4, 2, 2, 1, true>(d, c, ws, fault, spin, stream);
+      case 2: return ls_launch_t<FMT, DT, 2, 4, 2, 2, 2, true>(d, c, ws, fault, spin, stream);
+      case 3: return ls_launch_t<FMT, DT, 2, 4, 2, 2, 3, true>(d, c, ws, fault, spin, stream);
+      case 4: return ls_launch_t<FMT, DT, 2, 4, 2, 2, 4, true>(d, c, ws, fault, spin, stream);
+      case 5: return ls_launch_t<FMT, DT, 2, 4, 2, 2, 5, true>(d, c, ws, fault, spin, stream);
+      default: return hipErrorInvalidConfiguration;
+    }
+  }
   if (c.MT > 1 && c.KG == 1) {  // one k-group, two workgroups per CU
     if (c.GW * 1000 + c.KG * 100 + c.T * 10 + c.U != 4122) return hipErrorInvalidConfiguration;
     switch (c.MT) {
@@ -619,6 +721,14 @@ LsConfig choose_decode_ls(int fmt, const GemmDesc& d, size_t ws_cap) {
   if (c.MT > 1 && eKG == 0 && (uint64_t)G * (uint32_t)c.S > cus && (uint64_t)G * (uint32_t)c.S <= 2ull * cus) c.KG = 1;
   // Narrower slabs that would cover every CU measured slower (5120 x 27648, M = 1..16:
   // 247 slabs of 7 tiles 2-15% behind 216 of 8), so slabs stay GW * T tiles wide.
+  // The general kernels exist in one configuration: two k-groups of four wavefronts, two
+  // tiles each, two steps in flight (8-tile slabs).
+  if (d.gen) {
+    c.KG = 2;
+    c.GW = 4;
+    c.T = 2;
+    c.U = 2;
+  }
   const int eSW = ls_env("HQ_DECODE_LS_SW", 0);
   if (eSW >= 1 && eSW <= c.GW * c.T) c.SW = eSW;
   const int eS = ls_env("HQ_DECODE_LS_S", 0);

@@ -124,7 +124,7 @@ hipError_t launch_prefill(int fmt, int dtype, const PrefillConfig& c, void* ws, 
 
 // Whether this build has the general kernels (a bias, groups that are multiples of 32 but
 // not of 128); without them such calls fail with HQ_ERR_UNSUPPORTED.
-constexpr bool kGeneralKernels = false;
+constexpr bool kGeneralKernels = true;
 
 // Counter area at the start of every workspace, the same for all shapes and both kernels
 // so that one workspace can serve calls of different shapes (the counters stay zero

@@ -39,8 +39,10 @@ constexpr int kValuFirst = 32;
 constexpr int kValuPerFrag = 7;
 
 // Dequantised B fragment with the group scale applied. s2 holds the fp16 scale twice.
-template <int FMT, int DT>
-__device__ __forceinline__ u4 dq_scaled(const u4& w, int c, uint32_t s_f16, const DqConst& k) {
+// GEN (int4): `add` is the weight of code 8, e = 8 s + b, as fp16 bits (fp16 activations) or
+// the bias b as fp32 bits (bf16 activations), so that the fragment is q * s + b.
+template <int FMT, int DT, bool GEN = false>
+__device__ __forceinline__ u4 dq_scaled(const u4& w, int c, uint32_t s_f16, const DqConst& k, uint32_t add = 0) {
   if constexpr (DT == HQ_DTYPE_F16) {
     const h2 s2 = bits_h2(s_f16 | (s_f16 << 16));
     u4 q;
@@ -49,6 +51,13 @@ __device__ __forceinline__ u4 dq_scaled(const u4& w, int c, uint32_t s_f16, cons
     } else {
       const uint32_t word = w[c >> 1];
       q = (c & 1) ? dq_tern2<1>(word) : dq_tern2<0>(word);  // exact 2t; the epilogue halves
+    }
+    if constexpr (GEN && FMT == HQ_FORMAT_INT4) {
+      const h2 e2 = bits_h2(add | (add << 16));
+      return u4{h2_bits(__builtin_elementwise_fma(bits_h2(q[0]), s2, e2)),
+                h2_bits(__builtin_elementwise_fma(bits_h2(q[1]), s2, e2)),
+                h2_bits(__builtin_elementwise_fma(bits_h2(q[2]), s2, e2)),
+                h2_bits(__builtin_elementwise_fma(bits_h2(q[3]), s2, e2))};
     }
     return u4{h2_bits(bits_h2(q[0]) * s2), h2_bits(bits_h2(q[1]) * s2), h2_bits(bits_h2(q[2]) * s2),
               h2_bits(bits_h2(q[3]) * s2)};
@@ -60,7 +69,7 @@ __device__ __forceinline__ u4 dq_scaled(const u4& w, int c, uint32_t s_f16, cons
       const uint32_t x = w[c];
       const uint32_t lo = x & 0x0F0F0F0Fu, hi = (x >> 4) & 0x0F0F0F0Fu;
       // byte b of lo holds element {0,4,1,5}[b], of hi element {2,6,3,7}[b] (nibble order of hq_layout.hpp)
-      const float ms = -8.0f * s;
+      const float ms = GEN ? __builtin_bit_cast(float, add) : -8.0f * s;
       v[0] = __builtin_fmaf((float)((lo >> 0) & 0xFFu), s, ms);
       v[4] = __builtin_fmaf((float)((lo >> 8) & 0xFFu), s, ms);
       v[1] = __builtin_fmaf((float)((lo >> 16) & 0xFFu), s, ms);
@@ -112,7 +121,8 @@ __device__ __forceinline__ void tile_geom(const GemmDesc& d, uint32_t nb, uint32
 // registers never weigh on the whole-tile pipeline.
 // One-row-wave 128-row tiles are held to 256 VGPRs so that two workgroups share a CU (their
 // barriers are independent, so one's dequantisation overlaps the other's MFMAs).
-template <int FMT, int DT, int RT, int WM, bool SKP>
+// GEN: the general kernels (one scale per 32-wide k chunk, optional int4 bias), 64-row tiles.
+template <int FMT, int DT, int RT, int WM, bool SKP, bool GEN = false>
 __global__ void __launch_bounds__(256 * WM, WM == 1 && RT == 8 ? 2 : 1) hq_prefill_kernel(const GemmDesc d, const PrefillPlan pp) {
   constexpr uint32_t BM = 16u * RT * WM;
   constexpr uint32_t kStageBytes = BM * 256u;        // BM rows x 128 fp16
@@ -120,7 +130,7 @@ __global__ void __launch_bounds__(256 * WM, WM == 1 && RT == 8 ? 2 : 1) hq_prefi
   constexpr uint32_t kWavePart = RT * kTilesPerWave * 1024u;  // one wavefront's share of it
   // The explicit order holds more values live; the fp16 128-row kernels make room for it with
   // a weight ring of two k-blocks (one ahead: a k-block's MFMAs outlast a load's latency).
-  constexpr bool kOrdered = DT == HQ_DTYPE_F16 && RT == 8;
+  constexpr bool kOrdered = DT == HQ_DTYPE_F16 && RT == 8 && !GEN;
   constexpr int kRing = kOrdered ? 2 : 3;
   // Partial tiles are stored and loaded with the sc1 cache policy: agent-coherent, so a
   // store that has completed is visible to loads from any XCD.
@@ -206,8 +216,11 @@ __global__ void __launch_bounds__(256 * WM, WM == 1 && RT == 8 ? 2 : 1) hq_prefi
       const bool ok = ct < sg.ntiles;
       wrs[t] = make_rsrc(reinterpret_cast<const char*>(sg.Wp) + (size_t)(ok ? ct : 0u) * tile_bytes, ok ? tile_bytes : 0u);
     }
-    // Scale of column 16 ct + c16 (clamped to N - 1: columns past N are not stored).
-    const __amdgpu_buffer_rsrc_t srs = make_rsrc(sg.S, ((nkb / d.gkb - 1u) * sg.lds + sg.N) * 2u);
+    // Scale of column 16 ct + c16 (clamped to N - 1: columns past N are not stored). GEN: the
+    // scale (and bias) of that column in chunk g4 of the k-block, row (4 kb + g4) / g32.
+    const uint32_t srows = GEN ? 4u * nkb / d.g32 : nkb / d.gkb;
+    const __amdgpu_buffer_rsrc_t srs = make_rsrc(sg.S, ((srows - 1u) * sg.lds + sg.N) * 2u);
+    const __amdgpu_buffer_rsrc_t brs = make_rsrc(sg.B, GEN && sg.B ? ((srows - 1u) * sg.lds + sg.N) * 4u : 0u);
     uint32_t soff[kTilesPerWave];
 #pragma unroll
     for (int t = 0; t < kTilesPerWave; ++t) soff[t] = min((ct0 + t) * 16u + c16, sg.N - 1u) * 2u;
@@ -216,9 +229,11 @@ __global__ void __launch_bounds__(256 * WM, WM == 1 && RT == 8 ? 2 : 1) hq_prefi
     // Column tiles past the segment have an empty descriptor and read zero.
     u4 wr[kRing][kTilesPerWave];
     uint32_t sr[kRing][kTilesPerWave];
+    uint32_t br[GEN ? kRing : 1][kTilesPerWave];
     auto load_b = [&](int slot, uint32_t kb) {
       const uint32_t kc = min(kb, kz - 1u);
       const uint32_t so = kc / d.gkb * sg.lds * 2u;
+      const uint32_t grow = GEN ? plan_div(4u * kc + g4, d.g32, d.g32_m) : 0u;
 #pragma unroll
       for (int t = 0; t < kTilesPerWave; ++t) {
         if constexpr (FMT == HQ_FORMAT_INT4) {
@@ -227,9 +242,15 @@ __global__ void __launch_bounds__(256 * WM, WM == 1 && RT == 8 ? 2 : 1) hq_prefi
           const u2 v = __builtin_amdgcn_raw_buffer_load_b64(wrs[t], lane * 8u, kc * 512u, 0);
           wr[slot][t] = u4{v[0], v[1], 0u, 0u};
         }
-        sr[slot][t] = __builtin_amdgcn_raw_buffer_load_b16(srs, soff[t], so, 0);
+        if constexpr (GEN) {
+          sr[slot][t] = __builtin_amdgcn_raw_buffer_load_b16(srs, soff[t] + grow * sg.lds * 2u, 0, 0);
+          br[slot][t] = __builtin_amdgcn_raw_buffer_load_b32(brs, soff[t] * 2u + grow * sg.lds * 4u, 0, 0);
+        } else {
+          sr[slot][t] = __builtin_amdgcn_raw_buffer_load_b16(srs, soff[t], so, 0);
+        }
       }
     };
+    const bool has_bias = GEN && sg.B != nullptr;
 
 #pragma unroll
     for (int r = 0; r < RT; ++r)
@@ -237,10 +258,11 @@ __global__ void __launch_bounds__(256 * WM, WM == 1 && RT == 8 ? 2 : 1) hq_prefi
       for (int t = 0; t < kTilesPerWave; ++t) acc[r][t] = f4{0.f, 0.f, 0.f, 0.f};
 
     // One k-block. Issue order per step: A(kb + 1) to LDS, then B(kb + kRing - 1) to
-    // registers, so at the top of the next step vmcnt((kRing - 2) * 2 * kTilesPerWave) leaves
-    // only the B loads of later k-blocks in flight (none with a ring of two).
+    // registers, so at the top of the next step vmcnt((kRing - 2) * kBLoads) leaves only the
+    // B loads of later k-blocks in flight (none with a ring of two).
+    constexpr int kBLoads = (GEN ? 3 : 2) * kTilesPerWave;  // weight, scale (and bias) loads per k-block
     auto step = [&](uint32_t kb, int slot) {
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm((kRing - 2) * 2 * kTilesPerWave));  // A(kb), B(kb) landed for this wave
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm((kRing - 2) * kBLoads));  // A(kb), B(kb) landed for this wave
       __syncthreads();                                            // ... for every wave; stage (kb+1)&1 is free
       load_a((kb + 1) & 1u, kb + 1);
       load_b((slot + kRing - 1) % kRing, kb + kRing - 1);
@@ -254,11 +276,35 @@ __global__ void __launch_bounds__(256 * WM, WM == 1 && RT == 8 ? 2 : 1) hq_prefi
 #pragma unroll
         for (int t = 0; t < kTilesPerWave; ++t)
           sc[t] = FMT == HQ_FORMAT_TERNARY2 && (sr[slot][t] & 0x7C00u) == 0x7C00u ? 0u : sr[slot][t];
+        // GEN: chunk c's scale and addend of tile t come from lane 16 c + c16 of the loads.
+        uint32_t gsc[GEN ? 4 : 1][kTilesPerWave], gadd[GEN ? 4 : 1][kTilesPerWave];
+        if constexpr (GEN) {
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int t = 0; t < kTilesPerWave; ++t) {
+              const uint32_t sv = (uint32_t)__builtin_amdgcn_ds_bpermute((int)((16u * c + c16) * 4u), (int)sc[t]) & 0xFFFFu;
+              const uint32_t bv = (uint32_t)__builtin_amdgcn_ds_bpermute((int)((16u * c + c16) * 4u), (int)br[slot][t]);
+              gsc[c][t] = sv;
+              if constexpr (FMT == HQ_FORMAT_INT4) {
+                const float s32 = f16_to_f32((uint16_t)sv);
+                if constexpr (DT == HQ_DTYPE_F16)  // e = 8 s + b (0 without a bias), as fp16
+                  gadd[c][t] = has_bias ? f32_to_out<HQ_DTYPE_F16>(__builtin_fmaf(8.0f, s32, __builtin_bit_cast(float, bv))) : 0u;
+                else  // the bias b (or -8 s), fp32
+                  gadd[c][t] = has_bias ? bv : __builtin_bit_cast(uint32_t, -8.0f * s32);
+              } else {
+                gadd[c][t] = 0u;
+              }
+            }
+        }
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
           u4 b[kTilesPerWave];
 #pragma unroll
-          for (int t = 0; t < kTilesPerWave; ++t) b[t] = dq_scaled<FMT, DT>(wr[slot][t], c, sc[t], dqk);
+          for (int t = 0; t < kTilesPerWave; ++t) {
+            if constexpr (GEN) b[t] = dq_scaled<FMT, DT, true>(wr[slot][t], c, gsc[c][t], dqk, gadd[c][t]);
+            else b[t] = dq_scaled<FMT, DT>(wr[slot][t], c, sc[t], dqk);
+          }
 #pragma unroll
           for (int r = 0; r < RT; ++r) {
             const u4 a = *reinterpret_cast<const u4*>(sbase + (wrow0 + 16u * r) * 256u + ldsoff[c]);
@@ -452,7 +498,7 @@ uint32_t assign_blocks(GemmDesc& d) {
 
 int env_int(const char* name, int dflt);
 
-template <int FMT, int DT, int RT, int WM>
+template <int FMT, int DT, int RT, int WM, bool GEN = false>
 hipError_t launch_rt(const PrefillLaunch& c, void* ws, hipStream_t stream) {
   constexpr uint32_t BM = 16u * RT * WM;
   GemmDesc d = c.d;
@@ -477,19 +523,20 @@ hipError_t launch_rt(const PrefillLaunch& c, void* ws, hipStream_t stream) {
   const size_t lds = prefill_lds<FMT, DT, RT, WM>();
   // More than the default 64 KiB of dynamic LDS needs an opt-in per kernel (idempotent).
   static const hipError_t attr =
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&hq_prefill_kernel<FMT, DT, RT, WM, false>),
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&hq_prefill_kernel<FMT, DT, RT, WM, false, GEN>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess
           ? hipErrorInvalidConfiguration
-          : hipFuncSetAttribute(reinterpret_cast<const void*>(&hq_prefill_kernel<FMT, DT, RT, WM, true>),
+          : hipFuncSetAttribute(reinterpret_cast<const void*>(&hq_prefill_kernel<FMT, DT, RT, WM, true, GEN>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   if (attr != hipSuccess) return attr;
   // Stream-K part first, then the whole tiles (stream order: one after the other).
   if (c.psk) {
-    hipLaunchKernelGGL((hq_prefill_kernel<FMT, DT, RT, WM, true>), dim3(c.psk), dim3(256 * WM), lds, stream, d, pp);
+    hipLaunchKernelGGL((hq_prefill_kernel<FMT, DT, RT, WM, true, GEN>), dim3(c.psk), dim3(256 * WM), lds, stream, d, pp);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
-  if (c.dp) hipLaunchKernelGGL((hq_prefill_kernel<FMT, DT, RT, WM, false>), dim3(c.dp), dim3(256 * WM), lds, stream, d, pp);
+  if (c.dp)
+    hipLaunchKernelGGL((hq_prefill_kernel<FMT, DT, RT, WM, false, GEN>), dim3(c.dp), dim3(256 * WM), lds, stream, d, pp);
   return hipGetLastError();
 }
 
@@ -542,6 +589,7 @@ int prefill_slots(int fmt, int RT, int WM) {
 
 template <int FMT, int DT>
 hipError_t launch_fd(const PrefillLaunch& c, void* ws, hipStream_t stream) {
+  if (c.d.gen) return c.RT == 4 && c.WM == 1 ? launch_rt<FMT, DT, 4, 1, true>(c, ws, stream) : hipErrorInvalidConfiguration;
   if (c.RT == 4) return launch_rt<FMT, DT, 4, 1>(c, ws, stream);
   if (c.RT == 16) return launch_rt<FMT, DT, 16, 1>(c, ws, stream);
   if (c.WM == 1) return launch_rt<FMT, DT, 8, 1>(c, ws, stream);
@@ -605,6 +653,10 @@ PrefillConfig choose_prefill(int fmt, const GemmDesc& d, size_t ws_cap) {
   PrefillConfig c{};
   int RT = 8, WM = 2;
   prefill_shape(d.M, RT, WM);
+  if (d.gen) {  // the general kernels: 64-row tiles only
+    RT = 4;
+    WM = 1;
+  }
   // 128-row tiles too few for the slots would be split along K; when those pieces would be
   // short (under 64 k-blocks) 64-row tiles do better: twice the tiles, split half as often
   // or not at all. Measured on MI355X: fused QKV (N = 7168) M = 256..1024 7-38% faster,

@@ -153,14 +153,19 @@ void hqo_repack_ref(const uint32_t* src, uint32_t* dst, uint32_t K, uint32_t N) 
     }
 }
 
-/* One dequantised weight, exactly as the reference's host loop forms it. */
-static inline float dq_int4(const uint32_t* w, const uint16_t* s, uint32_t N, uint32_t group,
-                            uint32_t k, uint32_t n) {
+/* One dequantised weight, exactly as the reference's host loop forms it; b is the caller's
+ * fp32 bias array [K/group][N], or NULL for the reference's own bias -8 * scale. */
+static inline float dq_int4b(const uint32_t* w, const uint16_t* s, const float* b, uint32_t N,
+                             uint32_t group, uint32_t k, uint32_t n) {
     uint32_t q = (w[(size_t)(k / 8) * N + n] >> (4 * (k % 8))) & 0xFu;
     float scale = hqo_f16_to_f32(s[(size_t)(k / group) * N + n]);
-    float bias = -8.0f * scale;
+    float bias = b ? b[(size_t)(k / group) * N + n] : -8.0f * scale;
     float prod = (float)q * scale;   /* -ffp-contract=off keeps this a separate rounding */
     return prod + bias;
+}
+static inline float dq_int4(const uint32_t* w, const uint16_t* s, uint32_t N, uint32_t group,
+                            uint32_t k, uint32_t n) {
+    return dq_int4b(w, s, NULL, N, group, k, n);
 }
 
 /* Ternary: t = c - 1, w = d * t; a non-finite scale drops the group as in native_decoder.cu:174. */
@@ -179,6 +184,13 @@ void hqo_dequant_int4(const uint32_t* w, const uint16_t* s, uint32_t K, uint32_t
 #pragma omp parallel for schedule(static)
     for (long long k = 0; k < (long long)K; ++k)
         for (uint32_t n = 0; n < N; ++n) wdq[(size_t)k * N + n] = dq_int4(w, s, N, group, (uint32_t)k, n);
+}
+
+void hqo_dequant_int4_bias(const uint32_t* w, const uint16_t* s, const float* bias, uint32_t K, uint32_t N,
+                           uint32_t group, float* wdq) {
+#pragma omp parallel for schedule(static)
+    for (long long k = 0; k < (long long)K; ++k)
+        for (uint32_t n = 0; n < N; ++n) wdq[(size_t)k * N + n] = dq_int4b(w, s, bias, N, group, (uint32_t)k, n);
 }
 
 int hqo_dequant_ternary2(const uint32_t* w, const uint16_t* s, uint32_t K, uint32_t N, uint32_t group,
@@ -215,6 +227,12 @@ void hqo_gemm_f32(const float* X, const float* W, float* Y, uint32_t M, uint32_t
 int hqo_qgemm(const uint16_t* X, int xdtype, size_t ldx, int fmt, const uint32_t* w,
               const uint16_t* s, uint32_t M, uint32_t K, uint32_t N, uint32_t group, float* Y,
               int threads) {
+    return hqo_qgemm_bias(X, xdtype, ldx, fmt, w, s, NULL, M, K, N, group, Y, threads);
+}
+
+int hqo_qgemm_bias(const uint16_t* X, int xdtype, size_t ldx, int fmt, const uint32_t* w,
+                   const uint16_t* s, const float* bias, uint32_t M, uint32_t K, uint32_t N,
+                   uint32_t group, float* Y, int threads) {
     const uint32_t NB = 128;
     uint32_t nblk = (N + NB - 1) / NB;
     int bad = 0;
@@ -232,7 +250,7 @@ int hqo_qgemm(const uint16_t* X, int xdtype, size_t ldx, int fmt, const uint32_t
             for (uint32_t n = n0; n < n1; ++n) Y[(size_t)m * N + n] = 0.0f;
         for (uint32_t k = 0; k < K; ++k) {
             if (fmt == HQO_INT4) {
-                for (uint32_t n = n0; n < n1; ++n) wrow[n - n0] = dq_int4(w, s, N, group, k, n);
+                for (uint32_t n = n0; n < n1; ++n) wrow[n - n0] = dq_int4b(w, s, bias, N, group, k, n);
             } else {
                 for (uint32_t n = n0; n < n1; ++n)
                     if (dq_ternary(w, s, N, group, k, n, &wrow[n - n0])) bad = 1;

@@ -9,9 +9,12 @@
  * reference repository root):
  *   hqo_repack_ref        hydrogen/src/model/marlin_gemm.cu:432-467 (loop 446-455)
  *   hqo_dequant_int4      hydrogen/src/model/marlin_gemm.cu:495-512 (w = q*s + b, b = -8*s, :483-488)
+ *   hqo_dequant_int4_bias the same with a caller-given fp32 bias per group (marlin_gemm.hpp:100-107,
+ *                         the forward's d_biases; marlin_gemm.cu:195-196 reads it per 32-wide chunk)
  *   hqo_dequant_ternary2  hydrogen/src/model/native_decoder.cu:184-186 (w = d * t)
  *   hqo_gemm_f32          hydrogen/src/model/marlin_gemm.cu:52-70 (fp32, k ascending, FMA)
  *   hqo_qgemm             the two above fused row by row (bit-identical to running them in turn)
+ *   hqo_qgemm_bias        hqo_qgemm with the bias of hqo_dequant_int4_bias (NULL: hqo_qgemm)
  *   hqo_fidelity          hydrogen/src/model/marlin_gemm.cu:619-644 (max |d|, MSE in fp64)
  *   hqo_tq1_0_code        hydrogen/src/model/native_decoder.cu:31-36, 87-101 (base-3 trits of a TQ1_0 block)
  *   hqo_gemv_tq1_0        hydrogen/src/model/native_decoder.cu:155-206 (kernel_gemv_tq1_0, any M)
@@ -64,6 +67,11 @@ void hqo_repack_ref(const uint32_t* src_linear, uint32_t* dst, uint32_t K, uint3
  * Wdq[k*N + n] = (float)q * scale + bias, evaluated without contraction. */
 void hqo_dequant_int4(const uint32_t* w_linear, const uint16_t* scales_f16, uint32_t K, uint32_t N,
                       uint32_t group, float* wdq);
+/* marlin_gemm.cu:495-512 with the caller's fp32 bias [K/group][N] (NULL: -8 * scale):
+ * Wdq[k*N + n] = (float)q * scale + bias[(k/group)*N + n], evaluated without contraction. Any group
+ * that divides K (the reference takes one per 32-wide chunk: group % 32 == 0). */
+void hqo_dequant_int4_bias(const uint32_t* w_linear, const uint16_t* scales_f16, const float* bias,
+                           uint32_t K, uint32_t N, uint32_t group, float* wdq);
 /* native_decoder.cu:184-186: Wdq[k*N + n] = scale * (float)t, t = c - 1. Returns -1 if a code 3 is present. */
 int hqo_dequant_ternary2(const uint32_t* w_linear, const uint16_t* scales_f16, uint32_t K, uint32_t N,
                          uint32_t group, float* wdq);
@@ -76,6 +84,10 @@ void hqo_gemm_f32(const float* X, const float* W, float* Y, uint32_t M, uint32_t
 int hqo_qgemm(const uint16_t* X, int xdtype, size_t ldx, int fmt, const uint32_t* w_linear,
               const uint16_t* scales_f16, uint32_t M, uint32_t K, uint32_t N, uint32_t group,
               float* Y, int threads);
+/* hqo_qgemm with an int4 bias (hqo_dequant_int4_bias semantics; NULL gives hqo_qgemm). */
+int hqo_qgemm_bias(const uint16_t* X, int xdtype, size_t ldx, int fmt, const uint32_t* w_linear,
+                   const uint16_t* scales_f16, const float* bias, uint32_t M, uint32_t K, uint32_t N,
+                   uint32_t group, float* Y, int threads);
 /* marlin_gemm.cu:619-644: max |a - b| and mean squared difference, accumulated in fp64. */
 void hqo_fidelity(const float* a, const float* b, size_t count, double* max_abs, double* mse);
 

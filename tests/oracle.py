@@ -51,6 +51,9 @@ def lib() -> ctypes.CDLL:
     L.hqo_gemm_f32.argtypes = [vp, vp, vp, u32, u32, u32, i32]
     L.hqo_qgemm.restype = i32
     L.hqo_qgemm.argtypes = [vp, i32, sz, i32, vp, vp, u32, u32, u32, u32, vp, i32]
+    L.hqo_qgemm_bias.restype = i32
+    L.hqo_qgemm_bias.argtypes = [vp, i32, sz, i32, vp, vp, vp, u32, u32, u32, u32, vp, i32]
+    L.hqo_dequant_int4_bias.argtypes = [vp, vp, vp, u32, u32, u32, vp]
     L.hqo_fidelity.argtypes = [vp, vp, sz, ctypes.POINTER(dbl), ctypes.POINTER(dbl)]
     L.hqo_tq1_0_code.restype = u32
     L.hqo_tq1_0_code.argtypes = [vp, u32]
@@ -120,6 +123,17 @@ def dequant(fmt: int, linear: np.ndarray, scales: np.ndarray, K: int, N: int, gr
     return out
 
 
+def dequant_int4_bias(linear: np.ndarray, scales: np.ndarray, bias: np.ndarray | None, K: int, N: int,
+                      group: int) -> np.ndarray:
+    """The reference's host dequantisation w = q * s + b with a caller bias (fp32 [K/group, N])."""
+    w = np.ascontiguousarray(linear, dtype=np.uint32)
+    s = np.ascontiguousarray(scales, dtype=np.uint16)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    out = np.empty((K, N), dtype=np.float32)
+    lib().hqo_dequant_int4_bias(_p(w), _p(s), None if b is None else _p(b), K, N, group, _p(out))
+    return out
+
+
 def gemm_f32(X: np.ndarray, W: np.ndarray, threads: int = 8) -> np.ndarray:
     X = np.ascontiguousarray(X, dtype=np.float32)
     W = np.ascontiguousarray(W, dtype=np.float32)
@@ -142,6 +156,22 @@ def qgemm(fmt: int, X_bits: np.ndarray, xdtype: int, linear: np.ndarray, scales:
     rc = lib().hqo_qgemm(_p(X), xdtype, K, fmt, _p(w), _p(s), M, K, N, group, _p(Y), threads)
     if rc == -1:
         raise ValueError("ternary code 3 in weight")
+    if rc != 0:
+        raise MemoryError("oracle allocation failed")
+    return Y
+
+
+def qgemm_bias(X_bits: np.ndarray, xdtype: int, linear: np.ndarray, scales: np.ndarray, bias: np.ndarray | None,
+               N: int, group: int = 128, threads: int = 8) -> np.ndarray:
+    """qgemm for int4 weights with the reference's bias: w = q * s + b (b fp32 [K/group, N])."""
+    X = np.ascontiguousarray(X_bits, dtype=np.uint16)
+    M, K = X.shape
+    w = np.ascontiguousarray(linear, dtype=np.uint32)
+    s = np.ascontiguousarray(scales, dtype=np.uint16)
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32)
+    Y = np.empty((M, N), dtype=np.float32)
+    rc = lib().hqo_qgemm_bias(_p(X), xdtype, K, INT4, _p(w), _p(s), None if b is None else _p(b), M, K, N, group,
+                              _p(Y), threads)
     if rc != 0:
         raise MemoryError("oracle allocation failed")
     return Y
@@ -199,17 +229,29 @@ def gen_tq1_0(seed: int, N: int, K: int, nonfinite_every: int = 0) -> np.ndarray
 
 # ------------------------------------------------------------ problem builder
 class Problem:
-    """Seeded synthetic inputs of one qGEMM case (the distributions of the benchmark configs)."""
+    """Seeded synthetic inputs of one qGEMM case (the distributions of the benchmark configs).
+    bias: None (zero point 8), "random" (fp32 bias -8 s + N(0, 0.02) per group and column: the
+    weight of code 8 becomes a small random offset) or "minus8s" (exactly -8 s, the reference's
+    own data)."""
 
     def __init__(self, fmt: int, M: int, K: int, N: int, group: int = 128, xdtype: int = F16, seed: int = 42,
-                 x_sigma: float = 1.0, s_sigma: float = 0.02):
+                 x_sigma: float = 1.0, s_sigma: float = 0.02, bias: str | None = None):
         self.fmt, self.M, self.K, self.N, self.group, self.xdtype, self.seed = fmt, M, K, N, group, xdtype, seed
         self.X = gen_normal(seed, 1, M * K, x_sigma, False, xdtype).reshape(M, K)
         self.scales = gen_normal(seed, 2, (K // group) * N, s_sigma, True, F16).reshape(K // group, N)
         self.W = gen_int4(seed, 3, K, N) if fmt == INT4 else gen_ternary(seed, 3, K, N)
+        self.bias = None
+        if bias is not None:
+            s32 = to_f32(self.scales, F16)
+            self.bias = (-8.0 * s32).astype(np.float32)
+            if bias == "random":
+                off = to_f32(gen_normal(seed, 4, (K // group) * N, 0.02, False, F16), F16).reshape(K // group, N)
+                self.bias = (self.bias + off).astype(np.float32)
 
     def reference(self, rows=None, threads: int = 8) -> np.ndarray:
         X = self.X if rows is None else self.X[rows]
+        if self.bias is not None:
+            return qgemm_bias(X, self.xdtype, self.W, self.scales, self.bias, self.N, self.group, threads)
         return qgemm(self.fmt, X, self.xdtype, self.W, self.scales, self.N, self.group, threads)
 
 

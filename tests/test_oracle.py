@@ -243,6 +243,65 @@ def test_qgemm_one_hot_rows_select_weight_rows(fmt):
     assert np.array_equal(Y, Wdq[ks])
 
 
+# ---------------------------------------------------------------- caller bias, small groups
+# The reference's forward takes any per-group fp32 bias (marlin_gemm.hpp:100-107) and reads
+# one scale and bias per 32-wide chunk (marlin_gemm.cu:191-196), so groups of 32 and 64 are valid.
+@pytest.mark.parametrize("g", [32, 64, 128, 256])
+def test_dequant_int4_bias_reference_form(g):
+    K, N = 512, 24
+    q = dense_codes_int4(K, N)
+    s_bits = O.gen_normal(12, 1, (K // g) * N, 0.02, True).reshape(K // g, N)
+    b = (RNG.standard_normal((K // g, N)) * 0.05).astype(np.float32)
+    wdq = O.dequant_int4_bias(pack_linear_int4(q).ravel(), s_bits, b, K, N, g)
+    sk = np.repeat(O.to_f32(s_bits, O.F16), g, axis=0)
+    bk = np.repeat(b, g, axis=0)
+    # numpy float32: q * s rounded, then + b rounded (the reference's host form)
+    ref = q.astype(np.float32) * sk + bk
+    assert np.array_equal(wdq.view(np.uint32), ref.view(np.uint32))
+    # a group index off by one (k // g + 1) or a transposed bias would not match
+    assert not np.array_equal(wdq, q.astype(np.float32) * sk + np.roll(bk, g, axis=0))
+
+
+@pytest.mark.parametrize("g", [32, 128])
+def test_bias_minus_8s_is_the_zero_point_form_bitwise(g):
+    P = O.Problem(O.INT4, 5, 512, 40, g, O.F16, seed=23, bias="minus8s")
+    Yb = P.reference()
+    Y0 = O.qgemm(O.INT4, P.X, O.F16, P.W, P.scales, P.N, g)
+    assert np.array_equal(Yb.view(np.uint32), Y0.view(np.uint32))
+    Wb = O.dequant_int4_bias(P.W, P.scales, P.bias, P.K, P.N, g)
+    W0 = O.dequant(O.INT4, P.W, P.scales.ravel(), P.K, P.N, g)
+    assert np.array_equal(Wb.view(np.uint32), W0.view(np.uint32))
+    # NULL bias is the same function
+    Yn = O.qgemm_bias(P.X, O.F16, P.W, P.scales, None, P.N, g)
+    assert np.array_equal(Yn.view(np.uint32), Y0.view(np.uint32))
+
+
+@pytest.mark.parametrize("g", [32, 64, 128])
+def test_qgemm_bias_against_float64(g):
+    P = O.Problem(O.INT4, 4, 512, 48, g, O.F16, seed=24, bias="random")
+    Y = P.reference()
+    X = O.to_f32(P.X, O.F16)
+    Wdq = O.dequant_int4_bias(P.W, P.scales, P.bias, P.K, P.N, g)
+    ref = X.astype(np.float64) @ Wdq.astype(np.float64)
+    assert np.all(np.abs(Y - ref) <= fp32_bound(X, Wdq))
+    # equals dequant-then-gemm bit for bit
+    assert np.array_equal(Y.view(np.uint32), O.gemm_f32(X, Wdq).view(np.uint32))
+
+
+def test_qgemm_bias_constant_code_closed_form():
+    # constant code c: Y[m, n] = sum_g (c s[g, n] + b[g, n]) * sum_{k in g} x[m, k], groups of 32
+    K, N, g, M, c = 512, 20, 32, 3, 5
+    W = np.full((K // 8) * N, int("".join([f"{c:x}"] * 8), 16), dtype=np.uint32)
+    X = O.gen_normal(3, 1, M * K).reshape(M, K)
+    S = O.gen_normal(3, 2, (K // g) * N, 0.02, True).reshape(K // g, N)
+    B = (RNG.standard_normal((K // g, N)) * 0.05).astype(np.float32)
+    Y = O.qgemm_bias(X, O.F16, W, S, B, N, g)
+    xf = O.to_f32(X, O.F16).astype(np.float64)
+    wg = c * O.to_f32(S, O.F16).astype(np.float64) + B.astype(np.float64)  # [G, N]
+    ref = xf.reshape(M, K // g, g).sum(axis=2) @ wg
+    assert np.allclose(Y, ref, rtol=1e-5, atol=1e-5)
+
+
 def test_qgemm_constant_code_closed_form():
     # constant code c: Y[m, n] = sum_g (c - 8) * s[g, n] * sum_{k in g} x[m, k]
     K, N, g, M, c = 512, 20, 128, 3, 13
