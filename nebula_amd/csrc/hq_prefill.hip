@@ -12,7 +12,9 @@
 // gfx950 buffer->LDS path (buffer_load_dwordx4 ... lds), in a layout whose 16-byte units
 // are XOR-swizzled by row so the ds_read_b128 fragment reads are bank-conflict free.
 // Weights go straight from HBM into registers in the tile layout (hq_layout.hpp), which
-// already is the v_mfma_f32_16x16x32 B-fragment order. Accumulation is fp32 (AGPRs).
+// already is the v_mfma_f32_16x16x32 fragment order; they are the MFMA's A operand and the
+// activations its B operand, so each result is the transposed 16 x 16 tile and a lane holds
+// four consecutive output columns of one row (8-byte output stores). Accumulation is fp32.
 // Workgroups are renumbered so that each XCD owns a contiguous band of row blocks and
 // keeps its activation rows resident in its own L2.
 #include <hip/hip_runtime.h>
@@ -167,29 +169,40 @@ __global__ void __launch_bounds__(256 * WM, WM == 1 && RT == 8 ? 2 : 1) hq_prefi
 
   f4 acc[RT][kTilesPerWave];
 
-  // Epilogue of a finished tile: tile (r, t), lane -> column 16 (ct0 + t) + c16, rows
-  // 16 r + 4 g4 + v. Rows past M fall outside the descriptor; columns past N get an
-  // out-of-range offset. Only row tiles r0 <= r < r1 (compile-time after unrolling).
+  // Epilogue of a finished tile. The MFMAs take the weight fragment as their A operand and the
+  // activations as B, so each 16 x 16 result is the transposed tile: lane -> activation row
+  // 16 r + c16 and the four consecutive output columns 16 (ct0 + t) + 4 g4 + v, one 8-byte
+  // store (the lanes of a row write its 128 bytes of the wavefront's 64 columns in four
+  // instructions). Rows past M fall outside the descriptor; columns past N, and outputs whose
+  // rows are not 8-byte aligned, take 2-byte stores. Only row tiles r0 <= r < r1
+  // (compile-time after unrolling).
   auto store_tile = [&](uint32_t s, uint32_t m0, uint32_t ct0, int r0 = 0, int r1 = RT) {
     constexpr float post = (FMT == HQ_FORMAT_TERNARY2 && DT == HQ_DTYPE_F16) ? 0.5f : 1.0f;
     const SegDesc& sg = d.seg[s];
     const uint32_t rows = min(BM, d.M - m0);
     const __amdgpu_buffer_rsrc_t yr =
         make_rsrc(reinterpret_cast<char*>(sg.Y) + (size_t)m0 * (size_t)sg.ldy * 2u, rows * (uint32_t)sg.ldy * 2u);
+    const bool wide = ((reinterpret_cast<uintptr_t>(sg.Y) | ((uint32_t)sg.ldy * 2u)) & 7u) == 0u;  // uniform
 #pragma unroll
     for (int t = 0; t < kTilesPerWave; ++t) {
-      const uint32_t n = (ct0 + t) * 16u + c16;
-      const uint32_t cbase = n < sg.N ? n * 2u : kOutOfRange;
+      const uint32_t n0 = (ct0 + t) * 16u + 4u * g4;
 #pragma unroll
-      for (int r = 0; r < RT; ++r)
+      for (int r = 0; r < RT; ++r) {
+        if (r < r0 || r >= r1) continue;
+        const uint32_t row = wrow0 + 16u * r + c16;
+        const uint32_t o = (row * (uint32_t)sg.ldy + n0) * 2u;
+        const f4 v = acc[r][t] * post;
+        if (wide && n0 + 3u < sg.N) {
+          const u2 packed = {(uint32_t)f32_to_out<DT>(v[0]) | ((uint32_t)f32_to_out<DT>(v[1]) << 16),
+                             (uint32_t)f32_to_out<DT>(v[2]) | ((uint32_t)f32_to_out<DT>(v[3]) << 16)};
+          __builtin_amdgcn_raw_buffer_store_b64(packed, yr, o, 0, 0);
+        } else {
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          if (r < r0 || r >= r1) continue;
-          const uint32_t row = wrow0 + 16u * r + 4u * g4 + v;
-          __builtin_amdgcn_raw_buffer_store_b16(f32_to_out<DT>(acc[r][t][v] * post), yr,
-                                                cbase == kOutOfRange ? kOutOfRange : cbase + row * (uint32_t)sg.ldy * 2u,
-                                                0, 0);
+          for (int e = 0; e < 4; ++e)
+            __builtin_amdgcn_raw_buffer_store_b16(f32_to_out<DT>(v[e]), yr, n0 + e < sg.N ? o + 2u * e : kOutOfRange,
+                                                  0, 0);
         }
+      }
     }
   };
 
@@ -309,7 +322,7 @@ __global__ void __launch_bounds__(256 * WM, WM == 1 && RT == 8 ? 2 : 1) hq_prefi
           for (int r = 0; r < RT; ++r) {
             const u4 a = *reinterpret_cast<const u4*>(sbase + (wrow0 + 16u * r) * 256u + ldsoff[c]);
 #pragma unroll
-            for (int t = 0; t < kTilesPerWave; ++t) acc[r][t] = mfma16x16x32<DT>(a, b[t], acc[r][t]);
+            for (int t = 0; t < kTilesPerWave; ++t) acc[r][t] = mfma16x16x32<DT>(b[t], a, acc[r][t]);
           }
         }
         if constexpr (kOrdered) {
