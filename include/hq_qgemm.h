@@ -43,7 +43,10 @@ typedef enum hq_status {
     HQ_ERR_WORKSPACE = 5,    /* workspace missing or smaller than hq_workspace_bytes() */
     HQ_ERR_BAD_CODE = 6,     /* ternary code 3 met while repacking */
     HQ_ERR_DEVICE = 7,       /* HIP runtime error */
-    HQ_ERR_INTERNAL = 8
+    HQ_ERR_INTERNAL = 8,
+    HQ_ERR_FORMAT = 9,       /* malformed or unsupported GGUF data */
+    HQ_ERR_NOT_FOUND = 10,   /* no such GGUF tensor or metadata key */
+    HQ_ERR_IO = 11           /* a file could not be opened or mapped */
 } hq_status;
 
 typedef enum hq_dtype { HQ_DTYPE_F16 = 1, HQ_DTYPE_BF16 = 2 } hq_dtype;
@@ -156,6 +159,74 @@ hq_status hq_convert_tq1_0(const void* blocks, uint32_t K, uint32_t N, uint32_t*
  * same words as hq_convert_tq1_0 followed by hq_repack_ternary2. */
 hq_status hq_repack_tq1_0_device(const void* d_blocks, uint32_t K, uint32_t N, uint32_t* d_packed,
                                  uint16_t* d_scales, hq_stream stream);
+
+/* ---- GGUF container: replaces hydrogen::ModelLoader / parse_gguf (tensor_loader.hpp:14-53,
+ *      gguf_parser.hpp:33-145, tensor_loader.cpp) for the weights of this path ----
+ * The parse follows the reference's rules: magic "GGUF", versions 2 and 3, 64-bit counts,
+ * every metadata value type (arrays of any element type, nested), at most 4 tensor
+ * dimensions, tensor data starting at the header's end rounded up to general.alignment
+ * (default 32; 0 reads as 32), a tensor's byte size from its element count and its type's
+ * block traits (gguf_parser.hpp:108-139; unlisted types one byte per element), and a null data
+ * pointer for a tensor that extends past the end of the data. Malformed data gives
+ * HQ_ERR_FORMAT (the reference throws std::runtime_error). A weight matrix is a 2-D tensor
+ * with shape[0] = K (inputs, the contiguous dimension) and shape[1] = N (output rows), its
+ * blocks stored row by row ([N][K/256] for the 256-weight block types). */
+typedef struct hq_gguf hq_gguf; /* an open GGUF file or buffer */
+typedef struct hq_gguf_header_info {
+    uint32_t version;
+    uint64_t tensor_count, kv_count;
+    uint64_t alignment;            /* general.alignment, or 32 */
+    uint64_t header_bytes;         /* end of the tensor directory */
+    uint64_t tensor_data_offset;   /* start of the tensor data (aligned) */
+    uint64_t total_tensor_bytes;   /* largest offset + size over the tensors */
+    uint64_t file_bytes;
+} hq_gguf_header_info;
+typedef struct hq_gguf_tensor_info {
+    const char* name;              /* valid until hq_gguf_close */
+    uint32_t n_dims;
+    uint64_t shape[4];
+    uint32_t type;                 /* GGML type: 0 F32, 1 F16, 12 Q4_K, 34 / 143 TQ1_0, ... */
+    uint64_t offset;               /* relative to the tensor data */
+    uint64_t absolute_offset;
+    uint64_t size_bytes;
+    const void* data;              /* host address in the mapping, NULL past the end of the data */
+} hq_gguf_tensor_info;
+/* Memory-maps a file read-only and parses it (ModelLoader::load). */
+hq_status hq_gguf_open(const char* path, hq_gguf** out);
+/* Parses GGUF bytes the caller keeps alive until hq_gguf_close (parse_gguf). */
+hq_status hq_gguf_parse(const void* data, size_t bytes, hq_gguf** out);
+void hq_gguf_close(hq_gguf* g);
+hq_status hq_gguf_header(const hq_gguf* g, hq_gguf_header_info* out);
+hq_status hq_gguf_tensor_at(const hq_gguf* g, uint64_t index, hq_gguf_tensor_info* out);
+/* GGUFModel::find_tensor; HQ_ERR_NOT_FOUND if absent (the last tensor of a repeated name wins). */
+hq_status hq_gguf_find_tensor(const hq_gguf* g, const char* name, hq_gguf_tensor_info* out);
+/* Typed metadata (GGUFValue::as_*): integers and bools, floats, strings (len gets the length;
+ * buf receives at most buf_len - 1 bytes and a zero), arrays (element type and count). */
+hq_status hq_gguf_get_int(const hq_gguf* g, const char* key, int64_t* out);
+hq_status hq_gguf_get_float(const hq_gguf* g, const char* key, double* out);
+hq_status hq_gguf_get_string(const hq_gguf* g, const char* key, char* buf, size_t buf_len, size_t* len);
+hq_status hq_gguf_get_array(const hq_gguf* g, const char* key, uint32_t* elem_type, uint64_t* count);
+/* A TQ1_0 weight (type 34 or 143, the reference's 56-byte BlockTQ1_0) onto the device: its
+ * blocks are copied into d_staging (>= size_bytes, device) and repacked there by
+ * hq_repack_tq1_0_device into d_packed (hq_packed_words(HQ_FORMAT_TERNARY2, K, N) words) and
+ * d_scales (fp16 [K/256][N]); *K, *N receive the shape. Enqueued on `stream`; keep g open until
+ * the stream has passed the copy. The reference instead uploads the whole tensor section and
+ * decodes the blocks at every token (native_decoder.cu:849-857, 155-206). */
+hq_status hq_gguf_load_tq1_0(const hq_gguf* g, const char* name, void* d_staging, size_t staging_bytes,
+                             uint32_t* d_packed, uint16_t* d_scales, uint32_t* K, uint32_t* N,
+                             hq_stream stream);
+/* GGML Q4_K blocks (144 bytes per 256 weights: fp16 d and dmin, 12 bytes of 6-bit sub-block
+ * scales and mins, 128 bytes of 4-bit codes; weight = d * sc_j * q - dmin * m_j per 32-weight
+ * sub-block j) -> int4 linear codes u32 [K/8][N] (the hq_repack_int4 input), fp16 scales
+ * [K/32][N] (d * sc_j, rounded to fp16) and fp32 biases [K/32][N] (-dmin * m_j): use them with
+ * hq_gemm_w4a16(..., bias, ..., group = 32). Host to host, K % 256 == 0. The layout is GGML's
+ * published block_q4_K (the reference names the type, gguf_parser.hpp:44, 130, but has no
+ * decoder for it). */
+hq_status hq_convert_q4_k(const void* blocks, uint32_t K, uint32_t N, uint32_t* codes_linear,
+                          uint16_t* scales, float* bias);
+/* The same for a Q4_K tensor of an open GGUF (type 12, shape [K, N]). */
+hq_status hq_gguf_convert_q4_k(const hq_gguf* g, const char* name, uint32_t* codes_linear,
+                               uint16_t* scales, float* bias, uint32_t* K, uint32_t* N);
 
 /* ---- forward: replaces MarlinGemmEngine::forward_marlin_int4 (marlin_gemm.hpp:100-107,
  *      marlin_gemm.cu:556-601) ----

@@ -38,6 +38,24 @@ hq_status ok() {
   return HQ_OK;
 }
 
+}  // namespace
+
+hq_status hq_set_error(hq_status s, const char* fmt, ...) {
+  if (s == HQ_OK) {
+    g_last_error.clear();
+    return s;
+  }
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return s;
+}
+
+namespace {
+
 hq_status from_hip(hipError_t e, const char* what) {
   if (e == hipSuccess) return ok();
   return fail(HQ_ERR_DEVICE, "%s: %s", what, hipGetErrorString(e));
@@ -454,6 +472,9 @@ const char* hq_status_string(hq_status s) {
     case HQ_ERR_BAD_CODE: return "invalid ternary code";
     case HQ_ERR_DEVICE: return "device error";
     case HQ_ERR_INTERNAL: return "internal error";
+    case HQ_ERR_FORMAT: return "malformed or unsupported GGUF data";
+    case HQ_ERR_NOT_FOUND: return "not found";
+    case HQ_ERR_IO: return "file error";
   }
   return "unknown status";
 }

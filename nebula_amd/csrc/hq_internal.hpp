@@ -5,6 +5,9 @@
 
 #include "hq_qgemm.h"
 
+// Sets the calling thread's hq_last_error message (cleared for HQ_OK) and returns s.
+hq_status hq_set_error(hq_status s, const char* fmt, ...);
+
 namespace hq {
 
 // One projection inside a (possibly fused) launch. blk_begin is the first workgroup

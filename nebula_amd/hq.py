@@ -25,6 +25,9 @@ HQ_ERR_WORKSPACE = 5
 HQ_ERR_BAD_CODE = 6
 HQ_ERR_DEVICE = 7
 HQ_ERR_INTERNAL = 8
+HQ_ERR_FORMAT = 9
+HQ_ERR_NOT_FOUND = 10
+HQ_ERR_IO = 11
 
 DTYPE_F16 = 1
 DTYPE_BF16 = 2
@@ -39,7 +42,9 @@ EXPORTS = (
     "hq_workspace_bytes", "hq_workspace_bytes_fused", "hq_describe_gemm", "hq_device_status", "hq_repack_int4_ref", "hq_repack_int4", "hq_repack_ternary2",
     "hq_unpack_int4", "hq_unpack_ternary2", "hq_repack_int4_device", "hq_repack_ternary2_device",
     "hq_gemm_w4a16", "hq_gemm_w2a16", "hq_gemm_fused", "hq_gemm_fused_noalloc", "hq_tq1_0_bytes", "hq_convert_tq1_0",
-    "hq_repack_tq1_0_device",
+    "hq_repack_tq1_0_device", "hq_gguf_open", "hq_gguf_parse", "hq_gguf_close", "hq_gguf_header",
+    "hq_gguf_tensor_at", "hq_gguf_find_tensor", "hq_gguf_get_int", "hq_gguf_get_float", "hq_gguf_get_string",
+    "hq_gguf_get_array", "hq_gguf_load_tq1_0", "hq_convert_q4_k", "hq_gguf_convert_q4_k",
 )
 
 

@@ -319,3 +319,39 @@ void hqo_gemv_tq1_0(const float* X, const uint8_t* W, float* Y, uint32_t M, uint
         }
     }
 }
+
+/* ---- GGML Q4_K (the published block_q4_K of GGML / llama.cpp) ---- */
+static void q4k_scale_min(uint32_t j, const uint8_t* q, uint32_t* d, uint32_t* m) {
+    if (j < 4) {
+        *d = q[j] & 63u;
+        *m = q[j + 4] & 63u;
+    } else {
+        *d = (q[j + 4] & 0xFu) | ((uint32_t)(q[j - 4] >> 6) << 4);
+        *m = (q[j + 4] >> 4) | ((uint32_t)(q[j - 0] >> 6) << 4);
+    }
+}
+
+void hqo_dequant_q4_k(const uint8_t* blocks, uint32_t K, uint32_t N, float* w) {
+    const uint32_t nb = K / 256;
+#pragma omp parallel for schedule(static)
+    for (long long n = 0; n < (long long)N; ++n) {
+        for (uint32_t b = 0; b < nb; ++b) {
+            const uint8_t* x = blocks + ((size_t)n * nb + b) * 144;
+            const float d = hqo_f16_to_f32((uint16_t)(x[0] | (x[1] << 8)));
+            const float min = hqo_f16_to_f32((uint16_t)(x[2] | (x[3] << 8)));
+            const uint8_t* sc = x + 4;
+            const uint8_t* q = x + 16;
+            uint32_t k = 256 * b;
+            for (uint32_t j = 0; j < 256; j += 64) {
+                uint32_t s1, m1, s2, m2;
+                q4k_scale_min(j / 32, sc, &s1, &m1);
+                q4k_scale_min(j / 32 + 1, sc, &s2, &m2);
+                const float d1 = d * (float)s1, mm1 = min * (float)m1;
+                const float d2 = d * (float)s2, mm2 = min * (float)m2;
+                for (uint32_t l = 0; l < 32; ++l) w[(size_t)(k++) * N + n] = d1 * (float)(q[l] & 0xF) - mm1;
+                for (uint32_t l = 0; l < 32; ++l) w[(size_t)(k++) * N + n] = d2 * (float)(q[l] >> 4) - mm2;
+                q += 32;
+            }
+        }
+    }
+}

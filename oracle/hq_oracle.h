@@ -18,6 +18,9 @@
  *   hqo_fidelity          hydrogen/src/model/marlin_gemm.cu:619-644 (max |d|, MSE in fp64)
  *   hqo_tq1_0_code        hydrogen/src/model/native_decoder.cu:31-36, 87-101 (base-3 trits of a TQ1_0 block)
  *   hqo_gemv_tq1_0        hydrogen/src/model/native_decoder.cu:155-206 (kernel_gemv_tq1_0, any M)
+ *   hqo_dequant_q4_k      GGML's published Q4_K block (dequantize_row_q4_K of GGML / llama.cpp); the
+ *                         reference names the type (hydrogen/include/gguf_parser.hpp:44, 130) but has
+ *                         no decoder for it, so this one is pinned by the published layout only
  *
  * The generator (hqo_rng_*, hqo_gen_*) is this build's own specification, not
  * the reference's: the reference seeds std::mt19937 with implementation-defined
@@ -107,6 +110,15 @@ uint16_t hqo_tq1_0_scale(const uint8_t* block);
  * in a tree; results agree within fp32 reassociation). */
 void hqo_gemv_tq1_0(const float* X, const uint8_t* W, float* Y, uint32_t M, uint32_t K, uint32_t N,
                     int threads);
+
+/* ---- GGML Q4_K: 144 bytes per 256 weights: fp16 d, fp16 dmin, 12 bytes of 6-bit sub-block
+ *      scales and mins, 128 bytes of 4-bit codes ---- */
+/* W holds N rows of K/256 blocks. Sub-block j of a block (weights 32 j .. 32 j + 31) has scale
+ * sc_j and min m_j: for j < 4, sc = s[j] & 63, m = s[j + 4] & 63; else sc = (s[j + 4] & 15) |
+ * ((s[j - 4] >> 6) << 4), m = (s[j + 4] >> 4) | ((s[j] >> 6) << 4). Weight 64 c + l (l < 32) has
+ * code q[32 c + l] & 15, weight 64 c + 32 + l the high nibble; w = (d * sc) * q - dmin * m in fp32
+ * (separate roundings). Output fp32 Wdq[k*N + n]. */
+void hqo_dequant_q4_k(const uint8_t* blocks, uint32_t K, uint32_t N, float* wdq);
 
 #ifdef __cplusplus
 }

@@ -60,6 +60,7 @@ def lib() -> ctypes.CDLL:
     L.hqo_tq1_0_scale.restype = u16
     L.hqo_tq1_0_scale.argtypes = [vp]
     L.hqo_gemv_tq1_0.argtypes = [vp, vp, vp, u32, u32, u32, i32]
+    L.hqo_dequant_q4_k.argtypes = [vp, u32, u32, vp]
     _lib = L
     return L
 
@@ -271,3 +272,15 @@ def elementwise_error(y: np.ndarray, r: np.ndarray, floor_frac: float = 1e-2) ->
     m = np.abs(r) >= floor
     rel = np.abs(y[m] - r[m]) / np.abs(r[m]) if m.any() else np.zeros(1)
     return float(rel.max()), int((~m).sum())
+
+
+Q4_K_BLOCK_BYTES = 144
+
+
+def dequant_q4_k(blocks: np.ndarray, K: int, N: int) -> np.ndarray:
+    """GGML Q4_K blocks (N rows of K/256 blocks) -> fp32 Wdq [K, N] (the published dequantisation)."""
+    b = np.ascontiguousarray(blocks, dtype=np.uint8)
+    assert b.size == N * (K // 256) * Q4_K_BLOCK_BYTES
+    out = np.empty((K, N), dtype=np.float32)
+    lib().hqo_dequant_q4_k(_p(b), K, N, _p(out))
+    return out
