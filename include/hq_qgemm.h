@@ -34,7 +34,15 @@ extern "C" {
 
 #define HQ_ABI_VERSION 2
 
-typedef enum hq_status {
+/* The enums are int-sized. C++ gives them int as their underlying type, so that any value a C
+ * caller passes (including invalid ones, which are rejected) is a valid enum value there. */
+#ifdef __cplusplus
+#define HQ_ENUM(name) enum name : int
+#else
+#define HQ_ENUM(name) enum name
+#endif
+
+typedef HQ_ENUM(hq_status) {
     HQ_OK = 0,
     HQ_ERR_INVALID_ARG = 1,  /* null pointer, bad enum */
     HQ_ERR_SHAPE = 2,        /* M, K, N, group or leading dimensions not supported */
@@ -49,9 +57,9 @@ typedef enum hq_status {
     HQ_ERR_IO = 11           /* a file could not be opened or mapped */
 } hq_status;
 
-typedef enum hq_dtype { HQ_DTYPE_F16 = 1, HQ_DTYPE_BF16 = 2 } hq_dtype;
+typedef HQ_ENUM(hq_dtype) { HQ_DTYPE_F16 = 1, HQ_DTYPE_BF16 = 2 } hq_dtype;
 
-typedef enum hq_format {
+typedef HQ_ENUM(hq_format) {
     HQ_FORMAT_INT4 = 1,      /* u32 [K/8][N], nibble i of word (kw, n) is k = 8*kw + i, code q in
                                 0..15, weight (q - 8) * scale (marlin_gemm.cu:495-512) */
     HQ_FORMAT_TERNARY2 = 2   /* u32 [K/16][N], bits 2i..2i+1 of word (kw, n) hold c = t + 1 for
