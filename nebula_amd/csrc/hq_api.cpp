@@ -155,6 +155,24 @@ bool use_lockstep(int fmt, const hq::GemmDesc& d) {
   return fmt == HQ_FORMAT_TERNARY2 && hq::choose_decode_ls(fmt, d).KG == 4;
 }
 
+// The X-resident kernel (hq_decode.hip) takes every call with at most 16 rows whose
+// activation rows fit in LDS, outside the general kernels. HQ_DECODE_KERNEL=2 forces it
+// where it fits, 0 or 1 keeps it off (tuning and tests).
+bool use_resident(int fmt, const hq::GemmDesc& d, hq::XrConfig* c) {
+  if (d.M > 16 || d.gen) return false;
+  const char* v = std::getenv("HQ_DECODE_KERNEL");
+  if (v && *v && std::atoi(v) != 2) return false;
+  *c = hq::choose_decode_xr(fmt, d);
+  return c->ok;
+}
+
+// Slabs of T tiles over the segments of d (the X-resident grid).
+uint32_t xr_slabs(const hq::GemmDesc& d, int T) {
+  uint32_t g = 0;
+  for (uint32_t i = 0; i < d.nseg; ++i) g += (d.seg[i].ntiles + T - 1) / T;
+  return g;
+}
+
 // Rows up to which the streaming (decode) kernels run; the MFMA tile kernel above. The
 // lockstep kernel takes up to 16 * kLsMaxRowTiles rows: a split-fuse step (16 decode
 // tokens and a 64-token prefill chunk) stays a weight stream. HQ_DECODE_MAX_M overrides
@@ -227,9 +245,10 @@ hq::GemmDesc make_desc(uint32_t M, uint32_t K, uint32_t group, const uint32_t* N
 }
 
 // What a call runs: the kernel family, its tiling and the workspace it needs.
-enum class Kind { kDecode, kLockstep, kPrefill };
+enum class Kind { kDecode, kLockstep, kPrefill, kResident };
 struct Plan {
   Kind kind;
+  hq::XrConfig xc{};
   hq::DecodeConfig c{};
   hq::LsConfig lc{};
   hq::PrefillConfig pc{};
@@ -243,6 +262,10 @@ Plan make_plan(int fmt, const hq::GemmDesc& d, size_t cap = SIZE_MAX) {
     p.kind = Kind::kPrefill;
     p.pc = hq::choose_prefill(fmt, d, cap);
     p.need = hq::prefill_workspace_bytes(d, p.pc);
+    return p;
+  }
+  if (use_resident(fmt, d, &p.xc)) {
+    p.kind = Kind::kResident;
     return p;
   }
   if (!use_lockstep(fmt, d)) {
@@ -347,6 +370,7 @@ hq_status launch_plan(int fmt, int dtype, const hq::GemmDesc& d, const Plan& p, 
     case Kind::kPrefill: return from_hip(hq::launch_prefill(fmt, dtype, p.pc, w, s), "prefill launch");
     case Kind::kLockstep:
       return from_hip(hq::launch_decode_ls(fmt, dtype, d, p.lc, w, fault, ls_spin(), s), "decode launch");
+    case Kind::kResident: return from_hip(hq::launch_decode_xr(fmt, dtype, d, p.xc, s), "decode launch");
     case Kind::kDecode: break;
   }
   return from_hip(hq::launch_decode(fmt, dtype, d, p.c, w, s), "decode launch");
@@ -430,7 +454,10 @@ int decode_ring(int T, int U) {
 
 std::string describe(int fmt, int dtype, const hq::GemmDesc& d, const Plan& p) {
   char b[512];
-  if (p.kind == Kind::kDecode) {
+  if (p.kind == Kind::kResident) {
+    std::snprintf(b, sizeof b, "hq_decode_xr_kernel<%s,%s,T=%d,U=%d> workgroups=%u x %d wavefronts lds=%u ws=0",
+                  fmt_name(fmt), dt_name(dtype), p.xc.T, p.xc.U, xr_slabs(d, p.xc.T), p.xc.WK, p.xc.lds);
+  } else if (p.kind == Kind::kDecode) {
     std::snprintf(b, sizeof b, "hq_decode_kernel<%s,%s,T=%d,U=%d> workgroups=%d x %d wavefronts%s%s ws=%zu",
                   fmt_name(fmt), dt_name(dtype), p.c.T, decode_ring(p.c.T, p.c.U), p.c.SK, p.c.WK,
                   p.c.G ? " variable-width slabs" : "", p.need ? " cut slabs (fix-up)" : "", p.need);

@@ -100,9 +100,8 @@ __global__ void __launch_bounds__(64 * max_wk(T)) hq_decode_kernel(const GemmDes
   uint32_t wvo[T];
 #pragma unroll
   for (int t = 0; t < T; ++t) wvo[t] = lane * kLaneBytes + (uint32_t)t * nkb * kBlockBytes;
-  // A operand: row c16 of X, k-slice g4 of each chunk; rows >= M read as zero (activation
-  // and scale loads past the wavefront's units re-read cached data and are discarded).
-  const __amdgpu_buffer_rsrc_t xr = make_rsrc(d.X, M * (uint32_t)d.ldx * 2u);
+  // A operand: row c16 of X, k-slice g4 of each chunk; rows >= M read as zero.
+  const uint32_t xbytes = M * (uint32_t)d.ldx * 2u;
   const uint32_t xo = c16 * (uint32_t)d.ldx * 2u + g4 * 16u;
 
   // Load-side iterator: piece lp, k-block lkb of this wavefront, with the buffer
@@ -161,6 +160,7 @@ __global__ void __launch_bounds__(64 * max_wk(T)) hq_decode_kernel(const GemmDes
       ++lp;
     }
     lw_num = 0;
+    ls_num = 0;
     lkb = 0;
   };
   auto advance_load = [&]() {
@@ -182,7 +182,9 @@ __global__ void __launch_bounds__(64 * max_wk(T)) hq_decode_kernel(const GemmDes
   auto load = [&](int slot) {
     const __amdgpu_buffer_rsrc_t lw = make_rsrc(lw_base, lw_num);
     const __amdgpu_buffer_rsrc_t ls = make_rsrc(ls_base, ls_num);
-    const __amdgpu_buffer_rsrc_t lx = xr;
+    // Past the wavefront's units every extent is zero: the ring's trailing loads return
+    // zeros without a memory access, so the final wait does not hang on cache round trips.
+    const __amdgpu_buffer_rsrc_t lx = make_rsrc(d.X, lw_num ? xbytes : 0u);
     const uint32_t kbo = __builtin_amdgcn_readfirstlane(lkb * kBlockBytes);
     const uint32_t so = __builtin_amdgcn_readfirstlane(plan_group_of_kb(lkb, pl.gmul) * lsrow);
 #pragma unroll
@@ -400,6 +402,213 @@ __global__ void __launch_bounds__(64 * max_wk(T)) hq_decode_kernel(const GemmDes
     for (uint32_t j = 0; j < kMaxIt; ++j) {
       const uint32_t o4 = threadIdx.x + j * nthr;
       if (o4 < SL4) store4(sg, col0, ncols, o4, v[j]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------
+// X-resident decode kernel: one workgroup per slab of T column tiles, its WK wavefronts
+// splitting the slab's k-blocks (k-block w, w + WK, ... for wavefront w). The activation
+// rows (M <= 16, all of K) are copied into LDS once, by LDS-DMA, before the weight stream
+// starts; afterwards every wavefront streams its weights through a register ring of U
+// steps (T tiles x one k-block each) with no barrier and no activation load in the ring,
+// and reads its A fragments from LDS. Measured on MI355X, a barrier-free register ring
+// streams at the rate of a plain copy, while activation loads from L2 inside the ring (one
+// wavefront fetching them per k-block) or a workgroup barrier per k-block cost 15-25% of
+// the stream. The partial sums of the wavefronts meet once, in LDS, summed in wavefront
+// order (deterministic), after the activation rows are no longer needed.
+//
+// LDS layout of the activation rows: 16-byte units, unit (r * nkb + kb) * 16 + (j ^ r)
+// holds elements 8 j .. 8 j + 7 of k-block kb of row r (j = 0..15). A fragment read of
+// chunk c (lane: row c16, slice g4, piece j = 4 c + g4) touches 16 distinct units mod 16
+// in every group of 16 lanes, i.e. every bank once. Lanes of rows >= M read row M - 1:
+// an MFMA output row depends only on its own A row, and rows >= M are never stored.
+struct XrPlan {
+  uint32_t nkb16_m;  // plan_div_magic(16 * nkb)
+  uint32_t gmul;     // plan_gmul(gkb)
+};
+
+constexpr int xr_max_wk(int T) { return T >= 8 ? 8 : 16; }
+
+template <int FMT, int DT, int T, int U, bool FUSED>
+__global__ void __launch_bounds__(64 * xr_max_wk(T)) hq_decode_xr_kernel(const GemmDesc d, const XrPlan pl) {
+  using W = typename WTraits<FMT>::V;
+  constexpr uint32_t WPL = WTraits<FMT>::wpl;
+  constexpr uint32_t kLaneBytes = WPL * 4u;
+  constexpr uint32_t kBlockBytes = 64u * kLaneBytes;  // one tile x one k-block
+  constexpr uint32_t kCols = 16u * T;
+  constexpr bool kInt4 = FMT == HQ_FORMAT_INT4;
+  constexpr int kSL = (T + 3) / 4;  // scale loads per step (one per four tiles)
+  extern __shared__ __attribute__((aligned(16))) char xs[];
+
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t WK = __builtin_amdgcn_readfirstlane(blockDim.x >> 6);
+  const uint32_t c16 = lane & 15u;
+  const uint32_t g4 = lane >> 4;
+  const uint32_t nkb = d.nkb;
+  const uint32_t M = d.M;
+  const uint32_t g = blockIdx.x;
+
+  uint32_t s = 0;
+  if constexpr (FUSED) {
+    for (uint32_t i = 1; i < d.nseg; ++i)
+      if (g >= d.seg[i].blk_begin) s = i;
+    s = __builtin_amdgcn_readfirstlane(s);
+  }
+  const SegDesc& sg = d.seg[s];
+  const uint32_t lsl = g - sg.blk_begin;
+  const uint32_t ct0 = lsl * sg.slab_w + min(lsl, sg.slab_r);
+  const uint32_t nv = sg.slab_w + (lsl < sg.slab_r ? 1u : 0u);
+  const uint32_t N = sg.N;
+
+  // 1. Activation rows -> LDS: 64 units per LDS-DMA instruction, instruction q by
+  //    wavefront q mod WK; lane i of instruction q fetches the element piece of unit 64 q + i.
+  {
+    const uint32_t ldx2 = (uint32_t)d.ldx * 2u;
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(d.X, M * ldx2);
+    const uint32_t nkb16 = nkb * 16u;
+    const uint32_t nq = (M * nkb16 + 63u) / 64u;
+    for (uint32_t q = wave; q < nq; q += WK) {
+      const uint32_t u = q * 64u + lane;
+      const uint32_t r = plan_div(u, nkb16, pl.nkb16_m);
+      const uint32_t rem = u - r * nkb16;
+      const uint32_t voff = r < M ? r * ldx2 + (rem >> 4) * 256u + (((rem & 15u) ^ (r & 15u)) * 16u) : kOutOfRange;
+      buffer_to_lds16(xr, xs + q * 1024u, voff);
+    }
+  }
+  // The ring's first loads must be issued after the copies (vmcnt retires in order).
+  __builtin_amdgcn_sched_barrier(0);
+
+  // 2. Weight ring: step j of this wavefront is k-block kb = wave + j * WK, T tiles.
+  const uint32_t nj = wave < nkb ? (nkb - wave + WK - 1u) / WK : 0u;
+  const __amdgpu_buffer_rsrc_t wrs =
+      make_rsrc(sg.Wp + (size_t)ct0 * nkb * 64u * WPL, __builtin_amdgcn_readfirstlane(nv * nkb * kBlockBytes));
+  const __amdgpu_buffer_rsrc_t srs = make_rsrc(sg.S, __builtin_amdgcn_readfirstlane(((nkb / d.gkb - 1u) * sg.lds + N) * 2u));
+  const uint32_t lsrow = sg.lds * 2u;
+  uint32_t wvo[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) wvo[t] = lane * kLaneBytes + (uint32_t)t * nkb * kBlockBytes;
+  uint32_t svo[kSL];
+#pragma unroll
+  for (int jj = 0; jj < kSL; ++jj) svo[jj] = min(ct0 * 16u + 64u * jj + lane % kCols, N - 1u) * 2u;
+
+  W wr[U][T];
+  uint32_t sr[U][kSL];
+  auto load = [&](int slot, uint32_t j) {
+    const bool live = j < nj;
+    const uint32_t kb = wave + j * WK;
+    const uint32_t kbo = __builtin_amdgcn_readfirstlane(live ? kb * kBlockBytes : 0u);
+    const uint32_t so = __builtin_amdgcn_readfirstlane(live ? plan_group_of_kb(kb, pl.gmul) * lsrow : 0u);
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      if constexpr (WPL == 4) wr[slot][t] = __builtin_amdgcn_raw_buffer_load_b128(wrs, live ? wvo[t] : kOutOfRange, kbo, kStreamAux);
+      else wr[slot][t] = __builtin_amdgcn_raw_buffer_load_b64(wrs, live ? wvo[t] : kOutOfRange, kbo, kStreamAux);
+    }
+#pragma unroll
+    for (int jj = 0; jj < kSL; ++jj) sr[slot][jj] = __builtin_amdgcn_raw_buffer_load_b16(srs, live ? svo[jj] : kOutOfRange, so, 0);
+  };
+#pragma unroll
+  for (int u = 0; u < U; ++u) load(u, (uint32_t)u);
+  __builtin_amdgcn_sched_barrier(0);
+
+  // Wait for this wavefront's activation copies only: the ring's U * (T + kSL) loads were
+  // issued after them and stay in flight. Then publish the rows to the workgroup.
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(U * (T + kSL)));
+  __syncthreads();
+
+  // A fragment addresses: a[c] = xa[c] + kb * 256.
+  uint32_t xa[4];
+  const uint32_t xrow = min(c16, M - 1u);
+#pragma unroll
+  for (int c = 0; c < 4; ++c) xa[c] = (xrow * nkb * 16u + (((4u * c + g4) ^ xrow))) * 16u;
+
+  const DqBiasConst dqb = DT == HQ_DTYPE_F16 ? dq_bias_const_f16() : dq_bias_const_bf16();
+  const u4 corr_b = int4_corr_fragment<DT>();
+  f4 acc[T];
+#pragma unroll
+  for (int t = 0; t < T; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
+
+  auto compute = [&](int u, uint32_t j) {
+    const uint32_t kb = wave + j * WK;
+    u4 a[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) a[c] = *reinterpret_cast<const u4*>(xs + xa[c] + kb * 256u);
+    uint32_t sbits[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+      sbits[t] = T == 1 ? sr[u][0]
+                        : (uint32_t)__builtin_amdgcn_ds_bpermute((int)((16u * (t % 4) + c16) * 4u), (int)sr[u][t / 4]);
+    f4 seed = f4{0.f, 0.f, 0.f, 0.f};
+    if constexpr (kInt4) {
+#pragma unroll
+      for (int c = 0; c < 4; ++c) seed = mfma16x16x32<DT>(a[c], corr_b, seed);
+    }
+    f4 gs[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) gs[t] = seed;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        u4 bf;
+        if constexpr (kInt4) {
+          bf = dq_int4_biased<DT>(wr[u][t][c], dqb);
+        } else {
+          const uint32_t word = wr[u][t][c >> 1];
+          bf = (c & 1) ? dq_tern2<1>(word) : dq_tern2<0>(word);
+        }
+        gs[t] = mfma16x16x32<DT>(a[c], bf, gs[t]);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+      float sc = f16_to_f32((uint16_t)sbits[t]);
+      if constexpr (!kInt4) sc = __builtin_isfinite(sc) ? 0.5f * sc : 0.0f;  // fields hold 2t; non-finite drops
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[t][v] = __builtin_fmaf(gs[t][v], sc, acc[t][v]);
+    }
+  };
+
+  for (uint32_t j = 0; j < nj; j += U) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (j + u < nj) compute(u, j + u);  // uniform; no loads inside, so waitcnt stays exact across it
+      load(u, j + u + U);
+    }
+  }
+  // Loads past this wavefront's k-blocks read nothing; retire them before the registers
+  // and the LDS are reused.
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+
+  // 3. Reduction: park each wavefront's sums (rows < M) over the activation rows, then
+  //    sum them in wavefront order, four consecutive columns per thread.
+  __syncthreads();
+  const uint32_t SL = M * kCols;
+  float* red = reinterpret_cast<float*>(xs);
+#pragma unroll
+  for (int t = 0; t < T; ++t)
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const uint32_t row = 4u * g4 + v;
+      if (row < M) red[wave * SL + row * kCols + t * 16u + c16] = acc[t][v];
+    }
+  __syncthreads();
+  const uint32_t col0 = ct0 * 16u, ncols = nv * 16u;
+  for (uint32_t o4 = threadIdx.x; o4 < SL / 4u; o4 += WK * 64u) {
+    f4 v = f4{0.f, 0.f, 0.f, 0.f};
+    for (uint32_t w = 0; w < WK; ++w) v += *reinterpret_cast<const f4*>(red + w * SL + 4u * o4);
+    const uint32_t o = 4u * o4, row = o / kCols, lc = o % kCols, n = col0 + lc;
+    if (lc >= ncols) continue;
+    uint16_t* y = reinterpret_cast<uint16_t*>(sg.Y) + (size_t)row * sg.ldy + n;
+    if (n + 3u < N && (reinterpret_cast<uintptr_t>(y) & 7u) == 0) {
+      const u2 packed = {(uint32_t)f32_to_out<DT>(v[0]) | ((uint32_t)f32_to_out<DT>(v[1]) << 16),
+                         (uint32_t)f32_to_out<DT>(v[2]) | ((uint32_t)f32_to_out<DT>(v[3]) << 16)};
+      *reinterpret_cast<u2*>(y) = packed;
+    } else {
+#pragma unroll
+      for (uint32_t e = 0; e < 4u; ++e)
+        if (n + e < N) y[e] = f32_to_out<DT>(v[e]);
     }
   }
 }
@@ -624,6 +833,157 @@ hipError_t launch_decode(int fmt, int dtype, GemmDesc d, const DecodeConfig& c, 
   }
   return dtype == HQ_DTYPE_F16 ? launch_fd<HQ_FORMAT_TERNARY2, HQ_DTYPE_F16>(d, c, ws, stream)
                                : launch_fd<HQ_FORMAT_TERNARY2, HQ_DTYPE_BF16>(d, c, ws, stream);
+}
+
+}  // namespace hq
+
+namespace hq {
+namespace {
+
+// Padded activation area (whole LDS-DMA instructions) of an X-resident workgroup.
+uint32_t xr_x_bytes(const GemmDesc& d) { return (d.M * d.nkb * 16u + 63u) / 64u * 1024u; }
+
+uint32_t xr_lds_bytes(const GemmDesc& d, int T, int WK) {
+  const uint32_t x = xr_x_bytes(d);
+  const uint32_t red = (uint32_t)WK * d.M * 16u * (uint32_t)T * 4u;
+  return std::max(x, red);
+}
+
+template <int FMT, int DT, int T, int U>
+hipError_t xr_launch_t(GemmDesc d, const XrConfig& c, hipStream_t stream) {
+  if (c.WK < 1 || c.WK > xr_max_wk(T) || d.M > 16u) return hipErrorInvalidValue;
+  const uint32_t G = assign_slabs(d, T, 0);
+  XrPlan pl{};
+  pl.nkb16_m = plan_div_magic(16u * d.nkb);
+  pl.gmul = plan_gmul(d.gkb);
+  // Byte offsets into X, a slab's weights and Y are 32-bit buffer or LDS offsets.
+  bool fits = G >= 1 && (uint64_t)d.M * (uint64_t)d.ldx * 2u < (1ull << 31) && c.lds <= kXrLdsMax &&
+              c.lds >= xr_lds_bytes(d, T, c.WK);
+  for (uint32_t i = 0; i < d.nseg; ++i)
+    fits = fits && (uint64_t)(d.seg[i].slab_w + 1u) * d.nkb * 64u * WTraits<FMT>::wpl * 4u < (1ull << 31);
+  if (!fits) return hipErrorInvalidValue;
+  static const hipError_t attr =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&hq_decode_xr_kernel<FMT, DT, T, U, false>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)kXrLdsMax) != hipSuccess
+          ? hipErrorInvalidConfiguration
+          : hipFuncSetAttribute(reinterpret_cast<const void*>(&hq_decode_xr_kernel<FMT, DT, T, U, true>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)kXrLdsMax);
+  if (attr != hipSuccess) return attr;
+  if (d.nseg > 1)
+    hipLaunchKernelGGL((hq_decode_xr_kernel<FMT, DT, T, U, true>), dim3(G), dim3(64 * c.WK), c.lds, stream, d, pl);
+  else
+    hipLaunchKernelGGL((hq_decode_xr_kernel<FMT, DT, T, U, false>), dim3(G), dim3(64 * c.WK), c.lds, stream, d, pl);
+  return hipGetLastError();
+}
+
+template <int FMT, int DT>
+hipError_t xr_launch_fd(const GemmDesc& d, const XrConfig& c, hipStream_t stream) {
+  switch (c.T * 10 + c.U) {
+    case 82: return xr_launch_t<FMT, DT, 8, 2>(d, c, stream);
+    case 42: return xr_launch_t<FMT, DT, 4, 2>(d, c, stream);
+    case 43: return xr_launch_t<FMT, DT, 4, 3>(d, c, stream);
+    case 23: return xr_launch_t<FMT, DT, 2, 3>(d, c, stream);
+    case 24: return xr_launch_t<FMT, DT, 2, 4>(d, c, stream);
+    case 14: return xr_launch_t<FMT, DT, 1, 4>(d, c, stream);
+    case 16: return xr_launch_t<FMT, DT, 1, 6>(d, c, stream);
+    default: return hipErrorInvalidConfiguration;
+  }
+}
+
+}  // namespace
+
+// Wavefronts per SIMD the register use of hq_decode_xr_kernel<fmt, T, U> allows (runtime
+// occupancy query, cached per device; 4 when there is no device to ask).
+static int xr_waves_per_simd(int fmt, int T, int U) {
+  const void* f = nullptr;
+  const int key = T * 10 + U;
+  if (fmt == HQ_FORMAT_INT4) {
+    switch (key) {
+      case 82: f = reinterpret_cast<const void*>(&hq_decode_xr_kernel<HQ_FORMAT_INT4, HQ_DTYPE_F16, 8, 2, false>); break;
+      case 42: f = reinterpret_cast<const void*>(&hq_decode_xr_kernel<HQ_FORMAT_INT4, HQ_DTYPE_F16, 4, 2, false>); break;
+      case 23: f = reinterpret_cast<const void*>(&hq_decode_xr_kernel<HQ_FORMAT_INT4, HQ_DTYPE_F16, 2, 3, false>); break;
+      default: return 4;
+    }
+  } else {
+    switch (key) {
+      case 82: f = reinterpret_cast<const void*>(&hq_decode_xr_kernel<HQ_FORMAT_TERNARY2, HQ_DTYPE_F16, 8, 2, false>); break;
+      case 42: f = reinterpret_cast<const void*>(&hq_decode_xr_kernel<HQ_FORMAT_TERNARY2, HQ_DTYPE_F16, 4, 2, false>); break;
+      case 23: f = reinterpret_cast<const void*>(&hq_decode_xr_kernel<HQ_FORMAT_TERNARY2, HQ_DTYPE_F16, 2, 3, false>); break;
+      default: return 4;
+    }
+  }
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 4;
+  static std::mutex mu;
+  static int cached[64][2][9][5] = {};
+  std::lock_guard<std::mutex> lock(mu);
+  int& c = cached[dev][fmt == HQ_FORMAT_INT4 ? 0 : 1][T][U];
+  if (c == 0) {
+    int n = 0;  // workgroups of four wavefronts (one per SIMD) per CU, no LDS
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, f, 256, 0) != hipSuccess || n <= 0) n = 4;
+    c = std::min(n, 8);
+  }
+  return c;
+}
+
+// Tiling of the X-resident kernel. A workgroup places ceil(WK / 4) wavefronts on each SIMD,
+// so it fits on a CU as often as the register use and the LDS both allow; the planner takes
+// the narrowest slabs (T = 2, 4 or 8 tiles, the most workgroups) whose grid fits on the CUs in
+// one round, eight wavefronts per workgroup (four with 8-tile slabs), two steps in flight
+// (three with 2-tile slabs). Measured on MI355X against the per-wavefront and lockstep
+// kernels (graph-timed, weights rotated past the 256 MiB cache): 5120 x 5120 at M = 1..16
+// 5.7-7.1 us against 7.5-8.4, 27648 x 5120 at M = 1, 2 15.3-15.6 against 16.8-17.3, ternary
+// 5120 x 27648 at M = 1 11.5 against 14.1; with wide weights (more tiles than two per CU)
+// and more than four rows the lockstep kernel, which shares each activation k-block through
+// LDS instead of copying all of K per workgroup, is as fast or faster, so the planner leaves
+// those calls to it. HQ_XR_T / _WK / _U override (tuning and tests).
+XrConfig choose_decode_xr(int fmt, const GemmDesc& d) {
+  XrConfig c{2, 3, 8, 0, false};
+  if (d.M > 16u || d.gen) return c;
+  const uint32_t cus = (uint32_t)cu_count();
+  const uint32_t xb = xr_x_bytes(d);
+  if (xb > kXrLdsMax) return c;
+  uint32_t tiles = 0;
+  for (uint32_t i = 0; i < d.nseg; ++i) tiles += d.seg[i].ntiles;
+  const int eT = env_int("HQ_XR_T", 0), eWK = env_int("HQ_XR_WK", 0), eU = env_int("HQ_XR_U", 0);
+  const bool forced = eT || eWK || eU;
+  bool found = false;
+  for (int t : {2, 4, 8}) {
+    const int wk = t == 8 ? 4 : 8, u = t == 2 ? 3 : 2;
+    const uint32_t lds = xr_lds_bytes(d, t, wk);
+    if (lds > kXrLdsMax) continue;
+    const uint32_t by_regs = (uint32_t)(xr_waves_per_simd(fmt, t, u) / ((wk + 3) / 4));
+    const uint32_t per_cu = std::min(by_regs, kXrLdsMax / lds);
+    if (per_cu >= 1 && total_slabs(d, t) <= cus * per_cu) {
+      c.T = t;
+      c.WK = wk;
+      c.U = u;
+      found = true;
+      break;
+    }
+  }
+  if (!forced && (!found || (tiles > 2u * cus && d.M > 4u))) return c;
+  if (eT == 1 || eT == 2 || eT == 4 || eT == 8) c.T = eT;
+  if (eWK >= 1) c.WK = eWK;
+  if (eU >= 2) c.U = eU;
+  // Snap to an instantiated (T, U).
+  if (c.T == 8) c.U = 2;
+  if (c.T == 4) c.U = std::min(std::max(c.U, 2), 3);
+  if (c.T == 2) c.U = std::min(std::max(c.U, 3), 4);
+  if (c.T == 1) c.U = c.U >= 6 ? 6 : 4;
+  c.WK = std::max(1, std::min(c.WK, xr_max_wk(c.T)));
+  c.lds = xr_lds_bytes(d, c.T, c.WK);
+  c.ok = c.lds <= kXrLdsMax;
+  return c;
+}
+
+hipError_t launch_decode_xr(int fmt, int dtype, GemmDesc d, const XrConfig& c, hipStream_t stream) {
+  if (fmt == HQ_FORMAT_INT4) {
+    return dtype == HQ_DTYPE_F16 ? xr_launch_fd<HQ_FORMAT_INT4, HQ_DTYPE_F16>(d, c, stream)
+                                 : xr_launch_fd<HQ_FORMAT_INT4, HQ_DTYPE_BF16>(d, c, stream);
+  }
+  return dtype == HQ_DTYPE_F16 ? xr_launch_fd<HQ_FORMAT_TERNARY2, HQ_DTYPE_F16>(d, c, stream)
+                               : xr_launch_fd<HQ_FORMAT_TERNARY2, HQ_DTYPE_BF16>(d, c, stream);
 }
 
 }  // namespace hq

@@ -63,6 +63,20 @@ size_t decode_workspace_bytes(const GemmDesc& d, const DecodeConfig& c);
 // Decode (M <= 16): HBM-streaming MFMA kernel. Validated descriptor in, status out.
 hipError_t launch_decode(int fmt, int dtype, GemmDesc d, const DecodeConfig& c, void* ws, hipStream_t stream);
 
+// X-resident decode (M <= 16, activation rows of all K in LDS): one workgroup per slab of T
+// column tiles, WK wavefronts splitting its k-blocks, a register ring of U steps.
+struct XrConfig {
+  int T;
+  int U;
+  int WK;
+  uint32_t lds;  // dynamic LDS bytes per workgroup
+  bool ok;       // the rows fit in LDS and the kernel takes the call
+};
+// LDS one X-resident workgroup may use (the whole 160 KiB of a gfx950 CU).
+constexpr uint32_t kXrLdsMax = 160u * 1024u;
+XrConfig choose_decode_xr(int fmt, const GemmDesc& d);
+hipError_t launch_decode_xr(int fmt, int dtype, GemmDesc d, const XrConfig& c, hipStream_t stream);
+
 // Lockstep decode (M <= 80): KG k-groups of GW wavefronts per workgroup own a slab of up
 // to GW * T column tiles and walk one piece of its k-blocks together (S pieces per slab),
 // each k-group sharing its activation k-block (MT tiles of 16 rows) through LDS.

@@ -59,12 +59,15 @@ def workspace_bytes_fused(fmt, M, K, Ns, group=128, bias=0):
 
 
 def test_workspace_bytes():
-    # Large decode shapes with few column tiles cut their slabs along K and need a fix-up
-    # workspace: a fixed counter area plus fp32 partial tiles that scale with M.
+    # Large decode shapes with few column tiles whose activation rows do not fit in LDS
+    # cut their slabs along K and need a fix-up workspace: a fixed counter area plus fp32
+    # partial tiles that scale with M. With the rows in LDS (M <= 2 at K = 27648) the
+    # X-resident kernel needs none.
     st, b16 = workspace_bytes_fused(hq.FORMAT_INT4, 16, 27648, [5120])
-    st1, b1 = workspace_bytes_fused(hq.FORMAT_INT4, 1, 27648, [5120])
-    assert st == st1 == hq.HQ_OK
-    assert b16 > b1 > 0 and b16 % 256 == 0 and b1 % 256 == 0
+    st4, b4 = workspace_bytes_fused(hq.FORMAT_INT4, 4, 27648, [5120])
+    assert st == st4 == hq.HQ_OK
+    assert b16 > b4 > 0 and b16 % 256 == 0 and b4 % 256 == 0
+    assert workspace_bytes_fused(hq.FORMAT_INT4, 1, 27648, [5120]) == (hq.HQ_OK, 0)
     # hq_workspace_bytes covers the call with and without a bias.
     for M in (1, 16):
         plain = workspace_bytes_fused(hq.FORMAT_INT4, M, 27648, [5120])[1]
@@ -112,16 +115,18 @@ def test_workspace_bytes_fused_is_what_the_call_asks_for():
             hq.HQ_ERR_WORKSPACE, (fmt, M, K, Ns)
         assert L.hq_gemm_fused(0x1000, 1, K, fmt, segs, len(Ns), M, K, 128, 0x10010, need, None) == \
             hq.HQ_ERR_ALIGNMENT, (fmt, M, K, Ns)
-    # The case the single-shape rule under-sized: eight 16-column int4 segments at M = 8.
-    need8 = workspace_bytes_fused(hq.FORMAT_INT4, 8, 1024, [16] * 8)[1]
-    assert need8 >= workspace_bytes(hq.FORMAT_INT4, 8, 1024, 16 * 8)[1]
+    # The case the single-shape rule under-sized: eight 16-column int4 segments at M = 8
+    # (with a bias: the lockstep kernel, which cuts slabs along K).
+    need8 = workspace_bytes_fused(hq.FORMAT_INT4, 8, 1024, [16] * 8, bias=1)[1]
+    assert need8 >= workspace_bytes_fused(hq.FORMAT_INT4, 8, 1024, [16 * 8], bias=1)[1] > 0
     assert workspace_bytes_fused(hq.FORMAT_INT4, 8, 1024, [])[0] == hq.HQ_ERR_INVALID_ARG
     assert workspace_bytes_fused(hq.FORMAT_INT4, 8, 1024, [0])[0] == hq.HQ_ERR_SHAPE
     assert workspace_bytes_fused(hq.FORMAT_TERNARY2, 8, 1024, [64], bias=1)[0] == hq.HQ_ERR_UNSUPPORTED
 
 
 def test_describe_gemm_names_the_kernel_families():
-    assert hq.describe(hq.FORMAT_INT4, hq.DTYPE_F16, 1, 27648, 5120).startswith("hq_decode_kernel<int4,f16,")
+    assert hq.describe(hq.FORMAT_INT4, hq.DTYPE_F16, 1, 27648, 5120).startswith("hq_decode_xr_kernel<int4,f16,")
+    assert hq.describe(hq.FORMAT_INT4, hq.DTYPE_F16, 4, 27648, 5120).startswith("hq_decode_kernel<int4,f16,")
     assert hq.describe(hq.FORMAT_INT4, hq.DTYPE_F16, 16, 5120, 27648).startswith("hq_decode_ls_kernel<int4,f16,")
     assert hq.describe(hq.FORMAT_TERNARY2, hq.DTYPE_BF16, 2048, 5120, 27648).startswith(
         "hq_prefill_kernel<ternary2,bf16")

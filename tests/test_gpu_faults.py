@@ -17,9 +17,10 @@ pytestmark = pytest.mark.gpu
 
 
 def test_kgroup_barrier_timeout_is_reported(cuda):
-    P = O.Problem(O.INT4, 8, 2048, 1024, 128, O.F16, seed=9100)
+    # 20 rows: only the lockstep kernel takes them, with two k-groups (the barrier is used).
+    P = O.Problem(O.INT4, 20, 2048, 1024, 128, O.F16, seed=9100)
     D = DeviceProblem(P)
-    assert "KG=2" in hq.describe(O.INT4, O.F16, 8, 2048, 1024)  # two k-groups: the barrier is used
+    assert "KG=2" in hq.describe(O.INT4, O.F16, 20, 2048, 1024)
     D.run()
     hq.device_status()  # no fault so far
     os.environ["HQ_DECODE_LS_SPIN"] = "0"

@@ -457,6 +457,90 @@ def test_lockstep_matches_per_wavefront(cuda, M):
     check(y1, P.reference(threads=16), O.F16, f"lockstep M={M}")
 
 
+# ---------------------------------------------------------------- X-resident decode kernel
+class xr_env(decode_env):
+    """Force the X-resident decode kernel (activation rows in LDS) and its tiling for a block:
+    slab width T, wavefronts WK (splitting the slab's k-blocks), ring depth U."""
+
+    def __init__(self, **kv):
+        self.kv = {f"HQ_XR_{k}": str(v) for k, v in kv.items()}
+        self.kv["HQ_DECODE_KERNEL"] = "2"
+
+
+# (T, WK, U): every instantiated (slab width, ring depth); one wavefront, wavefront counts that
+# do not divide the 16 k-blocks, and 16 wavefronts of one k-block each.
+XR_CFGS = [(1, 1, 4), (1, 3, 6), (1, 16, 4), (2, 4, 3), (2, 7, 4), (2, 16, 3), (4, 5, 2), (4, 8, 3), (8, 4, 2),
+           (8, 8, 2)]
+
+
+@pytest.mark.parametrize("T,WK,U", XR_CFGS)
+@pytest.mark.parametrize("M", [1, 6, 16])
+def test_xr_configs_int4(cuda, T, WK, U, M):
+    # K = 2048 (16 k-blocks), N = 1000 (63 tiles: the last slab is partial for every width).
+    P = O.Problem(O.INT4, M, 2048, 1000, 128, O.F16, seed=3400 + M)
+    D = DeviceProblem(P)
+    with xr_env(T=T, WK=WK, U=U):
+        assert hq.describe(O.INT4, O.F16, M, 2048, 1000).startswith(f"hq_decode_xr_kernel<int4,f16,T={T},U={U}>")
+        y = D.run()
+        y2 = D.run()
+    assert torch_equal(y, y2)  # fixed summation order: bit-identical from run to run
+    check(y, P.reference(), O.F16, f"xr T={T} WK={WK} U={U} M={M}", P)
+
+
+@pytest.mark.parametrize("fmt,xdt", [(O.INT4, O.BF16), (O.TERNARY2, O.F16), (O.TERNARY2, O.BF16)])
+@pytest.mark.parametrize("T,WK,U", [(1, 8, 4), (2, 8, 3), (4, 4, 2), (8, 8, 2)])
+def test_xr_formats(cuda, fmt, xdt, T, WK, U):
+    # group 256: one scale row serves two k-blocks.
+    P = O.Problem(fmt, 9, 1536, 700, 256, xdt, seed=3450)
+    D = DeviceProblem(P)
+    with xr_env(T=T, WK=WK, U=U):
+        assert "hq_decode_xr_kernel" in hq.describe(fmt, xdt, 9, 1536, 700, group=256)
+        y = D.run()
+    check(y, P.reference(), xdt, f"xr fmt={fmt} T={T} WK={WK} U={U}", P)
+
+
+@pytest.mark.parametrize("T", [2, 8])
+def test_xr_fused(cuda, T):
+    # Slabs never straddle segments; each segment's last slab is partial.
+    Ns, K, M = [600, 130, 1000], 1024, 5
+    probs = [O.Problem(O.INT4, M, K, n, 128, O.F16, seed=3500 + i) for i, n in enumerate(Ns)]
+    for p in probs[1:]:
+        p.X = probs[0].X
+    devs = [DeviceProblem(p) for p in probs]
+    with xr_env(T=T, WK=4):
+        outs = hq.gemm_fused(O.INT4, devs[0].X, [(d.Wp, d.S, d.P.N) for d in devs])
+    for d, y in zip(devs, outs):
+        check(y, d.P.reference(), O.F16, f"xr fused T={T} N={d.P.N}", d.P)
+
+
+@pytest.mark.parametrize("M,K", [(16, 5120), (8, 5120), (3, 5120), (2, 27648), (1, 27648)])
+def test_xr_lds_limits(cuda, M, K):
+    # Default plans whose activation rows fill the LDS (16 x 5120 halves = 160 KiB), half of
+    # it, or hold the longest K (27648) for one and two rows.
+    N = 1000
+    desc = hq.describe(O.INT4, O.F16, M, K, N)
+    assert desc.startswith("hq_decode_xr_kernel<int4,f16,") and f"lds={M * K * 2}" in desc, desc
+    P = O.Problem(O.INT4, M, K, N, 128, O.F16, seed=3550 + M)
+    D = DeviceProblem(P)
+    check(D.run(), P.reference(threads=16), O.F16, f"xr lds M={M} K={K}", P)
+
+
+@pytest.mark.parametrize("M", [1, 4, 16])
+def test_xr_matches_other_decode_kernels(cuda, M):
+    # The three decode kernels compute the same values up to fp32 summation order.
+    P = O.Problem(O.INT4, M, 5120, 5120, 128, O.F16, seed=3600 + M)
+    D = DeviceProblem(P)
+    assert hq.describe(O.INT4, O.F16, M, 5120, 5120).startswith("hq_decode_xr_kernel")
+    y2 = D.run()
+    with decode_env(KERNEL=1):
+        y1 = D.run()
+    with decode_env(KERNEL=0):
+        y0 = D.run()
+    assert O.normwise_error(to_host_f32(y2), to_host_f32(y1)) <= OUT_TOL[O.F16]
+    assert O.normwise_error(to_host_f32(y2), to_host_f32(y0)) <= OUT_TOL[O.F16]
+    check(y2, P.reference(threads=16), O.F16, f"xr M={M}")
+
+
 class prefill_env(decode_env):
     """Force the prefill kernel (also for M <= 80, which the lockstep kernel takes by
     default) and its tiling for a block: WM (tile height 128 or 256 rows), SK=0 (no
