@@ -158,11 +158,11 @@ bool use_lockstep(int fmt, const hq::GemmDesc& d) {
 // The X-resident kernel (hq_decode.hip) takes every call with at most 16 rows whose
 // activation rows fit in LDS, outside the general kernels. HQ_DECODE_KERNEL=2 forces it
 // where it fits, 0 or 1 keeps it off (tuning and tests).
-bool use_resident(int fmt, const hq::GemmDesc& d, hq::XrConfig* c) {
+bool use_resident(int fmt, const hq::GemmDesc& d, size_t cap, hq::XrConfig* c) {
   if (d.M > 16 || d.gen) return false;
   const char* v = std::getenv("HQ_DECODE_KERNEL");
   if (v && *v && std::atoi(v) != 2) return false;
-  *c = hq::choose_decode_xr(fmt, d);
+  *c = hq::choose_decode_xr(fmt, d, cap);
   return c->ok;
 }
 
@@ -264,8 +264,9 @@ Plan make_plan(int fmt, const hq::GemmDesc& d, size_t cap = SIZE_MAX) {
     p.need = hq::prefill_workspace_bytes(d, p.pc);
     return p;
   }
-  if (use_resident(fmt, d, &p.xc)) {
+  if (use_resident(fmt, d, cap, &p.xc)) {
     p.kind = Kind::kResident;
+    p.need = hq::decode_xr_workspace_bytes(d, p.xc);
     return p;
   }
   if (!use_lockstep(fmt, d)) {
@@ -370,7 +371,7 @@ hq_status launch_plan(int fmt, int dtype, const hq::GemmDesc& d, const Plan& p, 
     case Kind::kPrefill: return from_hip(hq::launch_prefill(fmt, dtype, p.pc, w, s), "prefill launch");
     case Kind::kLockstep:
       return from_hip(hq::launch_decode_ls(fmt, dtype, d, p.lc, w, fault, ls_spin(), s), "decode launch");
-    case Kind::kResident: return from_hip(hq::launch_decode_xr(fmt, dtype, d, p.xc, s), "decode launch");
+    case Kind::kResident: return from_hip(hq::launch_decode_xr(fmt, dtype, d, p.xc, w, s), "decode launch");
     case Kind::kDecode: break;
   }
   return from_hip(hq::launch_decode(fmt, dtype, d, p.c, w, s), "decode launch");
@@ -455,8 +456,10 @@ int decode_ring(int T, int U) {
 std::string describe(int fmt, int dtype, const hq::GemmDesc& d, const Plan& p) {
   char b[512];
   if (p.kind == Kind::kResident) {
-    std::snprintf(b, sizeof b, "hq_decode_xr_kernel<%s,%s,T=%d,U=%d> workgroups=%u x %d wavefronts lds=%u ws=0",
-                  fmt_name(fmt), dt_name(dtype), p.xc.T, p.xc.U, xr_slabs(d, p.xc.T), p.xc.WK, p.xc.lds);
+    std::snprintf(b, sizeof b,
+                  "hq_decode_xr_kernel<%s,%s,T=%d,U=%d> workgroups=%u slabs x %d pieces x %d wavefronts lds=%u ws=%zu",
+                  fmt_name(fmt), dt_name(dtype), p.xc.T, p.xc.U, xr_slabs(d, p.xc.T), p.xc.S, p.xc.WK, p.xc.lds,
+                  p.need);
   } else if (p.kind == Kind::kDecode) {
     std::snprintf(b, sizeof b, "hq_decode_kernel<%s,%s,T=%d,U=%d> workgroups=%d x %d wavefronts%s%s ws=%zu",
                   fmt_name(fmt), dt_name(dtype), p.c.T, decode_ring(p.c.T, p.c.U), p.c.SK, p.c.WK,

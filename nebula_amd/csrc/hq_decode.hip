@@ -407,25 +407,33 @@ __global__ void __launch_bounds__(64 * max_wk(T)) hq_decode_kernel(const GemmDes
 }
 
 // ---------------------------------------------------------------------------------------
-// X-resident decode kernel: one workgroup per slab of T column tiles, its WK wavefronts
-// splitting the slab's k-blocks (k-block w, w + WK, ... for wavefront w). The activation
-// rows (M <= 16, all of K) are copied into LDS once, by LDS-DMA, before the weight stream
-// starts; afterwards every wavefront streams its weights through a register ring of U
+// X-resident decode kernel: one workgroup per (slab of T column tiles, piece of its
+// k-blocks), its WK wavefronts splitting the piece's k-blocks (k-block w, w + WK, ... for
+// wavefront w). The activation rows of the piece (M <= 16) are copied into LDS once, by
+// LDS-DMA, before the weight stream starts; afterwards every wavefront streams its weights through a register ring of U
 // steps (T tiles x one k-block each) with no barrier and no activation load in the ring,
 // and reads its A fragments from LDS. Measured on MI355X, a barrier-free register ring
 // streams at the rate of a plain copy, while activation loads from L2 inside the ring (one
 // wavefront fetching them per k-block) or a workgroup barrier per k-block cost 15-25% of
 // the stream. The partial sums of the wavefronts meet once, in LDS, summed in wavefront
-// order (deterministic), after the activation rows are no longer needed.
+// order (deterministic), after the activation rows are no longer needed. With S > 1 pieces
+// per slab each workgroup stores its partial tile to the workspace and the last of the
+// slab's workgroups to arrive (per-slab counter) sums the S partials in piece order.
 //
-// LDS layout of the activation rows: 16-byte units, unit (r * nkb + kb) * 16 + (j ^ r)
-// holds elements 8 j .. 8 j + 7 of k-block kb of row r (j = 0..15). A fragment read of
+// LDS layout of the activation rows of a piece of nkbp k-blocks from kb0: 16-byte units,
+// unit (r * nkbp + kb - kb0) * 16 + (j ^ r) holds elements 8 j .. 8 j + 7 of k-block kb of
+// row r (j = 0..15). A fragment read of
 // chunk c (lane: row c16, slice g4, piece j = 4 c + g4) touches 16 distinct units mod 16
 // in every group of 16 lanes, i.e. every bank once. Lanes of rows >= M read row M - 1:
 // an MFMA output row depends only on its own A row, and rows >= M are never stored.
 struct XrPlan {
-  uint32_t nkb16_m;  // plan_div_magic(16 * nkb)
+  uint32_t S;        // pieces per slab (grid x)
+  uint32_t kq, kr;   // piece p covers k-blocks [p * kq + min(p, kr), ...), kq + (p < kr) of them
+  uint32_t m_lo;     // plan_div_magic(16 * kq)
+  uint32_t m_hi;     // plan_div_magic(16 * (kq + 1))
   uint32_t gmul;     // plan_gmul(gkb)
+  uint32_t* cnt;     // [G] arrival counters, zero between launches (S > 1)
+  float* part;       // [G][S][M * 16 * T] partial tiles (S > 1)
 };
 
 constexpr int xr_max_wk(int T) { return T >= 8 ? 8 : 16; }
@@ -448,7 +456,10 @@ __global__ void __launch_bounds__(64 * xr_max_wk(T)) hq_decode_xr_kernel(const G
   const uint32_t g4 = lane >> 4;
   const uint32_t nkb = d.nkb;
   const uint32_t M = d.M;
-  const uint32_t g = blockIdx.x;
+  const uint32_t p = blockIdx.x;  // piece
+  const uint32_t g = blockIdx.y;  // slab
+  const uint32_t kb0 = p * pl.kq + min(p, pl.kr);
+  const uint32_t nkbp = pl.kq + (p < pl.kr ? 1u : 0u);
 
   uint32_t s = 0;
   if constexpr (FUSED) {
@@ -467,21 +478,23 @@ __global__ void __launch_bounds__(64 * xr_max_wk(T)) hq_decode_xr_kernel(const G
   {
     const uint32_t ldx2 = (uint32_t)d.ldx * 2u;
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(d.X, M * ldx2);
-    const uint32_t nkb16 = nkb * 16u;
+    const uint32_t nkb16 = nkbp * 16u;
+    const uint32_t m16 = p < pl.kr ? pl.m_hi : pl.m_lo;
     const uint32_t nq = (M * nkb16 + 63u) / 64u;
     for (uint32_t q = wave; q < nq; q += WK) {
       const uint32_t u = q * 64u + lane;
-      const uint32_t r = plan_div(u, nkb16, pl.nkb16_m);
+      const uint32_t r = plan_div(u, nkb16, m16);
       const uint32_t rem = u - r * nkb16;
-      const uint32_t voff = r < M ? r * ldx2 + (rem >> 4) * 256u + (((rem & 15u) ^ (r & 15u)) * 16u) : kOutOfRange;
+      const uint32_t voff =
+          r < M ? r * ldx2 + (kb0 + (rem >> 4)) * 256u + (((rem & 15u) ^ (r & 15u)) * 16u) : kOutOfRange;
       buffer_to_lds16(xr, xs + q * 1024u, voff);
     }
   }
   // The ring's first loads must be issued after the copies (vmcnt retires in order).
   __builtin_amdgcn_sched_barrier(0);
 
-  // 2. Weight ring: step j of this wavefront is k-block kb = wave + j * WK, T tiles.
-  const uint32_t nj = wave < nkb ? (nkb - wave + WK - 1u) / WK : 0u;
+  // 2. Weight ring: step j of this wavefront is k-block kb = kb0 + wave + j * WK, T tiles.
+  const uint32_t nj = wave < nkbp ? (nkbp - wave + WK - 1u) / WK : 0u;
   const __amdgpu_buffer_rsrc_t wrs =
       make_rsrc(sg.Wp + (size_t)ct0 * nkb * 64u * WPL, __builtin_amdgcn_readfirstlane(nv * nkb * kBlockBytes));
   const __amdgpu_buffer_rsrc_t srs = make_rsrc(sg.S, __builtin_amdgcn_readfirstlane(((nkb / d.gkb - 1u) * sg.lds + N) * 2u));
@@ -497,7 +510,7 @@ __global__ void __launch_bounds__(64 * xr_max_wk(T)) hq_decode_xr_kernel(const G
   uint32_t sr[U][kSL];
   auto load = [&](int slot, uint32_t j) {
     const bool live = j < nj;
-    const uint32_t kb = wave + j * WK;
+    const uint32_t kb = kb0 + wave + j * WK;
     const uint32_t kbo = __builtin_amdgcn_readfirstlane(live ? kb * kBlockBytes : 0u);
     const uint32_t so = __builtin_amdgcn_readfirstlane(live ? plan_group_of_kb(kb, pl.gmul) * lsrow : 0u);
 #pragma unroll
@@ -517,11 +530,11 @@ __global__ void __launch_bounds__(64 * xr_max_wk(T)) hq_decode_xr_kernel(const G
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(U * (T + kSL)));
   __syncthreads();
 
-  // A fragment addresses: a[c] = xa[c] + kb * 256.
+  // A fragment addresses: a[c] = xa[c] + (kb - kb0) * 256.
   uint32_t xa[4];
   const uint32_t xrow = min(c16, M - 1u);
 #pragma unroll
-  for (int c = 0; c < 4; ++c) xa[c] = (xrow * nkb * 16u + (((4u * c + g4) ^ xrow))) * 16u;
+  for (int c = 0; c < 4; ++c) xa[c] = (xrow * nkbp * 16u + (((4u * c + g4) ^ xrow))) * 16u;
 
   const DqBiasConst dqb = DT == HQ_DTYPE_F16 ? dq_bias_const_f16() : dq_bias_const_bf16();
   const u4 corr_b = int4_corr_fragment<DT>();
@@ -530,10 +543,10 @@ __global__ void __launch_bounds__(64 * xr_max_wk(T)) hq_decode_xr_kernel(const G
   for (int t = 0; t < T; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
 
   auto compute = [&](int u, uint32_t j) {
-    const uint32_t kb = wave + j * WK;
+    const uint32_t kbl = wave + j * WK;  // k-block within the piece
     u4 a[4];
 #pragma unroll
-    for (int c = 0; c < 4; ++c) a[c] = *reinterpret_cast<const u4*>(xs + xa[c] + kb * 256u);
+    for (int c = 0; c < 4; ++c) a[c] = *reinterpret_cast<const u4*>(xs + xa[c] + kbl * 256u);
     uint32_t sbits[T];
 #pragma unroll
     for (int t = 0; t < T; ++t)
@@ -595,9 +608,41 @@ __global__ void __launch_bounds__(64 * xr_max_wk(T)) hq_decode_xr_kernel(const G
     }
   __syncthreads();
   const uint32_t col0 = ct0 * 16u, ncols = nv * 16u;
-  for (uint32_t o4 = threadIdx.x; o4 < SL / 4u; o4 += WK * 64u) {
+  const uint32_t nthr = WK * 64u;
+  // Workspace partials, accessed 16 bytes at a time with the sc1 cache policy: agent-coherent
+  // (visible across XCDs once the store has completed).
+  constexpr int kCoherent = 16;
+  const uint32_t S = pl.S;
+  const __amdgpu_buffer_rsrc_t partr = make_rsrc(pl.part, S > 1u ? gridDim.y * S * SL * 4u : 0u);
+  if (S > 1u) {
+    for (uint32_t o4 = threadIdx.x; o4 < SL / 4u; o4 += nthr) {
+      f4 v = f4{0.f, 0.f, 0.f, 0.f};
+      for (uint32_t w = 0; w < WK; ++w) v += *reinterpret_cast<const f4*>(red + w * SL + 4u * o4);
+      __builtin_amdgcn_raw_buffer_store_b128(v, partr, ((g * S + p) * SL + 4u * o4) * 4u, 0, kCoherent);
+    }
+    // The stores have completed before the barrier, so they are ordered before the arrival
+    // count; the last arriver reads them with coherent loads after seeing the count. The
+    // flag word reuses the (no longer read) reduction area.
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+    __syncthreads();
+    uint32_t* flag = reinterpret_cast<uint32_t*>(xs);
+    if (threadIdx.x == 0) {
+      const uint32_t old = __hip_atomic_fetch_add(pl.cnt + g, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const uint32_t last = old == S - 1u ? 1u : 0u;
+      if (last) __hip_atomic_store(pl.cnt + g, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      *flag = last;
+    }
+    __syncthreads();
+    if (*flag == 0u) return;
+  }
+  for (uint32_t o4 = threadIdx.x; o4 < SL / 4u; o4 += nthr) {
     f4 v = f4{0.f, 0.f, 0.f, 0.f};
-    for (uint32_t w = 0; w < WK; ++w) v += *reinterpret_cast<const f4*>(red + w * SL + 4u * o4);
+    if (S > 1u) {
+      for (uint32_t q = 0; q < S; ++q)  // pieces in order
+        v += __builtin_amdgcn_raw_buffer_load_b128(partr, ((g * S + q) * SL + 4u * o4) * 4u, 0, kCoherent);
+    } else {
+      for (uint32_t w = 0; w < WK; ++w) v += *reinterpret_cast<const f4*>(red + w * SL + 4u * o4);
+    }
     const uint32_t o = 4u * o4, row = o / kCols, lc = o % kCols, n = col0 + lc;
     if (lc >= ncols) continue;
     uint16_t* y = reinterpret_cast<uint16_t*>(sg.Y) + (size_t)row * sg.ldy + n;
@@ -840,25 +885,38 @@ hipError_t launch_decode(int fmt, int dtype, GemmDesc d, const DecodeConfig& c, 
 namespace hq {
 namespace {
 
-// Padded activation area (whole LDS-DMA instructions) of an X-resident workgroup.
-uint32_t xr_x_bytes(const GemmDesc& d) { return (d.M * d.nkb * 16u + 63u) / 64u * 1024u; }
+// Padded activation area (whole LDS-DMA instructions) of an X-resident workgroup whose
+// piece has the most k-blocks (ceil(nkb / S)).
+uint32_t xr_x_bytes(const GemmDesc& d, int S) {
+  const uint32_t nkbp = (d.nkb + (uint32_t)S - 1u) / (uint32_t)S;
+  return (d.M * nkbp * 16u + 63u) / 64u * 1024u;
+}
 
-uint32_t xr_lds_bytes(const GemmDesc& d, int T, int WK) {
-  const uint32_t x = xr_x_bytes(d);
+uint32_t xr_lds_bytes(const GemmDesc& d, int T, int WK, int S) {
+  const uint32_t x = xr_x_bytes(d, S);
   const uint32_t red = (uint32_t)WK * d.M * 16u * (uint32_t)T * 4u;
   return std::max(x, red);
 }
 
 template <int FMT, int DT, int T, int U>
-hipError_t xr_launch_t(GemmDesc d, const XrConfig& c, hipStream_t stream) {
-  if (c.WK < 1 || c.WK > xr_max_wk(T) || d.M > 16u) return hipErrorInvalidValue;
+hipError_t xr_launch_t(GemmDesc d, const XrConfig& c, void* ws, hipStream_t stream) {
+  if (c.WK < 1 || c.WK > xr_max_wk(T) || d.M > 16u || c.S < 1 || (uint32_t)c.S > d.nkb) return hipErrorInvalidValue;
   const uint32_t G = assign_slabs(d, T, 0);
   XrPlan pl{};
-  pl.nkb16_m = plan_div_magic(16u * d.nkb);
+  pl.S = (uint32_t)c.S;
+  pl.kq = d.nkb / pl.S;
+  pl.kr = d.nkb % pl.S;
+  pl.m_lo = plan_div_magic(16u * pl.kq);
+  pl.m_hi = plan_div_magic(16u * (pl.kq + 1u));
   pl.gmul = plan_gmul(d.gkb);
-  // Byte offsets into X, a slab's weights and Y are 32-bit buffer or LDS offsets.
-  bool fits = G >= 1 && (uint64_t)d.M * (uint64_t)d.ldx * 2u < (1ull << 31) && c.lds <= kXrLdsMax &&
-              c.lds >= xr_lds_bytes(d, T, c.WK);
+  if (pl.S > 1) {
+    if (!ws || G > kMaxCounters) return hipErrorInvalidValue;
+    pl.cnt = static_cast<uint32_t*>(ws);
+    pl.part = reinterpret_cast<float*>(static_cast<char*>(ws) + kCounterBytes);
+  }
+  // Byte offsets into X, a slab's weights, Y and the partials are 32-bit buffer or LDS offsets.
+  bool fits = G >= 1 && G <= 65535 && (uint64_t)d.M * (uint64_t)d.ldx * 2u < (1ull << 31) && c.lds <= kXrLdsMax &&
+              c.lds >= xr_lds_bytes(d, T, c.WK, c.S) && (uint64_t)G * pl.S * d.M * 64u * T < (1ull << 31);
   for (uint32_t i = 0; i < d.nseg; ++i)
     fits = fits && (uint64_t)(d.seg[i].slab_w + 1u) * d.nkb * 64u * WTraits<FMT>::wpl * 4u < (1ull << 31);
   if (!fits) return hipErrorInvalidValue;
@@ -869,23 +927,24 @@ hipError_t xr_launch_t(GemmDesc d, const XrConfig& c, hipStream_t stream) {
           : hipFuncSetAttribute(reinterpret_cast<const void*>(&hq_decode_xr_kernel<FMT, DT, T, U, true>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)kXrLdsMax);
   if (attr != hipSuccess) return attr;
+  const dim3 grid(pl.S, G);
   if (d.nseg > 1)
-    hipLaunchKernelGGL((hq_decode_xr_kernel<FMT, DT, T, U, true>), dim3(G), dim3(64 * c.WK), c.lds, stream, d, pl);
+    hipLaunchKernelGGL((hq_decode_xr_kernel<FMT, DT, T, U, true>), grid, dim3(64 * c.WK), c.lds, stream, d, pl);
   else
-    hipLaunchKernelGGL((hq_decode_xr_kernel<FMT, DT, T, U, false>), dim3(G), dim3(64 * c.WK), c.lds, stream, d, pl);
+    hipLaunchKernelGGL((hq_decode_xr_kernel<FMT, DT, T, U, false>), grid, dim3(64 * c.WK), c.lds, stream, d, pl);
   return hipGetLastError();
 }
 
 template <int FMT, int DT>
-hipError_t xr_launch_fd(const GemmDesc& d, const XrConfig& c, hipStream_t stream) {
+hipError_t xr_launch_fd(const GemmDesc& d, const XrConfig& c, void* ws, hipStream_t stream) {
   switch (c.T * 10 + c.U) {
-    case 82: return xr_launch_t<FMT, DT, 8, 2>(d, c, stream);
-    case 42: return xr_launch_t<FMT, DT, 4, 2>(d, c, stream);
-    case 43: return xr_launch_t<FMT, DT, 4, 3>(d, c, stream);
-    case 23: return xr_launch_t<FMT, DT, 2, 3>(d, c, stream);
-    case 24: return xr_launch_t<FMT, DT, 2, 4>(d, c, stream);
-    case 14: return xr_launch_t<FMT, DT, 1, 4>(d, c, stream);
-    case 16: return xr_launch_t<FMT, DT, 1, 6>(d, c, stream);
+    case 82: return xr_launch_t<FMT, DT, 8, 2>(d, c, ws, stream);
+    case 42: return xr_launch_t<FMT, DT, 4, 2>(d, c, ws, stream);
+    case 43: return xr_launch_t<FMT, DT, 4, 3>(d, c, ws, stream);
+    case 23: return xr_launch_t<FMT, DT, 2, 3>(d, c, ws, stream);
+    case 24: return xr_launch_t<FMT, DT, 2, 4>(d, c, ws, stream);
+    case 14: return xr_launch_t<FMT, DT, 1, 4>(d, c, ws, stream);
+    case 16: return xr_launch_t<FMT, DT, 1, 6>(d, c, ws, stream);
     default: return hipErrorInvalidConfiguration;
   }
 }
@@ -927,37 +986,44 @@ static int xr_waves_per_simd(int fmt, int T, int U) {
 }
 
 // Tiling of the X-resident kernel. A workgroup places ceil(WK / 4) wavefronts on each SIMD,
-// so it fits on a CU as often as the register use and the LDS both allow; the planner takes
-// the narrowest slabs (T = 2, 4 or 8 tiles, the most workgroups) whose grid fits on the CUs in
-// one round, eight wavefronts per workgroup (four with 8-tile slabs), two steps in flight
-// (three with 2-tile slabs). Measured on MI355X against the per-wavefront and lockstep
-// kernels (graph-timed, weights rotated past the 256 MiB cache): 5120 x 5120 at M = 1..16
-// 5.7-7.1 us against 7.5-8.4, 27648 x 5120 at M = 1, 2 15.3-15.6 against 16.8-17.3, ternary
-// 5120 x 27648 at M = 1 11.5 against 14.1; with wide weights (more tiles than two per CU)
-// and more than four rows the lockstep kernel, which shares each activation k-block through
-// LDS instead of copying all of K per workgroup, is as fast or faster, so the planner leaves
-// those calls to it. HQ_XR_T / _WK / _U override (tuning and tests).
-XrConfig choose_decode_xr(int fmt, const GemmDesc& d) {
-  XrConfig c{2, 3, 8, 0, false};
+// so it fits on a CU as often as the register use and the LDS both allow. The planner takes
+// whole slabs (S = 1: the activation rows of all of K in LDS) and the narrowest slabs
+// (T = 2, 4 or 8 tiles) whose grid fits on the CUs in one round; only when whole slabs of up to
+// four rows leave more than half of the CUs idle does it cut K into pieces (S > 1) to fill
+// them. Pieces for the rows of a long K that do not fit in LDS measured slower than the
+// lockstep kernel (27648 x 5120, M = 8 and 16: 19.0 and 22.3 us against 18.2 and 20.9; each
+// workgroup copies up to 147 KiB of rows before streaming, and the pieces meet through the
+// workspace), so those calls stay with it. Eight wavefronts per workgroup (four with 8-tile slabs), two steps in flight (three
+// with 2-tile slabs). Measured on MI355X against the per-wavefront and lockstep kernels
+// (graph-timed, weights rotated past the 256 MiB cache): 5120 x 5120 at M = 1..16 5.7-7.1 us
+// against 7.5-8.4, 27648 x 5120 at M = 1, 2 15.0-15.8 against 16.8-17.3, ternary 5120 x 27648
+// at M = 1 12.3 against 14.1. With wide weights (more tiles than two per CU) and more than
+// four rows the lockstep kernel, which streams each activation k-block through LDS instead of
+// copying all of K per workgroup up front, is as fast or faster, so the planner leaves those
+// calls to it. HQ_XR_T / _WK / _U / _S override (tuning and tests).
+XrConfig choose_decode_xr(int fmt, const GemmDesc& d, size_t ws_cap) {
+  XrConfig c{2, 3, 8, 1, 0, false};
   if (d.M > 16u || d.gen) return c;
   const uint32_t cus = (uint32_t)cu_count();
-  const uint32_t xb = xr_x_bytes(d);
-  if (xb > kXrLdsMax) return c;
   uint32_t tiles = 0;
   for (uint32_t i = 0; i < d.nseg; ++i) tiles += d.seg[i].ntiles;
   const int eT = env_int("HQ_XR_T", 0), eWK = env_int("HQ_XR_WK", 0), eU = env_int("HQ_XR_U", 0);
-  const bool forced = eT || eWK || eU;
+  const int eS = env_int("HQ_XR_S", 0);
+  const bool forced = eT || eWK || eU || eS;
   bool found = false;
-  for (int t : {2, 4, 8}) {
-    const int wk = t == 8 ? 4 : 8, u = t == 2 ? 3 : 2;
-    const uint32_t lds = xr_lds_bytes(d, t, wk);
-    if (lds > kXrLdsMax) continue;
-    const uint32_t by_regs = (uint32_t)(xr_waves_per_simd(fmt, t, u) / ((wk + 3) / 4));
-    const uint32_t per_cu = std::min(by_regs, kXrLdsMax / lds);
-    if (per_cu >= 1 && total_slabs(d, t) <= cus * per_cu) {
-      c.T = t;
-      c.WK = wk;
-      c.U = u;
+  for (int s = 1; s <= 8 && !found; ++s) {
+    if ((uint32_t)s > d.nkb || xr_x_bytes(d, s) > kXrLdsMax || (s > 1 && d.M > 4u)) continue;
+    for (int t : {2, 4, 8}) {
+      const int wk = t == 8 ? 4 : 8, u = t == 2 ? 3 : 2;
+      const uint32_t lds = xr_lds_bytes(d, t, wk, s);
+      if (lds > kXrLdsMax) continue;
+      const uint32_t by_regs = (uint32_t)(xr_waves_per_simd(fmt, t, u) / ((wk + 3) / 4));
+      const uint32_t per_cu = std::min(by_regs, kXrLdsMax / lds);
+      const uint32_t wgs = total_slabs(d, t) * (uint32_t)s;
+      if (per_cu < 1 || wgs > cus * per_cu) continue;
+      // Whole slabs leaving more than half of the CUs idle: try a split first.
+      if (s == 1 && wgs * 2u < cus && total_slabs(d, t) * 2u <= cus * per_cu && d.nkb >= 2 && d.M <= 4u) break;
+      c = XrConfig{t, u, wk, s, lds, false};
       found = true;
       break;
     }
@@ -966,24 +1032,32 @@ XrConfig choose_decode_xr(int fmt, const GemmDesc& d) {
   if (eT == 1 || eT == 2 || eT == 4 || eT == 8) c.T = eT;
   if (eWK >= 1) c.WK = eWK;
   if (eU >= 2) c.U = eU;
+  if (eS >= 1) c.S = eS;
   // Snap to an instantiated (T, U).
   if (c.T == 8) c.U = 2;
   if (c.T == 4) c.U = std::min(std::max(c.U, 2), 3);
   if (c.T == 2) c.U = std::min(std::max(c.U, 3), 4);
   if (c.T == 1) c.U = c.U >= 6 ? 6 : 4;
   c.WK = std::max(1, std::min(c.WK, xr_max_wk(c.T)));
-  c.lds = xr_lds_bytes(d, c.T, c.WK);
+  c.S = std::max(1, std::min<int>(c.S, (int)d.nkb));
+  if (c.S > 1 && (total_slabs(d, c.T) > kMaxCounters || decode_xr_workspace_bytes(d, c) > ws_cap)) return c;
+  c.lds = xr_lds_bytes(d, c.T, c.WK, c.S);
   c.ok = c.lds <= kXrLdsMax;
   return c;
 }
 
-hipError_t launch_decode_xr(int fmt, int dtype, GemmDesc d, const XrConfig& c, hipStream_t stream) {
+size_t decode_xr_workspace_bytes(const GemmDesc& d, const XrConfig& c) {
+  if (c.S <= 1) return 0;
+  return kCounterBytes + (size_t)total_slabs(d, c.T) * (size_t)c.S * d.M * 16u * (size_t)c.T * 4u;
+}
+
+hipError_t launch_decode_xr(int fmt, int dtype, GemmDesc d, const XrConfig& c, void* ws, hipStream_t stream) {
   if (fmt == HQ_FORMAT_INT4) {
-    return dtype == HQ_DTYPE_F16 ? xr_launch_fd<HQ_FORMAT_INT4, HQ_DTYPE_F16>(d, c, stream)
-                                 : xr_launch_fd<HQ_FORMAT_INT4, HQ_DTYPE_BF16>(d, c, stream);
+    return dtype == HQ_DTYPE_F16 ? xr_launch_fd<HQ_FORMAT_INT4, HQ_DTYPE_F16>(d, c, ws, stream)
+                                 : xr_launch_fd<HQ_FORMAT_INT4, HQ_DTYPE_BF16>(d, c, ws, stream);
   }
-  return dtype == HQ_DTYPE_F16 ? xr_launch_fd<HQ_FORMAT_TERNARY2, HQ_DTYPE_F16>(d, c, stream)
-                               : xr_launch_fd<HQ_FORMAT_TERNARY2, HQ_DTYPE_BF16>(d, c, stream);
+  return dtype == HQ_DTYPE_F16 ? xr_launch_fd<HQ_FORMAT_TERNARY2, HQ_DTYPE_F16>(d, c, ws, stream)
+                               : xr_launch_fd<HQ_FORMAT_TERNARY2, HQ_DTYPE_BF16>(d, c, ws, stream);
 }
 
 }  // namespace hq

@@ -69,13 +69,16 @@ struct XrConfig {
   int T;
   int U;
   int WK;
+  int S;         // pieces per slab along K (workspace fix-up when > 1)
   uint32_t lds;  // dynamic LDS bytes per workgroup
   bool ok;       // the rows fit in LDS and the kernel takes the call
 };
 // LDS one X-resident workgroup may use (the whole 160 KiB of a gfx950 CU).
 constexpr uint32_t kXrLdsMax = 160u * 1024u;
-XrConfig choose_decode_xr(int fmt, const GemmDesc& d);
-hipError_t launch_decode_xr(int fmt, int dtype, GemmDesc d, const XrConfig& c, hipStream_t stream);
+// ws_cap: the largest workspace the plan may use (no plan with pieces above it).
+XrConfig choose_decode_xr(int fmt, const GemmDesc& d, size_t ws_cap = SIZE_MAX);
+size_t decode_xr_workspace_bytes(const GemmDesc& d, const XrConfig& c);
+hipError_t launch_decode_xr(int fmt, int dtype, GemmDesc d, const XrConfig& c, void* ws, hipStream_t stream);
 
 // Lockstep decode (M <= 80): KG k-groups of GW wavefronts per workgroup own a slab of up
 // to GW * T column tiles and walk one piece of its k-blocks together (S pieces per slab),

@@ -124,9 +124,12 @@ def test_workspace_bytes_fused_is_what_the_call_asks_for():
     assert workspace_bytes_fused(hq.FORMAT_TERNARY2, 8, 1024, [64], bias=1)[0] == hq.HQ_ERR_UNSUPPORTED
 
 
-def test_describe_gemm_names_the_kernel_families():
+def test_describe_gemm_names_the_kernel_families(monkeypatch):
     assert hq.describe(hq.FORMAT_INT4, hq.DTYPE_F16, 1, 27648, 5120).startswith("hq_decode_xr_kernel<int4,f16,")
-    assert hq.describe(hq.FORMAT_INT4, hq.DTYPE_F16, 4, 27648, 5120).startswith("hq_decode_kernel<int4,f16,")
+    assert "x 2 pieces" in hq.describe(hq.FORMAT_INT4, hq.DTYPE_F16, 4, 27648, 5120)
+    with monkeypatch.context() as m:
+        m.setenv("HQ_DECODE_KERNEL", "0")
+        assert hq.describe(hq.FORMAT_INT4, hq.DTYPE_F16, 4, 27648, 5120).startswith("hq_decode_kernel<int4,f16,")
     assert hq.describe(hq.FORMAT_INT4, hq.DTYPE_F16, 16, 5120, 27648).startswith("hq_decode_ls_kernel<int4,f16,")
     assert hq.describe(hq.FORMAT_TERNARY2, hq.DTYPE_BF16, 2048, 5120, 27648).startswith(
         "hq_prefill_kernel<ternary2,bf16")

@@ -515,14 +515,67 @@ def test_xr_fused(cuda, T):
 
 @pytest.mark.parametrize("M,K", [(16, 5120), (8, 5120), (3, 5120), (2, 27648), (1, 27648)])
 def test_xr_lds_limits(cuda, M, K):
-    # Default plans whose activation rows fill the LDS (16 x 5120 halves = 160 KiB), half of
+    # Whole-K plans whose activation rows fill the LDS (16 x 5120 halves = 160 KiB), half of
     # it, or hold the longest K (27648) for one and two rows.
     N = 1000
-    desc = hq.describe(O.INT4, O.F16, M, K, N)
-    assert desc.startswith("hq_decode_xr_kernel<int4,f16,") and f"lds={M * K * 2}" in desc, desc
     P = O.Problem(O.INT4, M, K, N, 128, O.F16, seed=3550 + M)
     D = DeviceProblem(P)
-    check(D.run(), P.reference(threads=16), O.F16, f"xr lds M={M} K={K}", P)
+    with xr_env(T=2, WK=8, S=1):
+        desc = hq.describe(O.INT4, O.F16, M, K, N)
+        assert desc.startswith("hq_decode_xr_kernel<int4,f16,") and f"lds={M * K * 2}" in desc, desc
+        y = D.run()
+    check(y, P.reference(threads=16), O.F16, f"xr lds M={M} K={K}", P)
+
+
+# K pieces per slab (S): even and uneven splits of 16 k-blocks, one k-block per piece, and
+# pieces that leave some wavefronts without k-blocks; the last of a slab's workgroups sums
+# the partials in piece order (bit-identical from run to run) and leaves its counter at zero.
+@pytest.mark.parametrize("T,WK,U,S", [(2, 8, 3, 2), (2, 4, 4, 3), (4, 8, 2, 5), (8, 4, 2, 16), (1, 3, 4, 7),
+                                      (8, 8, 2, 6)])
+@pytest.mark.parametrize("M", [1, 7, 16])
+def test_xr_pieces(cuda, T, WK, U, S, M):
+    import torch
+
+    P = O.Problem(O.INT4, M, 2048, 1000, 128, O.F16, seed=3700 + M)
+    D = DeviceProblem(P)
+    with xr_env(T=T, WK=WK, U=U, S=S):
+        desc = hq.describe(O.INT4, O.F16, M, 2048, 1000)
+        assert desc.startswith(f"hq_decode_xr_kernel<int4,f16,T={T},U={U}>") and f"x {S} pieces" in desc, desc
+        need = hq.workspace_bytes(O.INT4, M, 2048, 1000)
+        assert need > 0
+        ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
+        y = hq.gemm(O.INT4, D.X, D.Wp, D.S, 1000, workspace=ws)
+        y2 = hq.gemm(O.INT4, D.X, D.Wp, D.S, 1000, workspace=ws)
+        y3 = D.run()  # the library's own workspace
+    assert torch_equal(y, y2) and torch_equal(y, y3)
+    torch.cuda.synchronize()
+    assert int(ws[:4 * 64].view(torch.int32).abs().sum().item()) == 0  # counters back at zero
+    check(y, P.reference(), O.F16, f"xr pieces T={T} WK={WK} U={U} S={S} M={M}", P)
+
+
+@pytest.mark.parametrize("fmt,xdt", [(O.TERNARY2, O.BF16), (O.INT4, O.BF16)])
+def test_xr_pieces_fused(cuda, fmt, xdt):
+    Ns, K, M = [600, 130, 1000], 1536, 9
+    probs = [O.Problem(fmt, M, K, n, 256, xdt, seed=3750 + i) for i, n in enumerate(Ns)]
+    for p in probs[1:]:
+        p.X = probs[0].X
+    devs = [DeviceProblem(p) for p in probs]
+    with xr_env(T=4, WK=8, S=5):
+        outs = hq.gemm_fused(fmt, devs[0].X, [(d.Wp, d.S, d.P.N) for d in devs], group=256)
+    for d, y in zip(devs, outs):
+        check(y, d.P.reference(), xdt, f"xr pieces fused N={d.P.N}", d.P)
+
+
+@pytest.mark.parametrize("M", [1, 2, 4])
+def test_xr_pieces_default_plans(cuda, M):
+    # K = 27648, N = 1000: 32 whole slabs would leave most CUs idle (and from M = 3 on the rows
+    # of all of K do not fit in LDS); the planner cuts K.
+    K, N = 27648, 1000
+    desc = hq.describe(O.INT4, O.F16, M, K, N)
+    assert desc.startswith("hq_decode_xr_kernel<int4,f16,") and "x 1 pieces" not in desc, desc
+    P = O.Problem(O.INT4, M, K, N, 128, O.F16, seed=3800 + M)
+    D = DeviceProblem(P)
+    check(D.run(), P.reference(threads=16), O.F16, f"xr default pieces M={M}", P)
 
 
 @pytest.mark.parametrize("M", [1, 4, 16])
