@@ -427,7 +427,8 @@ __global__ void __launch_bounds__(64 * max_wk(T)) hq_decode_kernel(const GemmDes
 // in every group of 16 lanes, i.e. every bank once. Lanes of rows >= M read row M - 1:
 // an MFMA output row depends only on its own A row, and rows >= M are never stored.
 struct XrPlan {
-  uint32_t S;        // pieces per slab (grid x)
+  uint32_t wk;       // wavefronts per workgroup
+  uint32_t S;        // pieces per slab (grid y)
   uint32_t kq, kr;   // piece p covers k-blocks [p * kq + min(p, kr), ...), kq + (p < kr) of them
   uint32_t m_lo;     // plan_div_magic(16 * kq)
   uint32_t m_hi;     // plan_div_magic(16 * (kq + 1))
@@ -451,15 +452,21 @@ __global__ void __launch_bounds__(64 * xr_max_wk(T)) hq_decode_xr_kernel(const G
 
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const uint32_t WK = __builtin_amdgcn_readfirstlane(blockDim.x >> 6);
   const uint32_t c16 = lane & 15u;
   const uint32_t g4 = lane >> 4;
-  const uint32_t nkb = d.nkb;
-  const uint32_t M = d.M;
-  const uint32_t p = blockIdx.x;  // piece
-  const uint32_t g = blockIdx.y;  // slab
-  const uint32_t kb0 = p * pl.kq + min(p, pl.kr);
-  const uint32_t nkbp = pl.kq + (p < pl.kr ? 1u : 0u);
+  const uint32_t g = blockIdx.x;  // slab
+  const uint32_t p = blockIdx.y;  // piece
+  // Every scalar the prologue needs, read from the kernel arguments in one batch: the empty
+  // asm uses them all, so the loads issue together and are waited for once (left to itself
+  // the compiler waited for the plan fields, then the shape, then the activation pointer:
+  // three round trips before the first copy, 0.2-0.3 us on 5120 x 5120).
+  const uint32_t WK = pl.wk, nkb = d.nkb, M = d.M, gkb = d.gkb, ldx = (uint32_t)d.ldx;
+  const uint32_t kq = pl.kq, kr = pl.kr, m_lo = pl.m_lo, m_hi = pl.m_hi, gmul = pl.gmul;
+  const void* const Xp = d.X;
+  asm volatile("" ::"s"(WK), "s"(nkb), "s"(M), "s"(gkb), "s"(ldx), "s"(kq), "s"(kr), "s"(m_lo), "s"(m_hi),
+               "s"(gmul), "s"(Xp));
+  const uint32_t kb0 = p * kq + min(p, kr);
+  const uint32_t nkbp = kq + (p < kr ? 1u : 0u);
 
   uint32_t s = 0;
   if constexpr (FUSED) {
@@ -476,10 +483,10 @@ __global__ void __launch_bounds__(64 * xr_max_wk(T)) hq_decode_xr_kernel(const G
   // 1. Activation rows -> LDS: 64 units per LDS-DMA instruction, instruction q by
   //    wavefront q mod WK; lane i of instruction q fetches the element piece of unit 64 q + i.
   {
-    const uint32_t ldx2 = (uint32_t)d.ldx * 2u;
-    const __amdgpu_buffer_rsrc_t xr = make_rsrc(d.X, M * ldx2);
+    const uint32_t ldx2 = ldx * 2u;
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(Xp, M * ldx2);
     const uint32_t nkb16 = nkbp * 16u;
-    const uint32_t m16 = p < pl.kr ? pl.m_hi : pl.m_lo;
+    const uint32_t m16 = p < kr ? m_hi : m_lo;
     const uint32_t nq = (M * nkb16 + 63u) / 64u;
     for (uint32_t q = wave; q < nq; q += WK) {
       const uint32_t u = q * 64u + lane;
@@ -497,7 +504,7 @@ __global__ void __launch_bounds__(64 * xr_max_wk(T)) hq_decode_xr_kernel(const G
   const uint32_t nj = wave < nkbp ? (nkbp - wave + WK - 1u) / WK : 0u;
   const __amdgpu_buffer_rsrc_t wrs =
       make_rsrc(sg.Wp + (size_t)ct0 * nkb * 64u * WPL, __builtin_amdgcn_readfirstlane(nv * nkb * kBlockBytes));
-  const __amdgpu_buffer_rsrc_t srs = make_rsrc(sg.S, __builtin_amdgcn_readfirstlane(((nkb / d.gkb - 1u) * sg.lds + N) * 2u));
+  const __amdgpu_buffer_rsrc_t srs = make_rsrc(sg.S, __builtin_amdgcn_readfirstlane(((nkb / gkb - 1u) * sg.lds + N) * 2u));
   const uint32_t lsrow = sg.lds * 2u;
   uint32_t wvo[T];
 #pragma unroll
@@ -512,7 +519,7 @@ __global__ void __launch_bounds__(64 * xr_max_wk(T)) hq_decode_xr_kernel(const G
     const bool live = j < nj;
     const uint32_t kb = kb0 + wave + j * WK;
     const uint32_t kbo = __builtin_amdgcn_readfirstlane(live ? kb * kBlockBytes : 0u);
-    const uint32_t so = __builtin_amdgcn_readfirstlane(live ? plan_group_of_kb(kb, pl.gmul) * lsrow : 0u);
+    const uint32_t so = __builtin_amdgcn_readfirstlane(live ? plan_group_of_kb(kb, gmul) * lsrow : 0u);
 #pragma unroll
     for (int t = 0; t < T; ++t) {
       if constexpr (WPL == 4) wr[slot][t] = __builtin_amdgcn_raw_buffer_load_b128(wrs, live ? wvo[t] : kOutOfRange, kbo, kStreamAux);
@@ -613,7 +620,7 @@ __global__ void __launch_bounds__(64 * xr_max_wk(T)) hq_decode_xr_kernel(const G
   // (visible across XCDs once the store has completed).
   constexpr int kCoherent = 16;
   const uint32_t S = pl.S;
-  const __amdgpu_buffer_rsrc_t partr = make_rsrc(pl.part, S > 1u ? gridDim.y * S * SL * 4u : 0u);
+  const __amdgpu_buffer_rsrc_t partr = make_rsrc(pl.part, S > 1u ? gridDim.x * S * SL * 4u : 0u);
   if (S > 1u) {
     for (uint32_t o4 = threadIdx.x; o4 < SL / 4u; o4 += nthr) {
       f4 v = f4{0.f, 0.f, 0.f, 0.f};
@@ -909,6 +916,7 @@ hipError_t xr_launch_t(GemmDesc d, const XrConfig& c, void* ws, hipStream_t stre
   pl.m_lo = plan_div_magic(16u * pl.kq);
   pl.m_hi = plan_div_magic(16u * (pl.kq + 1u));
   pl.gmul = plan_gmul(d.gkb);
+  pl.wk = (uint32_t)c.WK;
   if (pl.S > 1) {
     if (!ws || G > kMaxCounters) return hipErrorInvalidValue;
     pl.cnt = static_cast<uint32_t*>(ws);
@@ -927,7 +935,7 @@ hipError_t xr_launch_t(GemmDesc d, const XrConfig& c, void* ws, hipStream_t stre
           : hipFuncSetAttribute(reinterpret_cast<const void*>(&hq_decode_xr_kernel<FMT, DT, T, U, true>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)kXrLdsMax);
   if (attr != hipSuccess) return attr;
-  const dim3 grid(pl.S, G);
+  const dim3 grid(G, pl.S);
   if (d.nseg > 1)
     hipLaunchKernelGGL((hq_decode_xr_kernel<FMT, DT, T, U, true>), grid, dim3(64 * c.WK), c.lds, stream, d, pl);
   else
