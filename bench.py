@@ -13,8 +13,10 @@ The same JSON line also carries:
   cases         per launch shape: average launch duration (HIP events on the launch stream
                 around back-to-back launches of one captured graph, rotating weight copies),
                 GB/s and fraction of the 8 TB/s HBM peak, and the plan (kernel, tiling) that
-                ran. The decode sweep's 15 shapes, the single W4A16 GEMM (M=16, K=N=4096)
-                and the ternary bf16 decode (K=5120, N=27648, M in {1, 8});
+                ran. The decode sweep's 15 shapes, the single W4A16 GEMM (M=16, K=N=4096),
+                the ternary bf16 decode (K=5120, N=27648, M in {1, 8}) and the int8 path
+                (fp32 activations, int8 weights, K=5120, N=27648, M in {1, 8}; bytes = int8
+                weights + fp32 scales);
   roofline      the dominant decode kernel (the kernel with the largest share of the step
                 time): its algorithmic bytes (packed weights + scales) per launch / its
                 average launch duration, against 8 TB/s; `traffic` is the HBM bytes per
@@ -316,6 +318,30 @@ def run_gpu(args):
     for M in (1, 8):
         cases[f"ternary_bf16_K{K}_N{N}_M{M}"] = time_case(FMT_TERN, K, N, M, ws, ss, Xt, Yt, dtype=2)
     del ws, ss
+    torch.cuda.empty_cache()
+
+    # ---- the int8 path (forward_cutlass_int8's operands: fp32 activations, int8 [K][N] weights) ----
+    K, N = 5120, 27648
+    packed = torch.from_numpy(hq.repack_int8(torch.randint(-128, 128, (K, N), dtype=torch.int8).numpy()))
+    copies = max(2, -(-ROTATE_BYTES // (K * N)))
+    w8 = [packed.cuda() for _ in range(copies)]
+    del packed
+    s8 = torch.rand(N, device="cuda") * 0.1 + 0.05
+    X8 = torch.randn((8, K), device="cuda") * 0.5
+    Y8 = torch.empty((8, N), device="cuda")
+    for M in (1, 8):
+        def launches(M=M):
+            reps = copies * max(1, 64 // copies)
+            for r in range(reps):
+                hq.gemm_w8a8(X8[:M], w8[r % copies], s8, N, out=Y8[:M])
+            return reps
+        us = graph_time_us(torch, stream, launches)
+        gbs = (K * N + N * 4) / (us * 1e-6) / 1e9
+        cases[f"int8_w8a8_K{K}_N{N}_M{M}"] = {"us": round(us, 2), "GBps": round(gbs, 1),
+                                             "pct_hbm": round(100 * gbs / HBM_PEAK_GBS, 1),
+                                             "plan": "hq_quantize_x_kernel + hq_w8a8_kernel (two launches)"}
+        log(f"int8 K={K} N={N} M={M}: {us:.2f} us, {gbs:.0f} GB/s")
+    del w8
     torch.cuda.empty_cache()
 
     # ---- prefill and the split-fuse mixed batch ----

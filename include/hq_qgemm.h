@@ -285,6 +285,39 @@ hq_status hq_gemm_fused_noalloc(const void* X, hq_dtype dtype, int64_t ldx, hq_f
                                 const hq_segment* segs, uint32_t nseg, uint32_t M, uint32_t K,
                                 uint32_t group, hq_stream stream);
 
+/* ---- The int8 path --------------------------------------------------------------------
+ * Replaces MarlinGemmEngine::forward_cutlass_int8 (hydrogen/src/model/marlin_gemm.cu:603-617)
+ * and kernel_cutlass_int8_gemm (:327-377), which the reference builds but never launches.
+ * Same operands and semantics: fp32 activations X [M][ldx] quantised per element to
+ * int8(clamp(x * 127, -128, 127)) converted toward zero; int8 weights [K][N] (the reference's
+ * W_int8: q * 16 - 128 of its int4 codes, :508), repacked once into the gfx950 tile layout;
+ * one fp32 scale per column (the reference reads row 0 of its scale matrix); fp32 output
+ * Y[m][n] = scales[n] * (sum_k xq[m][k] * w[k][n]) / 127. The products are summed exactly in
+ * int32 (the reference sums fp32 quad by quad, which differs by its own rounding only).
+ * M <= 16 (the reference's kernel takes M <= 8); K a multiple of 128, at most 131072 (the int32
+ * sum cannot overflow); N >= 1. */
+
+/* Bytes of the int8 tile layout of a K x N weight (N padded to 16 columns): K * ceil(N/16) * 16;
+ * 0 if K is not a positive multiple of 128 or N is 0. */
+size_t hq_int8_packed_bytes(uint32_t K, uint32_t N);
+
+/* Host repack of int8 weights w_kn [K][N] into the tile layout (hq_int8_packed_bytes(K, N)
+ * bytes, padding columns zero), and its inverse. Replaces the upload of h_W_int8
+ * (marlin_gemm.cu:517): the tile layout is what hq_gemm_w8a8 streams. */
+hq_status hq_repack_int8(const int8_t* w_kn, uint32_t K, uint32_t N, int8_t* packed);
+hq_status hq_unpack_int8(const int8_t* packed, uint32_t K, uint32_t N, int8_t* w_kn);
+
+/* Workspace bytes of an hq_gemm_w8a8 call (the quantised activations, and the partial sums when
+ * the call splits K): a NULL workspace makes the library use its own. */
+hq_status hq_workspace_bytes_w8a8(uint32_t M, uint32_t K, uint32_t N, size_t* bytes);
+
+/* The int8 GEMM on `stream`. X 16-byte aligned with ldx >= K a multiple of 4; Wp (the tile
+ * layout) 16-byte aligned; scales [N] fp32; Y [M][ldy] fp32, ldy >= N. workspace: NULL or
+ * hq_workspace_bytes_w8a8 bytes, 256-byte aligned. */
+hq_status hq_gemm_w8a8(const float* X, int64_t ldx, const int8_t* Wp, const float* scales, float* Y, int64_t ldy,
+                       uint32_t M, uint32_t K, uint32_t N, void* workspace, size_t workspace_bytes,
+                       hq_stream stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -22,7 +22,7 @@ BINDIR = PKG / "bin"
 BENCH_TOOL = BINDIR / "hq_bench_qgemm"
 ORACLE_DIR = ROOT / "oracle"
 
-SOURCES = ["hq_api.cpp", "hq_gguf.cpp", "hq_decode.hip", "hq_decode_ls.hip", "hq_prefill.hip", "hq_repack.hip"]
+SOURCES = ["hq_api.cpp", "hq_gguf.cpp", "hq_decode.hip", "hq_decode_ls.hip", "hq_prefill.hip", "hq_repack.hip", "hq_int8.hip"]
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = "gfx950"
 

@@ -485,6 +485,23 @@ std::string describe(int fmt, int dtype, const hq::GemmDesc& d, const Plan& p) {
 
 }  // namespace
 
+namespace {
+// Byte of the tile layout holding w[k][n] (column tile n / 16, k-block k / 128; lane
+// 16 ((k % 64) / 16) + n % 16 holds 16 consecutive k of chunk (k % 128) / 64 at byte 16 c).
+inline size_t int8_tile_byte(uint32_t k, uint32_t n, uint32_t nkb) {
+  const uint32_t ct = n / 16u, kb = k / 128u, c = (k % 128u) / 64u, s = (k % 64u) / 16u, i = k % 16u;
+  const uint32_t lane = 16u * s + n % 16u;
+  return ((size_t)ct * nkb + kb) * 2048u + lane * 32u + c * 16u + i;
+}
+
+hq_status check_int8_shape(uint32_t K, uint32_t N) {
+  if (K == 0 || K % hq::kBlockK) return fail(HQ_ERR_SHAPE, "K=%u must be a positive multiple of 128", K);
+  if (K > 131072u) return fail(HQ_ERR_SHAPE, "K=%u exceeds 131072 (the int32 sum could overflow)", K);
+  if (N == 0) return fail(HQ_ERR_SHAPE, "N must be >= 1");
+  return HQ_OK;
+}
+}  // namespace
+
 extern "C" {
 
 const char* hq_version(void) { return "nebula-hq 0.2.0 (gfx950, ABI 2)"; }
@@ -753,6 +770,84 @@ hq_status hq_gemm_fused(const void* X, hq_dtype dtype, int64_t ldx, hq_format fm
                         uint32_t nseg, uint32_t M, uint32_t K, uint32_t group, void* ws, size_t ws_bytes,
                         hq_stream stream) {
   return run_gemm(X, dtype, ldx, fmt, segs, nseg, M, K, group, ws, ws_bytes, stream);
+}
+
+// ---- the int8 path (hq_int8.hip) ----
+size_t hq_int8_packed_bytes(uint32_t K, uint32_t N) {
+  if (K == 0 || N == 0 || K % hq::kBlockK) return 0;
+  return (size_t)K * hq::col_tiles(N) * 16u;
+}
+
+hq_status hq_repack_int8(const int8_t* w, uint32_t K, uint32_t N, int8_t* packed) {
+  if (!w || !packed) return fail(HQ_ERR_INVALID_ARG, "null pointer");
+  hq_status st = check_int8_shape(K, N);
+  if (st != HQ_OK) return st;
+  const uint32_t nkb = K / hq::kBlockK, nt = hq::col_tiles(N);
+  parallel_for((size_t)nt * nkb, [=](size_t b, size_t e) {
+    for (size_t blk = b; blk < e; ++blk) {
+      const uint32_t ct = (uint32_t)(blk / nkb), kb = (uint32_t)(blk % nkb);
+      for (uint32_t kk = 0; kk < 128u; ++kk)
+        for (uint32_t c16 = 0; c16 < 16u; ++c16) {
+          const uint32_t k = kb * 128u + kk, n = ct * 16u + c16;
+          packed[int8_tile_byte(k, n, nkb)] = n < N ? w[(size_t)k * N + n] : (int8_t)0;
+        }
+    }
+  });
+  return HQ_OK;
+}
+
+hq_status hq_unpack_int8(const int8_t* packed, uint32_t K, uint32_t N, int8_t* w) {
+  if (!w || !packed) return fail(HQ_ERR_INVALID_ARG, "null pointer");
+  hq_status st = check_int8_shape(K, N);
+  if (st != HQ_OK) return st;
+  const uint32_t nkb = K / hq::kBlockK;
+  parallel_for((size_t)K, [=](size_t b, size_t e) {
+    for (size_t k = b; k < e; ++k)
+      for (uint32_t n = 0; n < N; ++n) w[k * N + n] = packed[int8_tile_byte((uint32_t)k, n, nkb)];
+  });
+  return HQ_OK;
+}
+
+hq_status hq_workspace_bytes_w8a8(uint32_t M, uint32_t K, uint32_t N, size_t* bytes) {
+  if (!bytes) return fail(HQ_ERR_INVALID_ARG, "bytes is null");
+  hq_status st = check_int8_shape(K, N);
+  if (st != HQ_OK) return st;
+  if (M == 0 || M > 16) return fail(HQ_ERR_UNSUPPORTED, "the int8 path takes 1..16 rows, got M=%u", M);
+  const hq::W8Config c = hq::choose_w8a8(M, K, N);
+  if (!c.ok) return fail(HQ_ERR_UNSUPPORTED, "no int8 plan for M=%u K=%u N=%u", M, K, N);
+  *bytes = hq::w8a8_workspace_bytes(M, K, N, c);
+  return HQ_OK;
+}
+
+hq_status hq_gemm_w8a8(const float* X, int64_t ldx, const int8_t* Wp, const float* scales, float* Y, int64_t ldy,
+                       uint32_t M, uint32_t K, uint32_t N, void* ws, size_t ws_bytes, hq_stream stream) {
+  if (take_fault()) return fault_status();
+  if (!X || !Wp || !scales || !Y) return fail(HQ_ERR_INVALID_ARG, "null pointer");
+  hq_status st = check_int8_shape(K, N);
+  if (st != HQ_OK) return st;
+  if (M == 0 || M > 16) return fail(HQ_ERR_UNSUPPORTED, "the int8 path takes 1..16 rows, got M=%u", M);
+  if (ldx < (int64_t)K || ldx % 4) return fail(HQ_ERR_SHAPE, "ldx=%lld must be >= K=%u and a multiple of 4", (long long)ldx, K);
+  if (ldy < (int64_t)N) return fail(HQ_ERR_SHAPE, "ldy=%lld < N=%u", (long long)ldy, N);
+  if ((uint64_t)M * (uint64_t)ldx >= (1ull << 29) || (uint64_t)M * (uint64_t)ldy >= (1ull << 31))
+    return fail(HQ_ERR_SHAPE, "X or Y too large for 32-bit offsets");
+  if (reinterpret_cast<uintptr_t>(X) % 16 || reinterpret_cast<uintptr_t>(Wp) % 16)
+    return fail(HQ_ERR_ALIGNMENT, "X and Wp must be 16-byte aligned");
+  if (reinterpret_cast<uintptr_t>(scales) % 4 || reinterpret_cast<uintptr_t>(Y) % 4)
+    return fail(HQ_ERR_ALIGNMENT, "scales and Y must be 4-byte aligned");
+  const hq::W8Config c = hq::choose_w8a8(M, K, N);
+  if (!c.ok) return fail(HQ_ERR_UNSUPPORTED, "no int8 plan for M=%u K=%u N=%u", M, K, N);
+  const size_t need = hq::w8a8_workspace_bytes(M, K, N, c);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  void* w = nullptr;
+  if (ws) {
+    if (ws_bytes < need)
+      return fail(HQ_ERR_WORKSPACE, "workspace of %zu bytes is smaller than the %zu this call needs", ws_bytes, need);
+    if (reinterpret_cast<uintptr_t>(ws) % 256) return fail(HQ_ERR_ALIGNMENT, "workspace must be 256-byte aligned");
+    w = ws;
+  } else if ((st = get_internal_ws(s, need, &w)) != HQ_OK) {
+    return st;
+  }
+  return from_hip(hq::launch_w8a8(X, (uint32_t)ldx, Wp, scales, Y, (uint32_t)ldy, M, K, N, c, w, s), "int8 launch");
 }
 
 hq_status hq_gemm_fused_noalloc(const void* X, hq_dtype dtype, int64_t ldx, hq_format fmt, const hq_segment* segs,

@@ -80,6 +80,21 @@ XrConfig choose_decode_xr(int fmt, const GemmDesc& d, size_t ws_cap = SIZE_MAX);
 size_t decode_xr_workspace_bytes(const GemmDesc& d, const XrConfig& c);
 hipError_t launch_decode_xr(int fmt, int dtype, GemmDesc d, const XrConfig& c, void* ws, hipStream_t stream);
 
+// The int8 path (hq_int8.hip): T column tiles per slab, U steps in flight, WK wavefronts, S K
+// pieces per slab; lds: dynamic LDS bytes per workgroup.
+struct W8Config {
+  int T;
+  int U;
+  int WK;
+  int S;
+  uint32_t lds;
+  bool ok;
+};
+W8Config choose_w8a8(uint32_t M, uint32_t K, uint32_t N);
+size_t w8a8_workspace_bytes(uint32_t M, uint32_t K, uint32_t N, const W8Config& c);
+hipError_t launch_w8a8(const float* X, uint32_t ldx, const int8_t* Wp, const float* scales, float* Y, uint32_t ldy,
+                       uint32_t M, uint32_t K, uint32_t N, const W8Config& c, void* ws, hipStream_t stream);
+
 // Lockstep decode (M <= 80): KG k-groups of GW wavefronts per workgroup own a slab of up
 // to GW * T column tiles and walk one piece of its k-blocks together (S pieces per slab),
 // each k-group sharing its activation k-block (MT tiles of 16 rows) through LDS.

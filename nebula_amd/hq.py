@@ -45,6 +45,7 @@ EXPORTS = (
     "hq_repack_tq1_0_device", "hq_gguf_open", "hq_gguf_parse", "hq_gguf_close", "hq_gguf_header",
     "hq_gguf_tensor_at", "hq_gguf_find_tensor", "hq_gguf_get_int", "hq_gguf_get_float", "hq_gguf_get_string",
     "hq_gguf_get_array", "hq_gguf_load_tq1_0", "hq_convert_q4_k", "hq_gguf_convert_q4_k",
+    "hq_int8_packed_bytes", "hq_repack_int8", "hq_unpack_int8", "hq_workspace_bytes_w8a8", "hq_gemm_w8a8",
 )
 
 
@@ -116,6 +117,15 @@ def lib() -> ctypes.CDLL:
     L.hq_gemm_fused.argtypes = [vp, i32, i64, i32, ctypes.POINTER(Segment), u32, u32, u32, u32, vp, sz, vp]
     L.hq_gemm_fused_noalloc.restype = i32
     L.hq_gemm_fused_noalloc.argtypes = [vp, i32, i64, i32, ctypes.POINTER(Segment), u32, u32, u32, u32, vp]
+    L.hq_int8_packed_bytes.restype = sz
+    L.hq_int8_packed_bytes.argtypes = [u32, u32]
+    for f in (L.hq_repack_int8, L.hq_unpack_int8):
+        f.restype = i32
+        f.argtypes = [vp, u32, u32, vp]
+    L.hq_workspace_bytes_w8a8.restype = i32
+    L.hq_workspace_bytes_w8a8.argtypes = [u32, u32, u32, ctypes.POINTER(sz)]
+    L.hq_gemm_w8a8.restype = i32
+    L.hq_gemm_w8a8.argtypes = [vp, i64, vp, vp, vp, i64, u32, u32, u32, vp, sz, vp]
     _lib = L
     return L
 
@@ -396,3 +406,51 @@ def gemm_fused(fmt: int, X, segments: Sequence[tuple], group: int = 128, outs=No
     check(lib().hq_gemm_fused(X.data_ptr(), _dt(X), X.stride(0), fmt, arr, len(segments), M, K, group, wp, wb,
                               _stream_ptr(stream)))
     return outs
+
+
+# ---------------------------------------------------------------- the int8 path
+def repack_int8(w_kn: np.ndarray) -> np.ndarray:
+    """int8 weights [K][N] -> the gfx950 int8 tile layout (hq_int8_packed_bytes(K, N) int8)."""
+    w_kn = np.ascontiguousarray(w_kn, dtype=np.int8)
+    K, N = w_kn.shape
+    out = np.empty(lib().hq_int8_packed_bytes(K, N), dtype=np.int8)
+    if out.size == 0:
+        raise ValueError(f"K={K} must be a positive multiple of 128 and N >= 1")
+    check(lib().hq_repack_int8(w_kn.ctypes.data, K, N, out.ctypes.data))
+    return out
+
+
+def unpack_int8(packed: np.ndarray, K: int, N: int) -> np.ndarray:
+    packed = np.ascontiguousarray(packed, dtype=np.int8)
+    if packed.size != lib().hq_int8_packed_bytes(K, N):
+        raise ValueError("packed size does not match K, N")
+    out = np.empty((K, N), dtype=np.int8)
+    check(lib().hq_unpack_int8(packed.ctypes.data, K, N, out.ctypes.data))
+    return out
+
+
+def workspace_bytes_w8a8(M: int, K: int, N: int) -> int:
+    b = ctypes.c_size_t(0)
+    check(lib().hq_workspace_bytes_w8a8(M, K, N, ctypes.byref(b)))
+    return b.value
+
+
+def gemm_w8a8(X, Wp, scales, N: int, out=None, stream=None, workspace=None):
+    """The int8 path: Y[M, N] (fp32) = scales[n] * sum_k int8(clamp(127 X)) W / 127, X fp32 [M, K]
+    (M <= 16), Wp the int8 tile layout (repack_int8) on X's device, scales fp32 [N]."""
+    import torch
+
+    M, K = X.shape
+    _check_rows("X", X, M, K, torch.float32)
+    if X.stride(0) % 4:
+        raise ValueError("X's row stride must be a multiple of 4 elements")
+    for name, t, dt, n in (("Wp", Wp, torch.int8, lib().hq_int8_packed_bytes(K, N)), ("scales", scales, torch.float32, N)):
+        if t.device != X.device or t.dtype != dt or not t.is_contiguous() or t.numel() < n:
+            raise ValueError(f"{name} must be a contiguous {dt} device tensor of at least {n} elements on X's device")
+    if out is None:
+        out = torch.empty((M, N), dtype=torch.float32, device=X.device)
+    _check_rows("out", out, M, N, torch.float32)
+    wp, wb = _ws(workspace)
+    check(lib().hq_gemm_w8a8(X.data_ptr(), X.stride(0), Wp.data_ptr(), scales.data_ptr(), out.data_ptr(), out.stride(0),
+                             M, K, N, wp, wb, _stream_ptr(stream)))
+    return out

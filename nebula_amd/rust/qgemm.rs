@@ -140,6 +140,15 @@ extern "C" {
                          stream: Stream) -> Status;
     pub fn hq_gemm_fused_noalloc(x: *const c_void, dtype: Dtype, ldx: i64, fmt: Format, segs: *const Segment,
                                  nseg: u32, m: u32, k: u32, group: u32, stream: Stream) -> Status;
+
+    // The int8 path (forward_cutlass_int8, hydrogen/src/model/marlin_gemm.cu:603-617).
+    pub fn hq_int8_packed_bytes(k: u32, n: u32) -> usize;
+    pub fn hq_repack_int8(w_kn: *const i8, k: u32, n: u32, packed: *mut i8) -> Status;
+    pub fn hq_unpack_int8(packed: *const i8, k: u32, n: u32, w_kn: *mut i8) -> Status;
+    pub fn hq_workspace_bytes_w8a8(m: u32, k: u32, n: u32, bytes: *mut usize) -> Status;
+    pub fn hq_gemm_w8a8(x: *const f32, ldx: i64, wp: *const i8, scales: *const f32, y: *mut f32, ldy: i64,
+                        m: u32, k: u32, n: u32, workspace: *mut c_void, workspace_bytes: usize,
+                        stream: Stream) -> Status;
 }
 
 /// A failed call: the status and hq_last_error's message (the reference throws

@@ -355,3 +355,41 @@ void hqo_dequant_q4_k(const uint8_t* blocks, uint32_t K, uint32_t N, float* w) {
         }
     }
 }
+
+/* ---- the int8 path ---- */
+void hqo_int8_from_int4(const uint32_t* w, uint32_t K, uint32_t N, int8_t* out) {
+    for (uint32_t kw = 0; kw < K / 8; ++kw)
+        for (uint32_t n = 0; n < N; ++n)
+            for (uint32_t i = 0; i < 8; ++i) {
+                const int q = (int)((w[(size_t)kw * N + n] >> (4 * i)) & 0xFu);
+                out[(size_t)(8 * kw + i) * N + n] = (int8_t)(q * 16 - 128);
+            }
+}
+
+int8_t hqo_quantize_x_int8(float x) {
+    /* marlin_gemm.cu:356-359: static_cast<int8_t>(fminf(fmaxf(X * 127.0f, -128.0f), 127.0f)) */
+    const float t = fminf(fmaxf(x * 127.0f, -128.0f), 127.0f);
+    return (int8_t)t;
+}
+
+void hqo_gemm_int8(const float* X, size_t ldx, const int8_t* W, const float* scales, uint32_t M, uint32_t K,
+                   uint32_t N, float* Y, int threads) {
+    if (threads <= 0) threads = 1;
+    const uint32_t nq = K / 4;
+    int8_t* xq = (int8_t*)malloc((size_t)M * K + 1);
+    for (uint32_t m = 0; m < M; ++m)
+        for (uint32_t k = 0; k < K; ++k) xq[(size_t)m * K + k] = hqo_quantize_x_int8(X[(size_t)m * ldx + k]);
+#pragma omp parallel for schedule(static) num_threads(threads)
+    for (long long u = 0; u < (long long)M * N; ++u) {
+        const uint32_t m = (uint32_t)(u / N), n = (uint32_t)(u % N);
+        const int8_t* x = xq + (size_t)m * K;
+        float acc = 0.0f;
+        for (uint32_t q = 0; q < nq; ++q) {
+            int32_t dot = 0;
+            for (uint32_t i = 0; i < 4; ++i) dot += (int32_t)x[4 * q + i] * (int32_t)W[(size_t)(4 * q + i) * N + n];
+            acc = fmaf((float)dot, 1.0f / 127.0f, acc);
+        }
+        Y[(size_t)m * N + n] = acc * scales[n];
+    }
+    free(xq);
+}

@@ -21,6 +21,9 @@
  *   hqo_dequant_q4_k      GGML's published Q4_K block (dequantize_row_q4_K of GGML / llama.cpp); the
  *                         reference names the type (hydrogen/include/gguf_parser.hpp:44, 130) but has
  *                         no decoder for it, so this one is pinned by the published layout only
+ *   hqo_int8_from_int4    hydrogen/src/model/marlin_gemm.cu:508 (h_W_int8 = q * 16 - 128)
+ *   hqo_quantize_x_int8   hydrogen/src/model/marlin_gemm.cu:356-359 (int8(clamp(x * 127, -128, 127)))
+ *   hqo_gemm_int8         hydrogen/src/model/marlin_gemm.cu:327-377 (kernel_cutlass_int8_gemm, any M)
  *
  * The generator (hqo_rng_*, hqo_gen_*) is this build's own specification, not
  * the reference's: the reference seeds std::mt19937 with implementation-defined
@@ -119,6 +122,19 @@ void hqo_gemv_tq1_0(const float* X, const uint8_t* W, float* Y, uint32_t M, uint
  * code q[32 c + l] & 15, weight 64 c + 32 + l the high nibble; w = (d * sc) * q - dmin * m in fp32
  * (separate roundings). Output fp32 Wdq[k*N + n]. */
 void hqo_dequant_q4_k(const uint8_t* blocks, uint32_t K, uint32_t N, float* wdq);
+
+/* ---- the int8 path (kernel_cutlass_int8_gemm; never launched by the reference) ---- */
+/* out[k*N + n] = q * 16 - 128 for the int4 code q of (k, n) in the linear layout. */
+void hqo_int8_from_int4(const uint32_t* w_linear, uint32_t K, uint32_t N, int8_t* out);
+/* fminf(fmaxf(x * 127, -128), 127) converted toward zero (NaN -> -128, as fmaxf returns the
+ * other operand). */
+int8_t hqo_quantize_x_int8(float x);
+/* Y[m*N + n] = acc * scales[n], acc accumulating, quad by quad over k (4 q .. 4 q + 3, K / 4
+ * quads), fmaf((float)dot, 1.0f / 127.0f, acc) with dot the exact integer product of the
+ * quantised activations and W[k*N + n] (int8, [K][N]); X fp32 [M][ldx]; scales fp32 [N] (the
+ * reference passes its scale matrix and reads row 0). */
+void hqo_gemm_int8(const float* X, size_t ldx, const int8_t* W, const float* scales, uint32_t M, uint32_t K,
+                   uint32_t N, float* Y, int threads);
 
 #ifdef __cplusplus
 }

@@ -61,6 +61,10 @@ def lib() -> ctypes.CDLL:
     L.hqo_tq1_0_scale.argtypes = [vp]
     L.hqo_gemv_tq1_0.argtypes = [vp, vp, vp, u32, u32, u32, i32]
     L.hqo_dequant_q4_k.argtypes = [vp, u32, u32, vp]
+    L.hqo_int8_from_int4.argtypes = [vp, u32, u32, vp]
+    L.hqo_quantize_x_int8.argtypes = [f32]
+    L.hqo_quantize_x_int8.restype = ctypes.c_int8
+    L.hqo_gemm_int8.argtypes = [vp, sz, vp, vp, u32, u32, u32, vp, i32]
     _lib = L
     return L
 
@@ -284,3 +288,27 @@ def dequant_q4_k(blocks: np.ndarray, K: int, N: int) -> np.ndarray:
     out = np.empty((K, N), dtype=np.float32)
     lib().hqo_dequant_q4_k(_p(b), K, N, _p(out))
     return out
+
+
+# ---------------------------------------------------------------- the int8 path
+def int8_from_int4(linear: np.ndarray, K: int, N: int) -> np.ndarray:
+    """int8 [K][N] weights q * 16 - 128 of the int4 codes (marlin_gemm.cu:508)."""
+    out = np.empty((K, N), dtype=np.int8)
+    lib().hqo_int8_from_int4(_p(np.ascontiguousarray(linear, dtype=np.uint32)), K, N, _p(out))
+    return out
+
+
+def quantize_x_int8(x: float) -> int:
+    return int(lib().hqo_quantize_x_int8(float(x)))
+
+
+def gemm_int8(X: np.ndarray, W: np.ndarray, scales: np.ndarray, threads: int = 8) -> np.ndarray:
+    """kernel_cutlass_int8_gemm (marlin_gemm.cu:327-377): X fp32 [M][K], W int8 [K][N], scales fp32 [N]."""
+    X = np.ascontiguousarray(X, dtype=np.float32)
+    W = np.ascontiguousarray(W, dtype=np.int8)
+    scales = np.ascontiguousarray(scales, dtype=np.float32)
+    M, K = X.shape
+    N = W.shape[1]
+    Y = np.empty((M, N), dtype=np.float32)
+    lib().hqo_gemm_int8(_p(X), K, _p(W), _p(scales), M, K, N, _p(Y), threads)
+    return Y

@@ -343,3 +343,41 @@ def test_convert_tq1_0_rejects_bad_arguments():
     assert L.hq_convert_tq1_0(None, 256, 4, p, p) == hq.HQ_ERR_INVALID_ARG
     assert L.hq_repack_tq1_0_device(p, 384, 4, p, p, None) == hq.HQ_ERR_SHAPE
     assert L.hq_repack_tq1_0_device(p + 4, 256, 4, p, p, None) == hq.HQ_ERR_ALIGNMENT
+
+
+# ---------------------------------------------------------------- the int8 path
+def test_int8_repack_layout_and_round_trip():
+    rng = np.random.default_rng(5)
+    K, N = 256, 37
+    w = rng.integers(-128, 128, (K, N), dtype=np.int16).astype(np.int8)
+    packed = hq.repack_int8(w)
+    assert packed.size == hq.lib().hq_int8_packed_bytes(K, N) == K * 48
+    assert np.array_equal(hq.unpack_int8(packed, K, N), w)
+    # Byte of w[k][n]: tile (n // 16, k // 128) of 2 KiB, lane 16 ((k % 64) // 16) + n % 16 of 32
+    # bytes, chunk (k % 128) // 64 of 16 bytes, element k % 16: each lane's 16 bytes are one
+    # column's consecutive k, the B operand of v_mfma_i32_16x16x64_i8 (lane: column l % 16,
+    # k-slice l / 16).
+    for k, n in [(0, 0), (5, 3), (70, 17), (255, 36), (129, 20)]:
+        off = ((n // 16) * (K // 128) + k // 128) * 2048 + (16 * ((k % 64) // 16) + n % 16) * 32 + ((k % 128) // 64) * 16 + k % 16
+        assert packed[off] == w[k, n]
+    # padding columns (37..47 of the last tile) are zero
+    pad = packed.reshape(3, 2, 64, 32)[2][:, [l for l in range(64) if l % 16 >= 5], :]
+    assert not pad.any()
+
+
+def test_int8_shapes_and_workspace():
+    L = hq.lib()
+    assert L.hq_int8_packed_bytes(100, 16) == 0 and L.hq_int8_packed_bytes(128, 0) == 0
+    b = ctypes.c_size_t(0)
+    assert L.hq_workspace_bytes_w8a8(8, 5120, 27648, ctypes.byref(b)) == hq.HQ_OK and b.value >= 8 * 5120
+    assert L.hq_workspace_bytes_w8a8(17, 5120, 512, ctypes.byref(b)) == hq.HQ_ERR_UNSUPPORTED
+    assert L.hq_workspace_bytes_w8a8(4, 5000, 512, ctypes.byref(b)) == hq.HQ_ERR_SHAPE
+    assert L.hq_workspace_bytes_w8a8(4, 262144, 512, ctypes.byref(b)) == hq.HQ_ERR_SHAPE  # int32 sum bound
+    # argument checks before any launch
+    assert L.hq_gemm_w8a8(None, 128, 0x1000, 0x2000, 0x3000, 16, 1, 128, 16, None, 0, None) == hq.HQ_ERR_INVALID_ARG
+    assert L.hq_gemm_w8a8(0x1000, 100, 0x1000, 0x2000, 0x3000, 16, 1, 128, 16, None, 0, None) == hq.HQ_ERR_SHAPE
+    assert L.hq_gemm_w8a8(0x1004, 128, 0x1000, 0x2000, 0x3000, 16, 1, 128, 16, None, 0, None) == hq.HQ_ERR_ALIGNMENT
+    assert L.hq_gemm_w8a8(0x1000, 128, 0x1000, 0x2000, 0x3000, 16, 0, 128, 16, None, 0, None) == hq.HQ_ERR_UNSUPPORTED
+    need = hq.workspace_bytes_w8a8(4, 1024, 64)
+    assert L.hq_gemm_w8a8(0x1000, 1024, 0x1000, 0x2000, 0x3000, 64, 4, 1024, 64, 0x10000, need - 1, None) == \
+        hq.HQ_ERR_WORKSPACE

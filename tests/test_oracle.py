@@ -401,3 +401,72 @@ def test_tq1_0_gemv_matches_float64_brute_force():
             d = np.uint16(O.tq1_0_scale(blocks[n, b])).view(np.float16).astype(np.float64)
             W[256 * b:256 * (b + 1), n] = d * (O.tq1_0_codes(blocks[n, b]).astype(np.float64) - 1)
     np.testing.assert_allclose(O.gemv_tq1_0(X, blocks, N), X.astype(np.float64) @ W, rtol=1e-4, atol=1e-4)
+
+
+# ---------------------------------------------------------------- the int8 path
+# kernel_cutlass_int8_gemm (hydrogen/src/model/marlin_gemm.cu:327-377): activations quantised as
+# static_cast<int8_t>(fminf(fmaxf(x * 127, -128), 127)) (:356-359), weights q * 16 - 128 (:508),
+# per-quad integer dot products accumulated as fp32 dot * (1 / 127), times scales[col] (:371-375).
+def test_quantize_x_int8_known_answers():
+    # Conversion toward zero (not rounding: 0.5 -> 63, not 64), clamping at both ends, and NaN
+    # to -128 (fmaxf returns the non-NaN operand, then fminf keeps -128).
+    cases = {1.0: 127, -1.0: -127, 0.5: 63, -0.5: -63, 1e-3: 0, -1e-3: 0, 2.0: 127, -2.0: -128, -1.01: -128,
+             1.007: 127, 0.99999: 126, float("inf"): 127, float("-inf"): -128, float("nan"): -128}
+    for x, q in cases.items():
+        assert O.quantize_x_int8(x) == q, (x, O.quantize_x_int8(x), q)
+
+
+def test_int8_from_int4_is_16q_minus_128():
+    K, N = 256, 12
+    q = dense_codes_int4(K, N)
+    w8 = O.int8_from_int4(pack_linear_int4(q).ravel(), K, N)
+    assert np.array_equal(w8.astype(np.int32), q.astype(np.int32) * 16 - 128)
+    assert w8.min() == -128 and w8.max() == 112
+
+
+def int8_problem(M, K, N, seed):
+    rng = np.random.default_rng(seed)
+    X = (rng.standard_normal((M, K)) * 0.4).astype(np.float32)
+    W = (rng.integers(0, 16, (K, N)) * 16 - 128).astype(np.int8)
+    s = (np.abs(rng.standard_normal(N)) * 0.02 + 1e-3).astype(np.float32)
+    return X, W, s
+
+
+@pytest.mark.parametrize("M,K,N", [(1, 128, 40), (5, 512, 33), (8, 4096, 64), (16, 1024, 17)])
+def test_gemm_int8_against_integer_float64(M, K, N):
+    X, W, s = int8_problem(M, K, N, M + K + N)
+    Y = O.gemm_int8(X, W, s)
+    xq = np.array([[O.quantize_x_int8(v) for v in row] for row in X], dtype=np.int64)
+    dots = xq.reshape(M, K // 4, 4, 1) * W.astype(np.int64).reshape(1, K // 4, 4, N)
+    quad = dots.sum(axis=2)                       # [M, K/4, N] exact integers
+    exact = quad.sum(axis=1) / 127.0 * s.astype(np.float64)
+    # fp32 accumulation of K / 4 terms (one rounding each) and the final product
+    bound = (K // 4 + 2) * 2.0**-24 * (np.abs(quad).sum(axis=1) / 127.0) * np.abs(s) + 1e-30
+    assert np.all(np.abs(Y - exact) <= bound)
+    # A rounding (not truncating) quantiser, or a scale row other than the first, fails this.
+    xr = np.clip(np.rint(X * 127), -128, 127).astype(np.int64)
+    alt = (xr @ W.astype(np.int64)) / 127.0 * s
+    assert not np.all(np.abs(Y - alt) <= bound)
+
+
+def test_gemm_int8_known_answers():
+    # x = 1 -> 127; every weight 16 (code 9): each quad contributes fp32(4 * 127 * 16 / 127).
+    K, N = 256, 3
+    X = np.ones((2, K), dtype=np.float32)
+    X[1, :] = 0.0
+    X[1, 7] = -1.0
+    W = np.full((K, N), 16, dtype=np.int8)
+    s = np.array([1.0, 0.5, 2.0], dtype=np.float32)
+    Y = O.gemm_int8(X, W, s)
+    # fmaf(dot, 1/127, acc) emulated exactly: the product of an integer below 2^13 and a 24-bit
+    # significand is exact in float64, and so is its sum with the fp32 accumulator.
+    acc = np.float32(0.0)
+    for _ in range(K // 4):
+        acc = np.float32(np.float64(acc) + np.float64(4 * 127 * 16) * np.float64(np.float32(1.0 / 127.0)))
+    assert np.array_equal(Y[0], acc * s)
+    # one nonzero activation: the single quad holding k = 7 gives -127 * 16 / 127 = -16 exactly
+    assert np.allclose(Y[1], np.float32(-127 * 16) * np.float32(1.0 / 127.0) * s, rtol=1e-7)
+    # thread count does not change the bits
+    X2, W2, s2 = int8_problem(3, 512, 50, 7)
+    assert np.array_equal(O.gemm_int8(X2, W2, s2, threads=1).view(np.uint32),
+                          O.gemm_int8(X2, W2, s2, threads=8).view(np.uint32))

@@ -24,7 +24,8 @@ C_TO_RUST = {
     "const void*": "*const c_void", "void*": "*mut c_void", "hq_status": "Status", "hq_format": "Format",
     "hq_dtype": "Dtype", "hq_stream": "Stream", "const hq_segment*": "*const Segment", "hq_gguf**": "*mut *mut Gguf",
     "hq_gguf*": "*mut Gguf", "const hq_gguf*": "*const Gguf", "hq_gguf_header_info*": "*mut GgufHeaderInfo",
-    "hq_gguf_tensor_info*": "*mut GgufTensorInfo", "uint64_t[4]": "[u64; 4]",
+    "hq_gguf_tensor_info*": "*mut GgufTensorInfo", "uint64_t[4]": "[u64; 4]", "const int8_t*": "*const i8",
+    "int8_t*": "*mut i8", "int64_t": "i64",
 }
 STRUCTS = {"hq_segment": "Segment", "hq_gguf_header_info": "GgufHeaderInfo", "hq_gguf_tensor_info": "GgufTensorInfo"}
 
