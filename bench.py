@@ -7,7 +7,8 @@ Workload (one "step"): the W4A16 decode sweep, group 128, fp16 activations,
 (GB/s). Every launch reads a weight copy that no launch of the previous ~640 MiB read
 (copies rotate per launch over >= 640 MiB per shape), so the 256 MiB Infinity Cache cannot
 serve them. Steps are replayed as HIP graphs, which keeps host launch cost off the GPU
-timeline; inputs are resident in HBM before the timed region.
+timeline; inputs are resident in HBM before the timed region. The default 50 warm-up steps
+bring the GPU to its steady clocks (after 5, the first timed steps ran up to 5% slower).
 
 The same JSON line also carries:
   cases         per launch shape: average launch duration (HIP events on the launch stream
@@ -32,7 +33,7 @@ The same JSON line also carries:
                 timed separately, median of 5 runs each.
 
 Usage:
-  python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--no-prefill] [--no-traffic]
+  python bench.py [--gpus 1] [--steps 100] [--warmup 50] [--no-cpu] [--no-prefill] [--no-traffic]
   python bench.py --roofline-only --case K N M  # one decode shape only (for rocprofv3 --pmc)
   python bench.py --copy-bytes 268435456        # a plain device copy of known size (counter calibration)
   python bench.py --prefill-only 2048           # W4A16 prefill M=2048, K=5120, N=27648 only (for counters)
@@ -510,8 +511,8 @@ def run_cpu(reps: int = 5):
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-traffic", action="store_true")

@@ -1006,9 +1006,12 @@ static int xr_waves_per_simd(int fmt, int T, int U) {
 // (graph-timed, weights rotated past the 256 MiB cache): 5120 x 5120 at M = 1..16 5.7-7.1 us
 // against 7.5-8.4, 27648 x 5120 at M = 1, 2 15.0-15.8 against 16.8-17.3, ternary 5120 x 27648
 // at M = 1 12.3 against 14.1. With wide weights (more tiles than two per CU) and more than
-// four rows the lockstep kernel, which streams each activation k-block through LDS instead of
-// copying all of K per workgroup up front, is as fast or faster, so the planner leaves those
-// calls to it. HQ_XR_T / _WK / _U / _S override (tuning and tests).
+// eight rows the lockstep kernel, which streams each activation k-block through LDS instead of
+// copying all of K per workgroup up front, is as fast or faster (5120 x 27648, M = 12 and 16:
+// 17.0-18.5 us against 17.7-18.8 with 8-tile slabs, the only one-round X-resident grid), so
+// the planner leaves those calls to it; at five to eight rows the 4-tile slabs still fit two
+// workgroups per CU and win (M = 5, 8: 15.5-16.3 against 16.6-17.7 us; ternary bf16 M = 8:
+// 13.5 against 15.0). HQ_XR_T / _WK / _U / _S override (tuning and tests).
 XrConfig choose_decode_xr(int fmt, const GemmDesc& d, size_t ws_cap) {
   XrConfig c{2, 3, 8, 1, 0, false};
   if (d.M > 16u || d.gen) return c;
@@ -1036,7 +1039,7 @@ XrConfig choose_decode_xr(int fmt, const GemmDesc& d, size_t ws_cap) {
       break;
     }
   }
-  if (!forced && (!found || (tiles > 2u * cus && d.M > 4u))) return c;
+  if (!forced && (!found || (tiles > 2u * cus && d.M > 8u))) return c;
   if (eT == 1 || eT == 2 || eT == 4 || eT == 8) c.T = eT;
   if (eWK >= 1) c.WK = eWK;
   if (eU >= 2) c.U = eU;

@@ -171,18 +171,50 @@ __global__ void __launch_bounds__(256 * WM, WM == 1 && RT == 8 ? 2 : 1) hq_prefi
 
   // Epilogue of a finished tile. The MFMAs take the weight fragment as their A operand and the
   // activations as B, so each 16 x 16 result is the transposed tile: lane -> activation row
-  // 16 r + c16 and the four consecutive output columns 16 (ct0 + t) + 4 g4 + v, one 8-byte
-  // store (the lanes of a row write its 128 bytes of the wavefront's 64 columns in four
-  // instructions). Rows past M fall outside the descriptor; columns past N, and outputs whose
-  // rows are not 8-byte aligned, take 2-byte stores. Only row tiles r0 <= r < r1
-  // (compile-time after unrolling).
+  // 16 r + c16 and the four consecutive output columns 16 (ct0 + t) + 4 g4 + v. When the
+  // wavefront's 64 columns lie inside N and rows are 16-byte aligned, the results go through
+  // the wavefront's own LDS area (16 RT rows x 128 bytes, 16-byte units XOR-swizzled by row)
+  // and leave as 16-byte stores, eight lanes per row: each instruction writes whole 128-byte
+  // row segments (8-byte stores straight from the MFMA layout wrote each line in four 32-byte
+  // pieces: 1.6x the output bytes in HBM writes). The area overlaps the activation stages: the
+  // caller guarantees every wavefront is done reading them. Otherwise one 8-byte store per
+  // lane, and 2-byte stores for columns past N or rows that are not 8-byte aligned. Rows past M
+  // fall outside the descriptor. Only row tiles r0 <= r < r1 (compile-time after unrolling).
   auto store_tile = [&](uint32_t s, uint32_t m0, uint32_t ct0, int r0 = 0, int r1 = RT) {
     constexpr float post = (FMT == HQ_FORMAT_TERNARY2 && DT == HQ_DTYPE_F16) ? 0.5f : 1.0f;
     const SegDesc& sg = d.seg[s];
     const uint32_t rows = min(BM, d.M - m0);
     const __amdgpu_buffer_rsrc_t yr =
         make_rsrc(reinterpret_cast<char*>(sg.Y) + (size_t)m0 * (size_t)sg.ldy * 2u, rows * (uint32_t)sg.ldy * 2u);
-    const bool wide = ((reinterpret_cast<uintptr_t>(sg.Y) | ((uint32_t)sg.ldy * 2u)) & 7u) == 0u;  // uniform
+    const uint32_t align = (uint32_t)reinterpret_cast<uintptr_t>(sg.Y) | ((uint32_t)sg.ldy * 2u);
+    if ((align & 15u) == 0u && ct0 * 16u + 64u <= sg.N) {  // uniform
+      char* const area = smem + wave * (16u * RT * 128u);
+#pragma unroll
+      for (int r = 0; r < RT; ++r) {
+        if (r < r0 || r >= r1) continue;
+        const uint32_t row = 16u * r + c16;
+#pragma unroll
+        for (int t = 0; t < kTilesPerWave; ++t) {
+          const f4 v = acc[r][t] * post;
+          const u2 packed = {(uint32_t)f32_to_out<DT>(v[0]) | ((uint32_t)f32_to_out<DT>(v[1]) << 16),
+                             (uint32_t)f32_to_out<DT>(v[2]) | ((uint32_t)f32_to_out<DT>(v[3]) << 16)};
+          const uint32_t unit = 2u * t + (g4 >> 1);
+          *reinterpret_cast<u2*>(area + row * 128u + ((unit ^ (row & 7u)) * 16u) + (g4 & 1u) * 8u) = packed;
+        }
+      }
+      // Read back in row order (this wavefront's own area: its LDS operations complete in
+      // order): lane -> row 8 i + lane / 8, columns 8 (lane % 8) .. + 7.
+      const uint32_t j = lane & 7u;
+#pragma unroll
+      for (int i = 0; i < 2 * RT; ++i) {
+        if (i < 2 * r0 || i >= 2 * r1) continue;
+        const uint32_t row = 8u * i + (lane >> 3);
+        const u4 v = *reinterpret_cast<const u4*>(area + row * 128u + ((j ^ (row & 7u)) * 16u));
+        __builtin_amdgcn_raw_buffer_store_b128(v, yr, ((wrow0 + row) * (uint32_t)sg.ldy + ct0 * 16u + 8u * j) * 2u, 0, 0);
+      }
+      return;
+    }
+    const bool wide = (align & 7u) == 0u;  // uniform
 #pragma unroll
     for (int t = 0; t < kTilesPerWave; ++t) {
       const uint32_t n0 = (ct0 + t) * 16u + 4u * g4;
@@ -376,6 +408,7 @@ __global__ void __launch_bounds__(256 * WM, WM == 1 && RT == 8 ? 2 : 1) hq_prefi
     uint32_t s, m0, ct0;
     tile_geom<BM>(d, pp.nb, tile, wn, s, m0, ct0);
     run_piece(s, m0, ct0, 0u, nkb);
+    __syncthreads();  // the output goes through the activation stages' LDS
     store_tile(s, m0, ct0);
     return;
   }

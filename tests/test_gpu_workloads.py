@@ -8,9 +8,9 @@ the tighter output-rounding bound OUT_TOL; where the oracle cost allows, the per
 
 Workloads:
   * decode sweep, int4 fp16, (K, N) in {(5120, 27648), (27648, 5120)}, M in {1, 2, 4, 8}
-    (the X-resident kernel with whole slabs at M <= 4 on 5120 x 27648 and at M <= 2 on
+    (the X-resident kernel with whole slabs at M <= 8 on 5120 x 27648 and at M <= 2 on
     27648 x 5120, with K cut in two pieces at M = 4 on 27648 x 5120, the lockstep kernel at
-    M = 8);
+    M = 8 on 27648 x 5120);
   * prefill, int4 fp16, K = 5120, N = 27648, M = 4096 (rows are independent: a random row
     subset is compared);
   * the split-fuse mixed batch, M = 1024 = 1008 prefill-chunk rows + 16 decode rows, in both
