@@ -26,7 +26,8 @@ The same JSON line also carries:
                 reads for a plain device copy of known size (null if rocprofv3 is absent);
   prefill_M2048 the metric's second half: W4A16 M=2048, K=5120, N=27648 TFLOP/s against the
                 2.5 PFLOP/s dense fp16 MFMA peak (also as roofline_prefill);
-  prefill       M in {512, 2048, 4096} and the split-fuse mixed batch (fused QKV int4, fused
+  prefill       M in {512, 2048, 4096} (each with hipBLASLt's dense fp16 GEMM on the same shape
+                for reference) and the split-fuse mixed batch (fused QKV int4, fused
                 gate||up ternary, M=1024);
   cpu_baseline  the CPU oracle (restated reference path: host dequantisation, then the fp32
                 matmul) on the host cores over the 15 decode GEMMs: dequantisation and matmul
@@ -366,7 +367,24 @@ def run_gpu(args):
                                 "frac_mfma_f16": round(tf / MFMA_F16_PEAK_TFLOPS, 4),
                                 "plan": hq.describe(FMT_INT4, 1, M, K, N, GROUP)}
             log(f"prefill M={M}: {us:.1f} us, {tf:.1f} TFLOP/s")
-            del Xp, Yp
+            # For reference, the vendor library on the same shape without quantisation: hipBLASLt's
+            # dense fp16 GEMM through torch.matmul (weights [N][K], the layout it runs fastest).
+            # Timed eagerly (back-to-back launches on one stream, HIP events), not captured.
+            Bt = torch.randn((N, K), device="cuda").to(torch.float16)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            with torch.cuda.stream(stream):
+                for _ in range(3):
+                    torch.matmul(Xp, Bt.t(), out=Yp)
+                e0.record(stream)
+                for _ in range(8):
+                    torch.matmul(Xp, Bt.t(), out=Yp)
+                e1.record(stream)
+            torch.cuda.synchronize()
+            us_d = e0.elapsed_time(e1) * 1e3 / 8
+            tf_d = 2.0 * M * K * N / (us_d * 1e-6) / 1e12
+            prefill[f"M{M}"]["dense_fp16_hipblaslt"] = {"us": round(us_d, 1), "TFLOPs": round(tf_d, 1)}
+            log(f"  dense fp16 (hipBLASLt) M={M}: {us_d:.1f} us, {tf_d:.1f} TFLOP/s")
+            del Xp, Yp, Bt
         del ws, ss
         # mixed split-fuse batch: 1008 prefill rows + 16 decode rows, fused QKV (int4) and gate||up (ternary)
         M = 1024
