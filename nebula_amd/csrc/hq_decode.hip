@@ -996,7 +996,8 @@ static int xr_waves_per_simd(int fmt, int T, int U) {
 // Tiling of the X-resident kernel. A workgroup places ceil(WK / 4) wavefronts on each SIMD,
 // so it fits on a CU as often as the register use and the LDS both allow. The planner takes
 // whole slabs (S = 1: the activation rows of all of K in LDS) and the narrowest slabs
-// (T = 2, 4 or 8 tiles) whose grid fits on the CUs in one round; only when whole slabs of up to
+// (T = 2, 4 or 8 tiles; 1 when that gives at most one workgroup per CU and fills at least half
+// of them) whose grid fits on the CUs in one round; only when whole slabs of up to
 // four rows leave more than half of the CUs idle does it cut K into pieces (S > 1) to fill
 // them. Pieces for the rows of a long K that do not fit in LDS measured slower than the
 // lockstep kernel (27648 x 5120, M = 8 and 16: 19.0 and 22.3 us against 18.2 and 20.9; each
@@ -1024,8 +1025,12 @@ XrConfig choose_decode_xr(int fmt, const GemmDesc& d, size_t ws_cap) {
   bool found = false;
   for (int s = 1; s <= 8 && !found; ++s) {
     if ((uint32_t)s > d.nkb || xr_x_bytes(d, s) > kXrLdsMax || (s > 1 && d.M > 4u)) continue;
-    for (int t : {2, 4, 8}) {
-      const int wk = t == 8 ? 4 : 8, u = t == 2 ? 3 : 2;
+    for (int t : {1, 2, 4, 8}) {
+      // One-tile slabs only when they give every CU at most one and at least half the CUs one
+      // (4096 x 4096, M = 16: 256 workgroups, 5.96 against 6.55-6.69 us with 2-tile slabs; with
+      // more tiles than CUs, 2-tile slabs measured faster: 5120 x 5120, M = 4: 6.08 against 7.14).
+      if (t == 1 && (tiles > cus || 2u * tiles <= cus || s > 1)) continue;
+      const int wk = t == 8 ? 4 : 8, u = t == 1 ? 4 : t == 2 ? 3 : 2;
       const uint32_t lds = xr_lds_bytes(d, t, wk, s);
       if (lds > kXrLdsMax) continue;
       const uint32_t by_regs = (uint32_t)(xr_waves_per_simd(fmt, t, u) / ((wk + 3) / 4));
