@@ -708,10 +708,16 @@ PrefillConfig choose_prefill(int fmt, const GemmDesc& d, size_t ws_cap) {
   // or not at all. Measured on MI355X: fused QKV (N = 7168) M = 256..1024 7-38% faster,
   // K = 27648 x N = 5120 at M = 256 17% faster; with long pieces (K = 27648, M = 1024) the
   // 128-row split stays (64-row tiles there: 40% slower).
+  const uint32_t cus = (uint32_t)cu_count();
   if (RT == 8 && WM == 1 && env_int("HQ_PREFILL_RT", 0) == 0 && env_int("HQ_PREFILL_WM", 0) == 0) {
     const uint32_t t128 = make_launch(8, 1, d).tiles, s128 = (uint32_t)prefill_slots(fmt, 8, 1);
     const uint32_t split = std::min<uint32_t>(s128 / std::max(t128, 1u), d.nkb / 4u);
-    if (split >= 2u && d.nkb / split < 64u) {
+    if (4u * t128 >= 3u * cus && 2u * t128 <= s128) {
+      // One round of 128-row tiles covering at least three quarters of the CUs: whole tiles.
+      // Measured on MI355X (K = 5120, alternated runs): fused QKV (N = 7168) M = 1024, 224
+      // tiles: 77.5 us against 82.5 with 448 64-row tiles; N = 27648 M = 256, 216 tiles: 75.9
+      // against 80.9.
+    } else if (split >= 2u && d.nkb / split < 64u) {
       RT = 4;
     } else if (split < 2u) {
       // Whole tiles either way: compare rounds, in units of a full 128-row round. A part-empty
@@ -750,7 +756,11 @@ PrefillConfig choose_prefill(int fmt, const GemmDesc& d, size_t ws_cap) {
       const size_t fit = ws_cap > kCounterBytes ? (ws_cap - kCounterBytes) / per_wg : 0u;
       if (psk > fit) psk = epsk > 0 ? (uint32_t)fit : (uint32_t)(fit / l.tiles) * l.tiles;
     }
-    if (psk > l.tiles && (psk >= 2u * l.tiles || epsk > 0)) {
+    // Stream-K only for grids that leave more than a quarter of the CUs idle: whole tiles
+    // covering three quarters of them or more measured faster (fused QKV M = 512, 224 64-row
+    // tiles: 58.2 against 66.3 us split two ways; N = 27648 M = 128, 216 tiles: 58.2 against
+    // 62.0); at 112 tiles and fewer the split still wins (QKV M = 256: 46.2 against 56.3).
+    if (psk > l.tiles && ((psk >= 2u * l.tiles && 4u * l.tiles < 3u * cus) || epsk > 0)) {
       l.psk = psk;
       l.dp = 0;
       return c;
