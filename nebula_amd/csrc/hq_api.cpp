@@ -475,8 +475,9 @@ std::string describe(int fmt, int dtype, const hq::GemmDesc& d, const Plan& p) {
                           d.gen ? ",general" : "");
     for (int i = 0; i < p.pc.n && n > 0 && (size_t)n < sizeof b; ++i) {
       const hq::PrefillLaunch& l = p.pc.l[i];
-      n += std::snprintf(b + n, sizeof b - n, "%s launch %d: %u-row tiles=%u whole=%u stream-K workgroups=%u",
-                         i ? ";" : "", i, 16u * l.RT * l.WM, l.tiles, l.dp, l.psk);
+      n += std::snprintf(b + n, sizeof b - n, "%s launch %d: %u-row tiles=%u whole=%u stream-K workgroups=%u%s",
+                         i ? ";" : "", i, 16u * l.RT * l.WM, l.tiles, l.dp, l.psk,
+                         l.KS == 2 ? " k-split in workgroup" : "");
     }
     if (n > 0 && (size_t)n < sizeof b) std::snprintf(b + n, sizeof b - n, " ws=%zu", p.need);
   }

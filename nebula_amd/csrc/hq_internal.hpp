@@ -135,6 +135,7 @@ hipError_t launch_decode_ls(int fmt, int dtype, GemmDesc d, const LsConfig& c, v
 struct PrefillLaunch {
   int RT;
   int WM;
+  int KS;  // 2: each tile's k-blocks split between two halves of one workgroup (whole tiles)
   GemmDesc d;
   uint32_t tiles;
   uint32_t dp;

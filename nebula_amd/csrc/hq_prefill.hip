@@ -124,8 +124,14 @@ __device__ __forceinline__ void tile_geom(const GemmDesc& d, uint32_t nb, uint32
 // One-row-wave 128-row tiles are held to 256 VGPRs so that two workgroups share a CU (their
 // barriers are independent, so one's dequantisation overlaps the other's MFMAs).
 // GEN: the general kernels (one scale per 32-wide k chunk, optional int4 bias), 64-row tiles.
-template <int FMT, int DT, int RT, int WM, bool SKP, bool GEN = false>
-__global__ void __launch_bounds__(256 * WM, WM == 1 && RT == 8 ? 2 : 1) hq_prefill_kernel(const GemmDesc d, const PrefillPlan pp) {
+// KS = 2 (whole 128-row tiles only): the workgroup's eight wavefronts are two halves of four,
+// each computing the tile over half of its k-blocks through its own LDS stages; the halves'
+// sums meet in LDS at the end (half 0 + half 1). A grid of one tile per CU then still keeps
+// two wavefronts on every SIMD, as two workgroups per CU do.
+template <int FMT, int DT, int RT, int WM, bool SKP, bool GEN = false, int KS = 1>
+__global__ void __launch_bounds__(256 * WM * KS, WM == 1 && RT == 8 && KS == 1 ? 2 : 1)
+    hq_prefill_kernel(const GemmDesc d, const PrefillPlan pp) {
+  static_assert(KS == 1 || (KS == 2 && !SKP && !GEN && WM == 1), "the K split is for whole fast tiles");
   constexpr uint32_t BM = 16u * RT * WM;
   constexpr uint32_t kStageBytes = BM * 256u;        // BM rows x 128 fp16
   constexpr uint32_t kPartBytes = BM * 256u * 4u;    // one fp32 partial tile
@@ -138,10 +144,13 @@ __global__ void __launch_bounds__(256 * WM, WM == 1 && RT == 8 ? 2 : 1) hq_prefi
   // store that has completed is visible to loads from any XCD.
   constexpr int kCoherent = 16;
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  uint32_t* const sh_last = reinterpret_cast<uint32_t*>(smem + 2u * kStageBytes);
+  uint32_t* const sh_last = reinterpret_cast<uint32_t*>(smem + 2u * KS * kStageBytes);
 
   const uint32_t lane = threadIdx.x & 63u;
-  const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t wave_all = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const uint32_t kh = KS > 1 ? wave_all / (4u * WM) : 0u;           // K half (KS = 2)
+  const uint32_t wave = KS > 1 ? wave_all % (4u * WM) : wave_all;    // wavefront within its half
+  char* const stages = smem + kh * 2u * kStageBytes;                 // this half's two LDS stages
   const uint32_t c16 = lane & 15u, g4 = lane >> 4;
   const uint32_t wm = wave / 4u, wn = wave % 4u;
   const uint32_t wrow0 = wm * 16u * RT;  // first tile row of this wavefront
@@ -251,7 +260,7 @@ __global__ void __launch_bounds__(256 * WM, WM == 1 && RT == 8 ? 2 : 1) hq_prefi
       const uint32_t ko = min(kb, kz - 1u) * 256u;
 #pragma unroll
       for (int i = 0; i < RT; ++i)
-        buffer_to_lds16(xr, smem + stage * kStageBytes + (wave * RT + i) * 1024u, aoff[i], ko);
+        buffer_to_lds16(xr, stages + stage * kStageBytes + (wave * RT + i) * 1024u, aoff[i], ko);
     };
     // Weights: one descriptor per column tile of this wavefront.
     __amdgpu_buffer_rsrc_t wrs[kTilesPerWave];
@@ -315,7 +324,7 @@ __global__ void __launch_bounds__(256 * WM, WM == 1 && RT == 8 ? 2 : 1) hq_prefi
       // sunk below the first use of this step's weights would be waited for with them.
       __builtin_amdgcn_sched_barrier(0);
       if (kb < kz) {  // uniform; no loads inside
-        const char* sbase = smem + (kb & 1u) * kStageBytes;
+        const char* sbase = stages + (kb & 1u) * kStageBytes;
         // Ternary: a group whose scale is not finite contributes nothing (its scale reads as 0).
         uint32_t sc[kTilesPerWave];
 #pragma unroll
@@ -407,9 +416,32 @@ __global__ void __launch_bounds__(256 * WM, WM == 1 && RT == 8 ? 2 : 1) hq_prefi
     }
     uint32_t s, m0, ct0;
     tile_geom<BM>(d, pp.nb, tile, wn, s, m0, ct0);
-    run_piece(s, m0, ct0, 0u, nkb);
-    __syncthreads();  // the output goes through the activation stages' LDS
-    store_tile(s, m0, ct0);
+    if constexpr (KS == 1) {
+      run_piece(s, m0, ct0, 0u, nkb);
+      __syncthreads();  // the output goes through the activation stages' LDS
+      store_tile(s, m0, ct0);
+    } else {
+      // Halves of equal length (nkb even, checked by the host), so both meet every barrier.
+      const uint32_t kmid = nkb / 2u;
+      run_piece(s, m0, ct0, kh ? kmid : 0u, kh ? nkb : kmid);
+      __syncthreads();  // both halves are done reading their stages
+      f4* const part = reinterpret_cast<f4*>(smem) + wave * (RT * kTilesPerWave * 64u);
+      if (kh) {
+#pragma unroll
+        for (int r = 0; r < RT; ++r)
+#pragma unroll
+          for (int t = 0; t < kTilesPerWave; ++t) part[(r * kTilesPerWave + t) * 64u + lane] = acc[r][t];
+      }
+      __syncthreads();
+      if (!kh) {
+#pragma unroll
+        for (int r = 0; r < RT; ++r)
+#pragma unroll
+          for (int t = 0; t < kTilesPerWave; ++t) acc[r][t] += part[(r * kTilesPerWave + t) * 64u + lane];
+      }
+      __syncthreads();  // every partial is read before the output reuses the LDS
+      if (!kh) store_tile(s, m0, ct0);
+    }
     return;
   }
 
@@ -507,9 +539,9 @@ __global__ void __launch_bounds__(256 * WM, WM == 1 && RT == 8 ? 2 : 1) hq_prefi
   }
 }
 
-template <int FMT, int DT, int RT, int WM>
+template <int FMT, int DT, int RT, int WM, int KS = 1>
 constexpr size_t prefill_lds() {
-  return 2u * (16u * RT * WM) * 256u + 16u;
+  return 2u * KS * (16u * RT * WM) * 256u + 16u;
 }
 
 // Whole-tile workgroups one CU holds at once (1 if the device cannot be queried).
@@ -586,6 +618,28 @@ hipError_t launch_rt(const PrefillLaunch& c, void* ws, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// Whole 128-row tiles with the K split inside the workgroup (KS = 2): one tile per workgroup.
+template <int FMT, int DT>
+hipError_t launch_ks2(const PrefillLaunch& c, hipStream_t stream) {
+  GemmDesc d = c.d;
+  PrefillPlan pp{};
+  pp.nb = assign_blocks(d);
+  if ((d.M + 127u) / 128u * pp.nb != c.tiles || c.psk != 0 || c.dp != c.tiles || d.nkb % 2u != 0 || d.nkb < 2u)
+    return hipErrorInvalidValue;
+  pp.dp = c.dp;
+  pp.xcd = c.dp % 8u == 0u ? 1u : 0u;
+  pp.bands = (d.M + 127u) / 128u;
+  pp.gb = (uint32_t)std::max(1, env_int("HQ_PREFILL_GB", 4));
+  pp.nkb_m = plan_div_magic(d.nkb);
+  const size_t lds = prefill_lds<FMT, DT, 8, 1, 2>();
+  static const hipError_t attr =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&hq_prefill_kernel<FMT, DT, 8, 1, false, false, 2>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (attr != hipSuccess) return attr;
+  hipLaunchKernelGGL((hq_prefill_kernel<FMT, DT, 8, 1, false, false, 2>), dim3(c.dp), dim3(512), lds, stream, d, pp);
+  return hipGetLastError();
+}
+
 int env_int(const char* name, int dflt) {
   const char* v = std::getenv(name);
   return v && *v ? std::atoi(v) : dflt;
@@ -636,6 +690,7 @@ int prefill_slots(int fmt, int RT, int WM) {
 template <int FMT, int DT>
 hipError_t launch_fd(const PrefillLaunch& c, void* ws, hipStream_t stream) {
   if (c.d.gen) return c.RT == 4 && c.WM == 1 ? launch_rt<FMT, DT, 4, 1, true>(c, ws, stream) : hipErrorInvalidConfiguration;
+  if (c.KS == 2) return c.RT == 8 && c.WM == 1 ? launch_ks2<FMT, DT>(c, stream) : hipErrorInvalidConfiguration;
   if (c.RT == 4) return launch_rt<FMT, DT, 4, 1>(c, ws, stream);
   if (c.RT == 16) return launch_rt<FMT, DT, 16, 1>(c, ws, stream);
   if (c.WM == 1) return launch_rt<FMT, DT, 8, 1>(c, ws, stream);
@@ -678,6 +733,7 @@ PrefillLaunch make_launch(int RT, int WM, const GemmDesc& d) {
   PrefillLaunch l{};
   l.RT = RT;
   l.WM = WM;
+  l.KS = 1;
   l.d = d;
   l.tiles = (d.M + 16u * RT * WM - 1) / (16u * RT * WM) * count_blocks(d);
   l.dp = l.tiles;
@@ -744,6 +800,15 @@ PrefillConfig choose_prefill(int fmt, const GemmDesc& d, size_t ws_cap) {
   c.n = 1;
   c.l[0] = make_launch(RT, WM, d);
   PrefillLaunch& l = c.l[0];
+  // One round of whole 128-row tiles, at most one per CU and at least three quarters of them:
+  // the K split inside the workgroup (KS = 2) keeps two wavefronts on every SIMD.
+  // HQ_PREFILL_KS = 1 turns it off, = 2 forces it for any whole-tile fast call (tests).
+  const int eks = env_int("HQ_PREFILL_KS", 0);
+  if (RT == 8 && WM == 1 && !d.gen && d.nkb % 2u == 0u && d.nkb >= 8u && eks != 1 &&
+      (eks == 2 || (l.tiles <= cus && 4u * l.tiles >= 3u * cus))) {
+    l.KS = 2;
+    return c;
+  }
   const uint32_t slots = (uint32_t)prefill_slots(fmt, RT, WM);
   const int epsk = env_int("HQ_PREFILL_PSK", 0);  // tuning / test override: stream-K grid
   if (env_int("HQ_PREFILL_SK", 1) != 0 && d.nkb >= 8u && l.tiles <= kMaxCounters &&

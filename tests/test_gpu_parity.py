@@ -669,6 +669,54 @@ def test_prefill_tail_equals_whole_tiles(cuda, fmt, xdt, M, Ns):
         assert err <= OUT_TOL[xdt]
 
 
+# The K split inside the workgroup (KS=2: two halves of four wavefronts, each over half of the
+# tile's k-blocks, summed in LDS) against whole tiles without it: the same values up to fp32
+# summation order, bit-reproducible, and the oracle's. Forced on grids of several rounds,
+# ragged M and N, fused segments, every format and dtype; by default it takes one-round grids
+# of 128-row tiles covering at least three quarters of the CUs (fused QKV at M = 1024).
+@pytest.mark.parametrize("fmt,xdt,M,K,N", [
+    (O.INT4, O.F16, 300, 2048, 1000),
+    (O.INT4, O.BF16, 129, 1024, 4000),
+    (O.TERNARY2, O.F16, 200, 4096, 700),
+    (O.TERNARY2, O.BF16, 1000, 1024, 2600),
+    (O.INT4, O.F16, 2048, 5120, 27648),
+])
+def test_prefill_k_split_in_workgroup(cuda, fmt, xdt, M, K, N):
+    P = O.Problem(fmt, M, K, N, 128, xdt, seed=2750 + M)
+    D = DeviceProblem(P)
+    with prefill_env(KS=2, WM=1, SK=0, TAIL=0):  # 128-row tiles (small grids would take 64)
+        assert "k-split in workgroup" in hq.describe(fmt, xdt, M, K, N)
+        y = D.run()
+        assert torch_equal(y, D.run())
+    with prefill_env(KS=1, WM=1, SK=0, TAIL=0):
+        y1 = D.run()
+    tol = 2 * (2.0**-11 if xdt == O.F16 else 2.0**-8)
+    assert normwise_between(y, y1) <= tol
+    if M * K * N <= 4e9:
+        check(y, P.reference(), xdt, f"k-split fmt={fmt} M={M} K={K} N={N}", P)
+    else:
+        rows = np.sort(np.random.default_rng(M).choice(M, size=16, replace=False))
+        assert O.normwise_error(to_host_f32(y)[rows], P.reference(rows=rows, threads=16)) <= OUT_TOL[xdt]
+
+
+def test_prefill_k_split_fused_default_plan(cuda):
+    # Fused QKV shape of the split-fuse step (M = 1024, N = 5120 | 1024 | 1024): 224 tiles take
+    # the K split by default (on a 256-CU part).
+    Ns, K, M = [5120, 1024, 1024], 5120, 1024
+    probs = [O.Problem(O.INT4, M, K, n, 128, O.F16, seed=2760 + i) for i, n in enumerate(Ns)]
+    for p in probs[1:]:
+        p.X = probs[0].X
+    devs = [DeviceProblem(p) for p in probs]
+    segs = [(d.Wp, d.S, d.P.N) for d in devs]
+    outs = hq.gemm_fused(O.INT4, devs[0].X, segs)
+    with prefill_env(KS=1, SK=0, TAIL=0):
+        ref_outs = hq.gemm_fused(O.INT4, devs[0].X, segs)
+    rows = np.sort(np.random.default_rng(5).choice(M, size=12, replace=False))
+    for d, y, y1 in zip(devs, outs, ref_outs):
+        assert normwise_between(y, y1) <= 2 * 2.0**-11
+        assert O.normwise_error(to_host_f32(y)[rows], d.P.reference(rows=rows, threads=16)) <= OUT_TOL[O.F16]
+
+
 # Forced stream-K grids on 15 tiles of 64 rows x 256 columns, K = 1024 (8 k-blocks):
 # 16 workgroups give ranges of 8 units aligned to tiles (whole-tile pieces inside the
 # stream-K part), 17 and 40 give ranges that straddle tiles, 119 gives 1-unit ranges.
