@@ -235,6 +235,40 @@ pub unsafe fn gemm_fused_noalloc(x: *const c_void, dtype: Dtype, ldx: i64, fmt: 
     check(hq_gemm_fused_noalloc(x, dtype, ldx, fmt, segs.as_ptr(), segs.len() as u32, m, k, group, stream))
 }
 
+/// Host repack of int8 weights [K][N] (the reference's forward_cutlass_int8 operand,
+/// marlin_gemm.hpp:112-118) into the gfx950 i8 tile layout.
+pub fn repack_int8(w_kn: &[i8], k: u32, n: u32) -> Result<Vec<i8>, QgemmError> {
+    // SAFETY: a pure size query.
+    let bytes = unsafe { hq_int8_packed_bytes(k, n) };
+    if bytes == 0 || w_kn.len() != k as usize * n as usize {
+        return Err(QgemmError { status: 2, message: format!("int8 weight of {} bytes, K={k} N={n}", w_kn.len()) });
+    }
+    let mut out = vec![0i8; bytes];
+    // SAFETY: `w_kn` holds K * N bytes and `out` the packed size the library writes.
+    check(unsafe { hq_repack_int8(w_kn.as_ptr(), k, n, out.as_mut_ptr()) })?;
+    Ok(out)
+}
+
+/// Workspace bytes of one int8 call (the quantised activations and K-piece partial sums).
+pub fn workspace_bytes_w8a8(m: u32, k: u32, n: u32) -> Result<usize, QgemmError> {
+    let mut bytes = 0usize;
+    // SAFETY: `bytes` is a valid out pointer.
+    check(unsafe { hq_workspace_bytes_w8a8(m, k, n, &mut bytes) })?;
+    Ok(bytes)
+}
+
+/// The int8 forward (replaces forward_cutlass_int8, marlin_gemm.cu:603-617): fp32 activations
+/// quantised to int8, exact int32 sums, y = scale * sum / 127. `workspace`: null/0 (the library
+/// allocates on first use) or at least workspace_bytes_w8a8 bytes (zero-filled once).
+/// # Safety
+/// The device buffers must have the sizes M, K, N, ldx and ldy imply and stay alive until
+/// `stream` has executed the call.
+pub unsafe fn gemm_w8a8(x: *const f32, ldx: i64, wp: *const i8, scales: *const f32, y: *mut f32, ldy: i64, m: u32,
+                        k: u32, n: u32, workspace: *mut c_void, workspace_bytes: usize, stream: Stream)
+                        -> Result<(), QgemmError> {
+    check(hq_gemm_w8a8(x, ldx, wp, scales, y, ldy, m, k, n, workspace, workspace_bytes, stream))
+}
+
 /// An open GGUF file (replaces hydrogen::ModelLoader for the weights of this path).
 pub struct GgufFile {
     g: *mut Gguf,
