@@ -31,10 +31,13 @@ The same JSON line also carries:
                 gate||up ternary, M=1024);
   cpu_baseline  the CPU oracle (restated reference path: host dequantisation, then the fp32
                 matmul) on the host cores over the 15 decode GEMMs: dequantisation and matmul
-                timed separately, median of 5 runs each.
+                timed separately, median of 5 runs each;
+  stream_ceiling the practical read ceiling of each decode launch size on this device (the
+                fastest plain streaming read of those bytes, nebula_amd/bin/hq_stream_ceiling,
+                launch cost included) and the sweep's rate at that ceiling.
 
 Usage:
-  python bench.py [--gpus 1] [--steps 100] [--warmup 50] [--no-cpu] [--no-prefill] [--no-traffic]
+  python bench.py [--gpus 1] [--steps 100] [--warmup 50] [--no-cpu] [--no-prefill] [--no-traffic] [--no-ceiling]
   python bench.py --roofline-only --case K N M  # one decode shape only (for rocprofv3 --pmc)
   python bench.py --copy-bytes 268435456        # a plain device copy of known size (counter calibration)
   python bench.py --prefill-only 2048           # W4A16 prefill M=2048, K=5120, N=27648 only (for counters)
@@ -222,6 +225,34 @@ def measure_traffic(K: int, N: int, M: int, kernel: str):
         return None, f"traffic not measured: {e}"
     finally:
         shutil.rmtree(out, ignore_errors=True)
+
+
+# ---------------------------------------------------------------- stream ceiling
+STREAM_TOOL = ROOT / "nebula_amd" / "bin" / "hq_stream_ceiling"
+
+
+def stream_ceiling(value: float):
+    """The practical read ceiling of each decode launch size on this device, measured in this
+    run by nebula_amd/bin/hq_stream_ceiling (the fastest of several launch shapes of a kernel
+    that only reads the bytes once, HIP-graph timed over rotating buffers), and the decode
+    sweep's rate if every launch ran at that ceiling."""
+    if not STREAM_TOOL.exists():
+        return {"note": f"{STREAM_TOOL.relative_to(ROOT)} not built (run __graft_entry__.build())"}
+    sizes = sorted({wbytes(K, N) for K, N in SHAPES})
+    p = subprocess.run(["timeout", "-k", "10", "120", str(STREAM_TOOL), *map(str, sizes)], capture_output=True, text=True)
+    if p.returncode != 0:
+        return {"note": f"hq_stream_ceiling exited {p.returncode}: {p.stderr[-300:]}"}
+    res = json.loads(p.stdout)
+    per = {str(s["bytes"]): {"us": round(s["us"], 3), "GBps": round(s["GBps"], 1),
+                             "workgroups_per_cu": s["workgroups_per_cu"], "unroll": s["unroll"]} for s in res["sizes"]}
+    step_us = sum(per[str(wbytes(K, N))]["us"] for K, N in SHAPES for _ in MS)
+    step_bytes = sum(wbytes(K, N) for K, N in SHAPES for _ in MS)
+    sweep = step_bytes / step_us / 1e3
+    log(f"stream ceiling: {per}; sweep at the ceiling {sweep:.1f} GB/s ({100 * sweep / HBM_PEAK_GBS:.1f}% of peak)")
+    return {"per_launch": per, "sweep_GBps": round(sweep, 1), "sweep_frac_hbm": round(sweep / HBM_PEAK_GBS, 3),
+            "value_over_ceiling": round(value / sweep, 3),
+            "note": "per decode launch size: the fastest plain read of those bytes (grid-stride 16-byte loads, "
+                    "1-8 workgroups of 256 threads per CU, unroll 2-8), launch cost included"}
 
 
 # ---------------------------------------------------------------- the GPU run
@@ -560,6 +591,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-traffic", action="store_true")
+    ap.add_argument("--no-ceiling", action="store_true")
     ap.add_argument("--cpu-reps", type=int, default=5)
     ap.add_argument("--roofline-only", action="store_true")
     ap.add_argument("--case", type=int, nargs=3, default=[5120, 27648, 16], metavar=("K", "N", "M"))
@@ -583,6 +615,7 @@ def main():
             run_case_only(torch, hq, *args.case)
         return
     value, ms_per_step, roofline, cases, prefill, tq1, layer_res = run_gpu(args)
+    ceiling = None if args.no_ceiling else stream_ceiling(value)
     if not args.no_traffic:
         K, N, M = (int(x[1:]) for x in roofline["traffic_case"].split("_"))
         roofline["traffic"], roofline["traffic_note"] = measure_traffic(K, N, M, roofline["kernel"])
@@ -607,6 +640,7 @@ def main():
                    "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 1)},
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "stream_ceiling": ceiling,
     }
     if prefill:
         p = prefill["M2048"]

@@ -20,6 +20,7 @@ LIBDIR = PKG / "lib"
 LIB = LIBDIR / "libnebula_hq.so"
 BINDIR = PKG / "bin"
 BENCH_TOOL = BINDIR / "hq_bench_qgemm"
+STREAM_TOOL = BINDIR / "hq_stream_ceiling"
 ORACLE_DIR = ROOT / "oracle"
 
 SOURCES = ["hq_api.cpp", "hq_gguf.cpp", "hq_decode.hip", "hq_decode_ls.hip", "hq_prefill.hip", "hq_repack.hip", "hq_int8.hip"]
@@ -85,12 +86,16 @@ def build_library(verbose: bool = False) -> Path:
 
 
 def build_tools() -> Path:
-    """The BENCH-compatible benchmark executable (links the library through its C ABI)."""
+    """The BENCH-compatible benchmark executable (links the library through its C ABI) and
+    the stream-ceiling probe that bench.py runs beside the decode sweep."""
     BINDIR.mkdir(exist_ok=True)
     tmp = BENCH_TOOL.with_suffix(".tmp")
     _run([HIPCC, "-x", "hip", *COMMON_FLAGS, str(PKG / "tools" / "hq_bench_qgemm.cpp"), "-o", str(tmp),
           f"-L{LIBDIR}", "-lnebula_hq", "-Wl,-rpath,$ORIGIN/../lib"])
     os.replace(tmp, BENCH_TOOL)
+    tmp = STREAM_TOOL.with_suffix(".tmp")
+    _run([HIPCC, "-x", "hip", *COMMON_FLAGS, str(PKG / "tools" / "hq_stream_ceiling.hip"), "-o", str(tmp)])
+    os.replace(tmp, STREAM_TOOL)
     return BENCH_TOOL
 
 
