@@ -29,8 +29,10 @@
 // Weights are dequantised in registers straight into v_mfma_f32_16x16x32 B fragments:
 // int4 in the biased form magic + q (one v_and_or_b32 per fragment word), with the bias
 // removed by a correction MFMA that seeds every tile's k-block sum; the fp16 group scale
-// multiplies the fp32 k-block sum. Pieces of a split slab are summed in piece order by
-// the last workgroup to finish (arrival counter), so results are deterministic.
+// multiplies the fp32 k-block sum (int4 with several fp16 row tiles: exact q - 8 instead of
+// the correction; at five row tiles the scale is folded into the fragment). Pieces of a
+// split slab are summed in piece order by the last workgroup to finish (arrival counter),
+// so results are deterministic.
 //
 // General kernels (GEN): one scale per 32-wide k chunk (groups that are multiples of 32, not
 // of 128) and an optional fp32 per-group bias, the reference's w = q * s + b
@@ -150,6 +152,20 @@ __global__ void __launch_bounds__(64 * KG * GW, KG == 1 && MT > 1 ? 2 : 1)
   // 27648 x 5120, M = 24..80): 5-11% faster. One row tile keeps the biased form (fewer VALU
   // instructions in the memory-bound case); bf16 has no packed add on gfx950.
   constexpr bool kUnbiased = kInt4 && DT == HQ_DTYPE_F16 && MT > 1;
+  // Five row tiles of int4 with fp16 activations: the group scale is folded into the
+  // dequantised fragment (one v_pk_mul_f16 per fragment word; (q - 8) s rounds to fp16, as in
+  // the prefill kernel), so the MFMAs accumulate straight into the result across k-blocks and
+  // the per-k-block sums (40 VGPRs) that would not fit beside the fragments are not needed.
+  // Measured on MI355X (5120 x 27648, M = 80): 36.2 -> 35.0 us. With fewer row tiles, or
+  // ternary weights, scaling each k-block's sums in fp32 measured as fast or faster (one
+  // v_pk_mul_f16 per fragment word against MT x T x 4 FMAs per k-block).
+  constexpr bool kFold = !GEN && DT == HQ_DTYPE_F16 && kInt4 && MT == 5;
+  // Several row tiles: every A fragment of a k-block is read before the first wait, and the
+  // weight fragments are dequantised while those reads are in flight (a wait per row tile
+  // left the LDS latency exposed MT times per step). Measured on MI355X: ternary 5120 x 34816
+  // at M = 80 61.4 -> 52.9 us, 5120 x 14336 31.6 -> 28.6 us. Not for int4 bf16 at five row
+  // tiles, whose correction chains would not fit in 256 VGPRs beside the fragments.
+  constexpr bool kAllA = !GEN && MT > 1 && (kFold || !kInt4 || MT <= 4);
   // The register ring holds U steps in flight plus the one being consumed. Activations
   // are staged through two LDS stages: a stage is written just before the barrier of its
   // step and rewritten two steps later, after every wavefront has passed the next barrier
@@ -286,6 +302,88 @@ __global__ void __launch_bounds__(64 * KG * GW, KG == 1 && MT > 1 ? 2 : 1)
   const u4 ones = u4{one2, one2, one2, one2};
   const bool has_bias = GEN && sB != nullptr;
 
+  // Several row tiles (kAllA): the k-block's A fragments, read at once.
+  auto compute_all = [&](int slot, uint32_t stage) {
+    if constexpr (kAllA) {
+      const uint32_t so = stage * kStep;
+      u4 xa[MT][4];
+#pragma unroll
+      for (int r = 0; r < MT; ++r)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) xa[r][c] = ls_lds_read_b128(xro[c] + so + (uint32_t)r * kStageBytes);
+      uint32_t sbt[T];
+#pragma unroll
+      for (int t = 0; t < T; ++t) sbt[t] = T == 1 ? sring[slot][0] : ls_bpermute((16u * t + c16) * 4u, sring[slot][0]);
+      // Dequantisation (VALU) while the LDS reads are in flight.
+      u4 bq[4][T];
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+          if constexpr (kInt4) {
+            bq[c][t] = dq_int4_biased<DT>(wring[slot][t][c], dqb);
+            if constexpr (kUnbiased) bq[c][t] = unbias_f16(bq[c][t]);
+          } else {
+            const uint32_t word = wring[slot][t][c >> 1];
+            bq[c][t] = (c & 1) ? dq_tern2<1>(word) : dq_tern2<0>(word);
+          }
+        }
+      ls_wait_lgkmcnt0();
+#pragma unroll
+      for (int r = 0; r < MT; ++r)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) ls_tie(xa[r][c]);
+#pragma unroll
+      for (int t = 0; t < T; ++t) ls_tie(sbt[t]);
+      if constexpr (kFold) {
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+          const uint32_t s = sbt[t] & 0xFFFFu;
+          const h2 s2 = bits_h2(s | (s << 16));
+#pragma unroll
+          for (int c = 0; c < 4; ++c)
+            bq[c][t] = u4{h2_bits(bits_h2(bq[c][t][0]) * s2), h2_bits(bits_h2(bq[c][t][1]) * s2),
+                          h2_bits(bits_h2(bq[c][t][2]) * s2), h2_bits(bits_h2(bq[c][t][3]) * s2)};
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+          for (int r = 0; r < MT; ++r)
+#pragma unroll
+            for (int t = 0; t < T; ++t) acc[r][t] = mfma16x16x32<DT>(xa[r][c], bq[c][t], acc[r][t]);
+      } else {
+        float scf[T];
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+          scf[t] = f16_to_f32((uint16_t)sbt[t]);
+          if constexpr (!kInt4) scf[t] = __builtin_isfinite(scf[t]) ? 0.5f * scf[t] : 0.0f;  // fields hold 2t
+        }
+        f4 corr[MT], gs[MT][T];
+#pragma unroll
+        for (int r = 0; r < MT; ++r) {
+          corr[r] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int t = 0; t < T; ++t) gs[r][t] = f4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+          for (int r = 0; r < MT; ++r) {
+            if constexpr (kInt4 && !kUnbiased) corr[r] = mfma16x16x32<DT>(xa[r][c], corr_b, corr[r]);
+#pragma unroll
+            for (int t = 0; t < T; ++t) gs[r][t] = mfma16x16x32<DT>(xa[r][c], bq[c][t], gs[r][t]);
+          }
+#pragma unroll
+        for (int r = 0; r < MT; ++r)
+#pragma unroll
+          for (int t = 0; t < T; ++t)
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+              acc[r][t][v] =
+                  __builtin_fmaf(kInt4 && !kUnbiased ? gs[r][t][v] + corr[r][v] : gs[r][t][v], scf[t], acc[r][t][v]);
+      }
+    }
+  };
   auto compute = [&](int slot, uint32_t stage) {
     const uint32_t so = stage * kStep;
     uint32_t sb[T];
@@ -448,7 +546,8 @@ __global__ void __launch_bounds__(64 * KG * GW, KG == 1 && MT > 1 ? 2 : 1)
 #pragma unroll
         for (int x = 0; x < XL; ++x) ls_lds_write_b128(xwo[x] + st * kStep, xring[s][x]);
         kgroup_barrier();  // every wavefront's activation rows of step i + s are in LDS
-        compute(s, st);
+        if constexpr (kAllA) compute_all(s, st);
+        else compute(s, st);
         st ^= 1u;
       }
     }
