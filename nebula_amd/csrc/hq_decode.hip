@@ -1036,7 +1036,12 @@ XrConfig choose_decode_xr(int fmt, const GemmDesc& d, size_t ws_cap) {
       const uint32_t by_regs = (uint32_t)(xr_waves_per_simd(fmt, t, u) / ((wk + 3) / 4));
       const uint32_t per_cu = std::min(by_regs, kXrLdsMax / lds);
       const uint32_t wgs = total_slabs(d, t) * (uint32_t)s;
-      if (per_cu < 1 || wgs > cus * per_cu) continue;
+      // 4-tile slabs up to one and a half rounds beat 8-tile slabs of four wavefronts in one
+      // round. Measured on MI355X (M = 1..8): ternary 5120 x 34816 20.0 -> 16.0 us at M = 1,
+      // int4 4096 x 40960 22.8 -> 17.4 us; at 1.7 rounds (5120 x 55296) 8-tile slabs stay
+      // ahead from M = 4.
+      const bool t4_spill = t == 4 && 2u * wgs <= 3u * cus * per_cu;
+      if (per_cu < 1 || (wgs > cus * per_cu && !t4_spill)) continue;
       // Whole slabs leaving more than half of the CUs idle: try a split first.
       if (s == 1 && wgs * 2u < cus && total_slabs(d, t) * 2u <= cus * per_cu && d.nkb >= 2 && d.M <= 4u) break;
       c = XrConfig{t, u, wk, s, lds, false};
