@@ -467,9 +467,9 @@ std::string describe(int fmt, int dtype, const hq::GemmDesc& d, const Plan& p) {
   } else if (p.kind == Kind::kLockstep) {
     std::snprintf(b, sizeof b,
                   "hq_decode_ls_kernel<%s,%s,KG=%d,GW=%d,T=%d,U=%d,MT=%d%s> grid=%d pieces x slabs of %d tiles, "
-                  "%d wavefronts ws=%zu",
+                  "%d wavefronts%s ws=%zu",
                   fmt_name(fmt), dt_name(dtype), p.lc.KG, p.lc.GW, p.lc.T, p.lc.U, p.lc.MT, d.gen ? ",general" : "",
-                  p.lc.S, p.lc.SW, p.lc.KG * p.lc.GW, p.need);
+                  p.lc.S, p.lc.SW, p.lc.KG * p.lc.GW, p.lc.P > 0 ? " balanced grid" : "", p.need);
   } else {
     int n = std::snprintf(b, sizeof b, "hq_prefill_kernel<%s,%s%s>", fmt_name(fmt), dt_name(dtype),
                           d.gen ? ",general" : "");

@@ -135,9 +135,10 @@ __device__ __forceinline__ void ls_tie(u4& a) { asm volatile("" : "+v"(a)); }
 __device__ __forceinline__ void ls_tie(u2& a) { asm volatile("" : "+v"(a)); }
 __device__ __forceinline__ void ls_tie(uint32_t& a) { asm volatile("" : "+v"(a)); }
 
-template <int FMT, int DT, int KG, int GW, int T, int U, int MT, bool FUSED, bool GEN>
+template <int FMT, int DT, int KG, int GW, int T, int U, int MT, bool FUSED, bool GEN, bool BAL = false>
 __global__ void __launch_bounds__(64 * KG * GW, KG == 1 && MT > 1 ? 2 : 1)
     hq_decode_ls_kernel(const GemmDesc d, const LsPlan pl) {
+  static_assert(!BAL || (KG > 1 && MT > 1 && !GEN), "the balanced grid is for fast kernels with several row tiles");
   static_assert(KG == 1 || KG == 2 || KG == 4, "one, two or four k-groups");
   static_assert(GW == 2 || GW == 4, "k-groups of two or four wavefronts");
   static_assert(T >= 1 && T <= 4, "the scale load covers at most four tiles");
@@ -180,6 +181,7 @@ __global__ void __launch_bounds__(64 * KG * GW, KG == 1 && MT > 1 ? 2 : 1)
   static_assert((KG - 1) * GW * T * MT * 1024 <= NS * kStep, "the k-group reduction reuses the activation stages");
   __shared__ __attribute__((aligned(16))) char xs[NS * kStep];
   __shared__ uint32_t sh_last;
+  __shared__ uint32_t sh_tail[2];  // balanced grid: last contributor of the first / last slab
   __shared__ uint32_t kg_arrived[KG];  // per k-group arrival count (k-group barrier)
 
   const uint32_t lane = threadIdx.x & 63u;
@@ -188,7 +190,21 @@ __global__ void __launch_bounds__(64 * KG * GW, KG == 1 && MT > 1 ? 2 : 1)
   const uint32_t c16 = lane & 15u, g4 = lane >> 4;
   const uint32_t nkb = d.nkb;
   const uint32_t M = d.M;
-  const uint32_t piece = blockIdx.x, g = blockIdx.y;  // grid (S, G)
+  const uint32_t piece = BAL ? 0u : blockIdx.x;  // grid (S, G); balanced grid (P)
+  // Pieces of this workgroup. S-piece grid: one, slab blockIdx.y, k-blocks of piece blockIdx.x.
+  // Balanced grid: the slabs gfirst .. glast of the units [u0, u1), in order; the first and the
+  // last may be partial (workspace slots 0 and 1), summed by the last contributor to arrive.
+  uint32_t u0 = 0, u1 = 0, gfirst = 0, glast = 0, npieces = 1;
+  if constexpr (BAL) {
+    u0 = plan_begin(pl.bL, pl.brem, blockIdx.x);
+    u1 = plan_begin(pl.bL, pl.brem, blockIdx.x + 1u);
+    gfirst = plan_div(u0, nkb, pl.nkb_m);
+    glast = plan_div(u1 - 1u, nkb, pl.nkb_m);
+    npieces = glast - gfirst + 1u;
+  }
+  uint32_t arrivals = 0;  // k-group barrier count, across pieces
+  for (uint32_t pi = 0; pi < npieces; ++pi) {
+  const uint32_t g = BAL ? gfirst + pi : blockIdx.y;
 
   // Segment of slab g, and its fields, read once (a reference into the kernel arguments
   // would be re-read from memory inside the loop). A one-segment call (FUSED = false) reads
@@ -222,8 +238,8 @@ __global__ void __launch_bounds__(64 * KG * GW, KG == 1 && MT > 1 ? 2 : 1)
   const uint32_t ntw = ctw < sNt ? min(own, sNt - ctw) : 0u;
   const uint32_t srow2 = sLds * 2u;  // bytes per scale row
   // k-blocks [ka, kz) of this piece; at step q k-group kg takes k-block ka + q * KG + kg.
-  const uint32_t ka = piece * pl.kq + min(piece, pl.kr);
-  const uint32_t kz = ka + pl.kq + (piece < pl.kr ? 1u : 0u);
+  const uint32_t ka = !BAL ? piece * pl.kq + min(piece, pl.kr) : (pi == 0u ? u0 - gfirst * nkb : 0u);
+  const uint32_t kz = !BAL ? ka + pl.kq + (piece < pl.kr ? 1u : 0u) : (g == glast ? u1 - glast * nkb : nkb);
 
   // Weights: tile t of this wavefront at t * nkb blocks; missing tiles read zero.
   const __amdgpu_buffer_rsrc_t wr =
@@ -498,10 +514,11 @@ __global__ void __launch_bounds__(64 * KG * GW, KG == 1 && MT > 1 ? 2 : 1)
   const uint32_t arr = (uint32_t)(uintptr_t)&kg_arrived[kg];
   const uint32_t arr_next = (uint32_t)(uintptr_t)&kg_arrived[(kg + 1u) % KG];
   if constexpr (KG > 1) {
-    if (threadIdx.x < (uint32_t)KG) kg_arrived[threadIdx.x] = 0;
-    __syncthreads();
+    if (pi == 0u) {  // uniform
+      if (threadIdx.x < (uint32_t)KG) kg_arrived[threadIdx.x] = 0;
+      __syncthreads();
+    }
   }
-  uint32_t arrivals = 0;
   auto kgroup_barrier = [&]() {
     if constexpr (KG == 1) {
       ls_wait_lgkmcnt0();
@@ -609,6 +626,32 @@ __global__ void __launch_bounds__(64 * KG * GW, KG == 1 && MT > 1 ? 2 : 1)
       }
     }
   };
+  constexpr uint32_t kTilesWg = GW * T * MT;  // 16 x 16 fp32 tiles per workgroup
+  if constexpr (BAL) {
+    // Whole slab: store. Partial (first or last slab of the range): publish the partial
+    // tile to slot 0 (first) or 1 (last) with agent-coherent stores; the arrival count
+    // follows after the last piece.
+    if (ka == 0u && kz == nkb) {
+      if (lead) {
+#pragma unroll
+        for (int r = 0; r < MT; ++r) store_out(r, acc[r]);
+      }
+    } else if (lead) {
+      const uint32_t slot = pi == 0u ? 0u : 1u;
+      const __amdgpu_buffer_rsrc_t bpart = make_rsrc(pl.part, gridDim.x * 2u * kTilesWg * 1024u);
+#pragma unroll
+      for (int r = 0; r < MT; ++r)
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+          const uint32_t o = 16u * r + 4u * g4 < M
+                                 ? (((blockIdx.x * 2u + slot) * kTilesWg + (wi * T + t) * MT + r) * 64u + lane) * 16u
+                                 : kOutOfRange;
+          __builtin_amdgcn_raw_buffer_store_b128(acc[r][t], bpart, o, 0, 16);
+        }
+    }
+    __syncthreads();  // this piece's LDS stages and reduction area are free for the next piece
+    continue;
+  }
   if (pl.S == 1) {
     if (lead) {
 #pragma unroll
@@ -622,7 +665,6 @@ __global__ void __launch_bounds__(64 * KG * GW, KG == 1 && MT > 1 ? 2 : 1)
   // order. Waiting for the stores before the barrier orders them before the count.
   constexpr int kCoherent = 16;
   const uint32_t pieces = pl.S;
-  constexpr uint32_t kTilesWg = GW * T * MT;  // 16 x 16 fp32 tiles per workgroup
   const __amdgpu_buffer_rsrc_t partr = make_rsrc(pl.part, gridDim.y * pieces * kTilesWg * 1024u);
   auto part_off = [&](uint32_t p, int r, int t) {
     return 16u * r + 4u * g4 < M ? (((g * pieces + p) * kTilesWg + (wi * T + t) * MT + r) * 64u + lane) * 16u
@@ -668,6 +710,85 @@ __global__ void __launch_bounds__(64 * KG * GW, KG == 1 && MT > 1 ? 2 : 1)
     }
     store_out(r, sum);
   }
+  }  // pieces
+
+  if constexpr (BAL) {
+    // Partial first / last slabs: count this workgroup's arrival at each; the last of a slab's
+    // (at most two) contributors sums their partials in workgroup order and stores the slab.
+    const uint32_t pfirst = u0 != gfirst * nkb || (glast == gfirst && u1 != (gfirst + 1u) * nkb) ? 1u : 0u;
+    const uint32_t plast = glast != gfirst && u1 != (glast + 1u) * nkb ? 1u : 0u;
+    if (!(pfirst | plast)) return;  // uniform
+    constexpr uint32_t kTiles = GW * T * MT;
+    const __amdgpu_buffer_rsrc_t bpart = make_rsrc(pl.part, gridDim.x * 2u * kTiles * 1024u);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));  // the partial stores have completed
+    __syncthreads();
+    if (threadIdx.x < 2u) {
+      const uint32_t i = threadIdx.x;
+      uint32_t last = 0;
+      if (i == 0u ? pfirst : plast) {
+        const uint32_t gs = i == 0u ? gfirst : glast;
+        const uint32_t bf = plan_wg_of_unit(pl.bL, pl.brem, gs * nkb);
+        const uint32_t bl = plan_wg_of_unit(pl.bL, pl.brem, (gs + 1u) * nkb - 1u);
+        const uint32_t old = __hip_atomic_fetch_add(pl.cnt + gs, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (old == bl - bf) {
+          last = 1u;
+          __hip_atomic_store(pl.cnt + gs, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
+      sh_tail[i] = last;
+    }
+    __syncthreads();
+    const uint32_t last0 = sh_tail[0], last1 = sh_tail[1];
+    if (!(last0 | last1) || kg != 0u) return;
+    for (uint32_t i = 0; i < 2u; ++i) {
+      if (!(i == 0u ? last0 : last1)) continue;  // uniform
+      const uint32_t gs = i == 0u ? gfirst : glast;
+      const uint32_t bf = plan_wg_of_unit(pl.bL, pl.brem, gs * nkb);
+      const uint32_t bl = plan_wg_of_unit(pl.bL, pl.brem, (gs + 1u) * nkb - 1u);
+      // The slab's segment, output and columns (as at the top of its piece).
+      uint32_t si = 0;
+      if constexpr (FUSED) {
+        for (uint32_t k = 1; k < d.nseg; ++k)
+          if (gs >= d.seg[k].blk_begin) si = k;
+        si = __builtin_amdgcn_readfirstlane(si);
+      }
+      const SegDesc& sg = d.seg[si];
+      const uint32_t ldyo = (uint32_t)sg.ldy, No = sg.N;
+      const uint32_t ctwo = (gs - sg.blk_begin) * pl.sw + wi * T;
+      const uint32_t owno = wi * T < pl.sw ? min((uint32_t)T, pl.sw - wi * T) : 0u;
+      const uint32_t ntwo = ctwo < sg.ntiles ? min(owno, sg.ntiles - ctwo) : 0u;
+      const __amdgpu_buffer_rsrc_t yro = make_rsrc(sg.Y, M * ldyo * 2u);
+      // Contributors bf .. bl (at most two): slot 0 when gs is the contributor's first slab.
+      const uint32_t s0 = plan_div(plan_begin(pl.bL, pl.brem, bf), nkb, pl.nkb_m) == gs ? 0u : 1u;
+      const uint32_t s1 = plan_div(plan_begin(pl.bL, pl.brem, bl), nkb, pl.nkb_m) == gs ? 0u : 1u;
+#pragma unroll
+      for (int r = 0; r < MT; ++r) {
+        if (16u * r + 4u * g4 >= M) continue;
+        f4 p0[T], p1[T];
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+          const uint32_t tile = (wi * T + t) * MT + r;
+          p0[t] = __builtin_amdgcn_raw_buffer_load_b128(
+              bpart, (((bf * 2u + s0) * kTiles + tile) * 64u + lane) * 16u, 0, 16);
+          p1[t] = bl != bf ? __builtin_amdgcn_raw_buffer_load_b128(
+                                 bpart, (((bl * 2u + s1) * kTiles + tile) * 64u + lane) * 16u, 0, 16)
+                           : f4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+          const f4 v = p0[t] + p1[t];
+          const uint32_t col = (ctwo + t) * 16u + c16;
+          const bool mine = (uint32_t)t < ntwo && col < No;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const uint32_t row = 16u * r + 4u * g4 + e;
+            const uint32_t o = row < M && mine ? (row * ldyo + col) * 2u : kOutOfRange;
+            __builtin_amdgcn_raw_buffer_store_b16(f32_to_out<DT>(v[e]), yro, o, 0, 0);
+          }
+        }
+      }
+    }
+  }
 }
 
 int ls_env(const char* name, int dflt) {
@@ -704,6 +825,31 @@ hipError_t ls_launch_t(GemmDesc d, const LsConfig& c, void* ws, uint32_t* fault,
     if (!ws) return hipErrorInvalidValue;
     pl.cnt = static_cast<uint32_t*>(ws);
     pl.part = reinterpret_cast<float*>(static_cast<char*>(ws) + kCounterBytes);
+  }
+  if (c.P > 0) {  // balanced grid
+    if constexpr (GEN || KG == 1 || MT == 1) {
+      return hipErrorInvalidConfiguration;
+    } else {
+      const uint32_t P = (uint32_t)c.P;
+      const uint64_t utot = (uint64_t)G * d.nkb;
+      if (P >= G || !ws || G > kMaxCounters || utot >= (1ull << 31) || utot / P < d.nkb) return hipErrorInvalidValue;
+      pl.S = 1;
+      pl.bL = (uint32_t)(utot / P);
+      pl.brem = (uint32_t)(utot % P);
+      pl.nkb_m = plan_div_magic(d.nkb);
+      pl.cnt = static_cast<uint32_t*>(ws);
+      pl.part = reinterpret_cast<float*>(static_cast<char*>(ws) + kCounterBytes);
+      bool fitsb = (uint64_t)d.M * (uint64_t)d.ldx * 2u < (1ull << 31) && (uint64_t)P * 2u * GW * T * MT * 1024u < (1ull << 31);
+      for (uint32_t i = 0; i < d.nseg; ++i) fitsb = fitsb && (uint64_t)d.M * (uint64_t)d.seg[i].ldy * 2u < (1ull << 31);
+      if (!fitsb) return hipErrorInvalidValue;
+      if (fused)
+        hipLaunchKernelGGL((hq_decode_ls_kernel<FMT, DT, KG, GW, T, U, MT, true, false, true>), dim3(P, 1),
+                           dim3(64 * KG * GW), 0, stream, d, pl);
+      else
+        hipLaunchKernelGGL((hq_decode_ls_kernel<FMT, DT, KG, GW, T, U, MT, false, false, true>), dim3(P, 1),
+                           dim3(64 * KG * GW), 0, stream, d, pl);
+      return hipGetLastError();
+    }
   }
   // Byte offsets into X, Y and the partials are 32-bit buffer offsets.
   const uint64_t xbytes = (uint64_t)d.M * (uint64_t)d.ldx * 2u;
@@ -825,6 +971,21 @@ LsConfig choose_decode_ls(int fmt, const GemmDesc& d, size_t ws_cap) {
   // MI355X (ternary 5120 x 34816, 272 slabs): M = 48 47 -> 41.5 us, M = 80 63 -> 60 us; with
   // slabs for every CU already (216-240) one k-group is 5-20% slower.
   if (c.MT > 1 && eKG == 0 && (uint64_t)G * (uint32_t)c.S > cus && (uint64_t)G * (uint32_t)c.S <= 2ull * cus) c.KG = 1;
+  // Several row tiles and more slabs than CUs: a balanced grid, one workgroup of two k-groups
+  // per CU, each an equal run of (slab, k-block) units (its first and last slab possibly
+  // shared with a neighbour through the workspace), where one k-group per workgroup would
+  // leave a few CUs with two (up to 1.25 slabs per CU) or where two k-groups would run more
+  // than two rounds. Measured on MI355X (M = 32 / 80, alternated): int4 5120 x 34816 (272
+  // slabs) 36.5 -> 29.8 / 54.7 -> 50.5 us, 4096 x 40960 (320) 28.5 -> 26.8 / 45.9 -> 44.5,
+  // ternary 5120 x 69632 (544) 55.8 -> 47.2 / 92.2 -> 84.3; at 432 slabs (int4 5120 x 55296)
+  // two workgroups per CU on most CUs stay 13-17% ahead. HQ_DECODE_LS_BAL = 0 / 1: off / on.
+  const int ebal = ls_env("HQ_DECODE_LS_BAL", -1);
+  const bool bal_fit = 4u * G <= 5u * cus || G > 2u * cus;
+  if (c.MT > 1 && !d.gen && G > cus && G <= kMaxCounters && (ebal == 1 || (ebal != 0 && bal_fit))) {
+    c.P = (int)cus;
+    c.KG = 2;
+    c.S = 1;
+  }
   // Narrower slabs that would cover every CU measured slower (5120 x 27648, M = 1..16:
   // 247 slabs of 7 tiles 2-15% behind 216 of 8), so slabs stay GW * T tiles wide.
   // The general kernels exist in one configuration: two k-groups of four wavefronts, two
@@ -842,10 +1003,15 @@ LsConfig choose_decode_ls(int fmt, const GemmDesc& d, size_t ws_cap) {
   c.S = std::max(1, std::min<int>({c.S, (int)d.nkb, (int)kMaxPieces}));
   if (c.S > 1 && ls_assign_slabs(x, (uint32_t)c.SW) > kMaxCounters) c.S = 1;
   while (c.S > 1 && decode_ls_workspace_bytes(d, c) > ws_cap) --c.S;  // fewer pieces under a cap
+  if (c.P > 0 && decode_ls_workspace_bytes(d, c) > ws_cap) {  // the S-piece grid under a cap
+    c.P = 0;
+    if (eKG == 0) c.KG = 1;
+  }
   return c;
 }
 
 size_t decode_ls_workspace_bytes(const GemmDesc& d, const LsConfig& c) {
+  if (c.P > 0) return kCounterBytes + (size_t)c.P * 2u * c.GW * c.T * c.MT * 1024u;
   if (c.S <= 1) return 0;
   GemmDesc x = d;
   const uint32_t G = ls_assign_slabs(x, (uint32_t)c.SW);

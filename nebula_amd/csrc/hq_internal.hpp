@@ -106,6 +106,8 @@ struct LsConfig {
   int GW;  // wavefronts per k-group (2 or 4)
   int SW;  // tiles per slab, at most GW * T (wavefront i takes tiles T i .. min(T i + T, SW) - 1)
   int MT;  // 16-row tiles of activations (1 .. kLsMaxRowTiles): rows M <= 16 MT
+  int P = 0;  // balanced grid (several row tiles, more slabs than CUs): P workgroups, each an
+              // equal run of (slab, k-block) units; 0 = the S-piece grid
 };
 // The lockstep kernel takes up to this many 16-row tiles (M <= 80: a split-fuse step of 16
 // decode tokens and a 64-token prefill chunk fits one call).
@@ -119,6 +121,12 @@ struct LsPlan {
   float* part;      // [G][S][GW * T * MT tiles][64 lanes] f4 partial tiles (S > 1)
   uint32_t* fault;  // host-visible word set to 1 when a k-group barrier gives up (may be null)
   uint32_t spin;    // polls before a k-group barrier gives up
+  // Balanced grid (LsConfig::P > 0, more slabs than workgroups): workgroup b takes units
+  // (g nkb + kb, slab-major) [begin(b), begin(b + 1)), begin(b) = b bL + min(b, brem): its
+  // first and last slab may be partial (at most two contributors each, bL >= nkb); part then
+  // holds [P][2][GW * T * MT tiles][64 lanes] f4 (slot 0: first slab, 1: last slab).
+  uint32_t bL, brem;
+  uint32_t nkb_m;   // plan_div_magic(nkb)
 };
 // Polls of the lockstep k-group barrier before it gives up (each poll sleeps ~64 cycles):
 // far beyond any correct launch, whose k-groups stay within one step of each other.

@@ -800,14 +800,59 @@ def test_lockstep_row_tiles_one_kgroup(cuda, fmt, xdt, M):
 
 
 def test_lockstep_row_tiles_wide_grid(cuda):
-    # More 8-tile slabs than CUs (260 on 256 CUs): the planner takes one k-group per workgroup.
+    # More 8-tile slabs than CUs (260 on 256 CUs): the planner takes the balanced grid; without
+    # it, one k-group per workgroup (two workgroups share a CU) or two rounds of two k-groups.
     N = 16 * 8 * 260
     P = O.Problem(O.INT4, 40, 512, N, 128, O.F16, seed=3900)
     D = DeviceProblem(P)
     y = D.run()
     check(y, P.reference(), O.F16, f"row tiles wide grid N={N}", P)
-    with decode_env(LS_KG=2):  # two rounds of one-per-CU workgroups: the same products
-        check(D.run(), P.reference(), O.F16, f"row tiles wide grid, two k-groups, N={N}", P)
+    with decode_env(LS_BAL=0):
+        check(D.run(), P.reference(), O.F16, f"row tiles wide grid, S-piece grid, N={N}", P)
+        with decode_env(LS_KG=2):
+            check(D.run(), P.reference(), O.F16, f"row tiles wide grid, two k-groups, N={N}", P)
+
+
+# Balanced grid (several row tiles, more slabs than CUs): every workgroup an equal run of
+# (slab, k-block) units, first and last slabs shared with the neighbours through the
+# workspace. Slab counts just above the CUs, two and three slabs per workgroup (middle
+# slabs whole), K of one to three k-blocks per slab boundary, every format and dtype.
+@pytest.mark.parametrize("fmt,xdt,M,K,slabs", [(O.INT4, O.F16, 40, 512, 260), (O.INT4, O.BF16, 80, 1024, 300),
+                                                (O.TERNARY2, O.F16, 33, 768, 520), (O.TERNARY2, O.BF16, 64, 384, 770),
+                                                (O.INT4, O.F16, 17, 128, 257), (O.INT4, O.F16, 80, 2048, 272)])
+def test_lockstep_balanced_grid(cuda, fmt, xdt, M, K, slabs):
+    N = 16 * 8 * slabs - 8 * (slabs % 3)  # the last slab's last tile ragged for some
+    P = O.Problem(fmt, M, K, N, 128, xdt, seed=4000 + slabs)
+    D = DeviceProblem(P)
+    with decode_env(LS_BAL=1):
+        assert "balanced grid" in hq.describe(fmt, xdt, M, K, N, 128)
+        y = D.run()
+        assert torch_equal(y, D.run())  # deterministic: partials summed in workgroup order
+    check(y, P.reference(), xdt, f"balanced grid fmt={fmt} M={M} K={K} slabs={slabs}", P)
+
+
+def test_lockstep_balanced_grid_fused_and_counters(cuda):
+    # Segment boundaries inside workgroup ranges; the arrival counters return to zero in a
+    # caller workspace reused by a second call.
+    import torch
+
+    K, M = 640, 48
+    Ns = [16 * 8 * 150 + 16, 1000, 16 * 8 * 120]
+    probs = [O.Problem(O.INT4, M, K, n, 128, O.F16, seed=4100 + i) for i, n in enumerate(Ns)]
+    for p in probs[1:]:
+        p.X = probs[0].X
+    devs = [DeviceProblem(p) for p in probs]
+    segs = [(d.Wp, d.S, d.P.N) for d in devs]
+    with decode_env(LS_BAL=1):
+        nbytes = hq.workspace_bytes_fused(O.INT4, M, K, [n for n in Ns], 128)
+        ws = torch.zeros(nbytes, dtype=torch.uint8, device="cuda")
+        outs = hq.gemm_fused(O.INT4, devs[0].X, segs, workspace=ws)
+        outs2 = hq.gemm_fused(O.INT4, devs[0].X, segs, workspace=ws)
+    for d, y, y2 in zip(devs, outs, outs2):
+        check(y, d.P.reference(), O.F16, f"balanced grid fused N={d.P.N}", d.P)
+        assert torch_equal(y, y2)
+    torch.cuda.synchronize()
+    assert int(ws[:65536].view(torch.int32).abs().sum().item()) == 0
 
 
 def test_lockstep_row_tiles_fused_and_vs_prefill(cuda):
