@@ -8,7 +8,9 @@
 //
 // Here a workgroup owns a slab of up to 4 * T column tiles (16 columns each) and a
 // contiguous range of 128-deep k-blocks ("piece"); a slab's k-blocks are split over S
-// workgroups (S = 1 for wide weights). The activation rows come in MT tiles of 16 rows
+// workgroups (S = 1 for wide weights). With several row tiles and more slabs than CUs, a
+// balanced grid gives every workgroup an equal run of (slab, k-block) units instead: whole
+// slabs in the middle, its first and last slab shared with a neighbour (fix-up as below). The activation rows come in MT tiles of 16 rows
 // (M <= 16 MT): every dequantised weight fragment feeds all MT row tiles. The workgroup has KG k-groups of four wavefronts; wavefront i
 // of every k-group streams tiles T i .. T i + T - 1 of the slab, and at step q k-group kg
 // takes k-block q * KG + kg of the piece, so the KG k-groups split K inside the CU and
