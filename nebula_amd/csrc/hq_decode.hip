@@ -567,18 +567,25 @@ __global__ void __launch_bounds__(64 * xr_max_wk(T)) hq_decode_xr_kernel(const G
     f4 gs[T];
 #pragma unroll
     for (int t = 0; t < T; ++t) gs[t] = seed;
+    if constexpr (kInt4) {
 #pragma unroll
-    for (int c = 0; c < 4; ++c) {
+      for (int c = 0; c < 4; ++c)
 #pragma unroll
-      for (int t = 0; t < T; ++t) {
-        u4 bf;
-        if constexpr (kInt4) {
-          bf = dq_int4_biased<DT>(wr[u][t][c], dqb);
-        } else {
-          const uint32_t word = wr[u][t][c >> 1];
-          bf = (c & 1) ? dq_tern2<1>(word) : dq_tern2<0>(word);
+        for (int t = 0; t < T; ++t) gs[t] = mfma16x16x32<DT>(a[c], dq_int4_biased<DT>(wr[u][t][c], dqb), gs[t]);
+    } else {
+      // Ternary: chunks 0 and 2, then 1 and 3, each pair from one set of 64-bit shifts.
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        u4 f0[T], f1[T];
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+          if (h == 0) dq_tern2_pair<0>(tern2_words(wr[u][t][0], wr[u][t][1]), f0[t], f1[t]);
+          else dq_tern2_pair<1>(tern2_words(wr[u][t][0], wr[u][t][1]), f0[t], f1[t]);
         }
-        gs[t] = mfma16x16x32<DT>(a[c], bf, gs[t]);
+#pragma unroll
+        for (int t = 0; t < T; ++t) gs[t] = mfma16x16x32<DT>(a[h], f0[t], gs[t]);
+#pragma unroll
+        for (int t = 0; t < T; ++t) gs[t] = mfma16x16x32<DT>(a[2 + h], f1[t], gs[t]);
       }
     }
 #pragma unroll

@@ -169,6 +169,9 @@ __global__ void __launch_bounds__(64 * KG * GW, KG == 1 && MT > 1 ? 2 : 1)
   // at M = 80 61.4 -> 52.9 us, 5120 x 14336 31.6 -> 28.6 us. Not for int4 bf16 at five row
   // tiles, whose correction chains would not fit in 256 VGPRs beside the fragments.
   constexpr bool kAllA = !GEN && MT > 1 && (kFold || !kInt4 || MT <= 4);
+  // Ternary fragments from 64-bit shifts of the word pair (dq_tern2_pair) up to three row
+  // tiles; with more, the register pairs the shifts need made some variants spill.
+  constexpr bool kPairTern = !kInt4 && MT <= 3;
   // The register ring holds U steps in flight plus the one being consumed. Activations
   // are staged through two LDS stages: a stage is written just before the barrier of its
   // step and rewritten two steps later, after every wavefront has passed the next barrier
@@ -334,18 +337,30 @@ __global__ void __launch_bounds__(64 * KG * GW, KG == 1 && MT > 1 ? 2 : 1)
       for (int t = 0; t < T; ++t) sbt[t] = T == 1 ? sring[slot][0] : ls_bpermute((16u * t + c16) * 4u, sring[slot][0]);
       // Dequantisation (VALU) while the LDS reads are in flight.
       u4 bq[4][T];
+      if constexpr (kInt4) {
 #pragma unroll
-      for (int c = 0; c < 4; ++c)
+        for (int c = 0; c < 4; ++c)
 #pragma unroll
-        for (int t = 0; t < T; ++t) {
-          if constexpr (kInt4) {
+          for (int t = 0; t < T; ++t) {
             bq[c][t] = dq_int4_biased<DT>(wring[slot][t][c], dqb);
             if constexpr (kUnbiased) bq[c][t] = unbias_f16(bq[c][t]);
-          } else {
+          }
+      } else if constexpr (kPairTern) {
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+          const uint64_t v = tern2_words(wring[slot][t][0], wring[slot][t][1]);
+          dq_tern2_pair<0>(v, bq[0][t], bq[2][t]);
+          dq_tern2_pair<1>(v, bq[1][t], bq[3][t]);
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+          for (int t = 0; t < T; ++t) {
             const uint32_t word = wring[slot][t][c >> 1];
             bq[c][t] = (c & 1) ? dq_tern2<1>(word) : dq_tern2<0>(word);
           }
-        }
+      }
       ls_wait_lgkmcnt0();
 #pragma unroll
       for (int r = 0; r < MT; ++r)
@@ -420,18 +435,30 @@ __global__ void __launch_bounds__(64 * KG * GW, KG == 1 && MT > 1 ? 2 : 1)
     }
     // The weight fragments of the k-block, dequantised once and used by every row tile.
     u4 bf[4][T];
+    if constexpr (kInt4) {
 #pragma unroll
-    for (int c = 0; c < 4; ++c)
+      for (int c = 0; c < 4; ++c)
 #pragma unroll
-      for (int t = 0; t < T; ++t) {
-        if constexpr (kInt4) {
+        for (int t = 0; t < T; ++t) {
           bf[c][t] = dq_int4_biased<DT>(wring[slot][t][c], dqb);
           if constexpr (kUnbiased) bf[c][t] = unbias_f16(bf[c][t]);
-        } else {
+        }
+    } else if constexpr (kPairTern) {
+#pragma unroll
+      for (int t = 0; t < T; ++t) {
+        const uint64_t v = tern2_words(wring[slot][t][0], wring[slot][t][1]);
+        dq_tern2_pair<0>(v, bf[0][t], bf[2][t]);
+        dq_tern2_pair<1>(v, bf[1][t], bf[3][t]);
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
           const uint32_t word = wring[slot][t][c >> 1];
           bf[c][t] = (c & 1) ? dq_tern2<1>(word) : dq_tern2<0>(word);
         }
-      }
+    }
     float sc[T];
     float gs_[GEN ? T : 1][4], ge_[GEN ? T : 1][4];  // GEN: scale and e = 8 s + b of (tile, chunk)
 #pragma unroll
