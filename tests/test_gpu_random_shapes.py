@@ -1,0 +1,52 @@
+"""GPU parity over seeded random shapes, each planned by the library's default planner.
+
+The parametrised tests elsewhere pin each kernel and tiling on chosen shapes; these cases draw
+(format, activation dtype, M, K, N, group, bias) at random from a fixed seed so that the
+planner's choices are exercised on shapes nobody picked: M over the three bands (1-16: the
+X-resident / per-wavefront kernels, 17-80: the lockstep kernel's row tiles, 81-300: the prefill
+tiles, whole and stream-K), ragged N (1..3000), K up to 6144 in multiples of 128 and of the
+group, groups 32 / 64 (general kernels) and 128 / 256, and the int4 caller bias. Each case is
+checked against the oracle with the bars of the general-kernel tests: normwise error within the
+output rounding (2e-3 fp16, 8e-3 bf16) and, per element, |y - r| <= rel * |X| (|W| + |E|) +
+ulp(r) (rel = 2^-10 fp16, 2^-7 bf16; E the weight of code 8 of each int4 group).
+"""
+import numpy as np
+import pytest
+
+import oracle as O
+from test_gpu_general import Dev, check
+
+pytestmark = pytest.mark.gpu
+
+MAX_MACS = 1.2e9  # keeps the oracle and the float64 bound check to about a second a case
+
+
+def _cases(n: int = 96, seed: int = 20261202):
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        fmt = (O.INT4, O.TERNARY2)[i % 2]
+        xdt = (O.F16, O.BF16)[(i // 2) % 2]
+        band = (i // 4) % 3
+        lo, hi = ((1, 16), (17, 80), (81, 300))[band]
+        M = int(rng.integers(lo, hi + 1))
+        group = int(rng.choice([32, 64, 128, 256]))
+        step = 256 if group == 256 else 128  # K: a multiple of 128 and of the group
+        K = step * int(rng.integers(1, 6144 // step + 1))
+        N = int(rng.integers(1, 3001))
+        N = max(1, min(N, int(MAX_MACS // (M * K))))
+        bias = "random" if fmt == O.INT4 and rng.random() < 0.5 else None
+        cases.append((fmt, xdt, M, K, N, group, bias, 9000 + i))
+    return cases
+
+
+CASES = _cases()
+
+
+@pytest.mark.parametrize("fmt,xdt,M,K,N,group,bias,seed", CASES,
+                         ids=[f"f{c[0]}-d{c[1]}-M{c[2]}-K{c[3]}-N{c[4]}-g{c[5]}-{c[6] or 'nobias'}" for c in CASES])
+def test_random_shape(cuda, fmt, xdt, M, K, N, group, bias, seed):
+    P = O.Problem(fmt, M, K, N, group, xdt, seed=seed, bias=bias)
+    label = f"fmt={fmt} dt={xdt} M={M} K={K} N={N} g={group} bias={bias} seed={seed}"
+    print(label, flush=True)
+    check(Dev(P).run(), P, label)
