@@ -1015,11 +1015,14 @@ static int xr_waves_per_simd(int fmt, int T, int U) {
 // against 7.5-8.4, 27648 x 5120 at M = 1, 2 15.0-15.8 against 16.8-17.3, ternary 5120 x 27648
 // at M = 1 12.3 against 14.1. With wide weights (more tiles than two per CU) and more than
 // eight rows the lockstep kernel, which streams each activation k-block through LDS instead of
-// copying all of K per workgroup up front, is as fast or faster (5120 x 27648, M = 12 and 16:
-// 17.0-18.5 us against 17.7-18.8 with 8-tile slabs, the only one-round X-resident grid), so
-// the planner leaves those calls to it; at five to eight rows the 4-tile slabs still fit two
-// workgroups per CU and win (M = 5, 8: 15.5-16.3 against 16.6-17.7 us; ternary bf16 M = 8:
-// 13.5 against 15.0). HQ_XR_T / _WK / _U / _S override (tuning and tests).
+// copying all of K per workgroup up front, is as fast or faster when the only one-round
+// X-resident grid has 8-tile slabs of four wavefronts (5120 x 27648, M = 12 and 16: 17.0-18.5
+// us against 17.7-18.8), so the planner leaves those calls to it; one round of 4-tile slabs
+// of eight wavefronts wins at any row count (M = 9..16: ternary 5120 x 14336 11.7-12.4 ->
+// 8.8-9.1 us, int4 bf16 14.4-14.8 -> 10.2-10.9, 5120 x 10240 and 16384 7-15% faster), and at
+// five to eight rows the 4-tile slabs still fit two workgroups per CU and win (M = 5, 8:
+// 15.5-16.3 against 16.6-17.7 us; ternary bf16 M = 8: 13.5 against 15.0).
+// HQ_XR_T / _WK / _U / _S override (tuning and tests).
 XrConfig choose_decode_xr(int fmt, const GemmDesc& d, size_t ws_cap) {
   XrConfig c{2, 3, 8, 1, 0, false};
   if (d.M > 16u || d.gen) return c;
@@ -1029,7 +1032,7 @@ XrConfig choose_decode_xr(int fmt, const GemmDesc& d, size_t ws_cap) {
   const int eT = env_int("HQ_XR_T", 0), eWK = env_int("HQ_XR_WK", 0), eU = env_int("HQ_XR_U", 0);
   const int eS = env_int("HQ_XR_S", 0);
   const bool forced = eT || eWK || eU || eS;
-  bool found = false;
+  bool found = false, one_round = false;
   for (int s = 1; s <= 8 && !found; ++s) {
     if ((uint32_t)s > d.nkb || xr_x_bytes(d, s) > kXrLdsMax || (s > 1 && d.M > 4u)) continue;
     for (int t : {1, 2, 4, 8}) {
@@ -1053,10 +1056,14 @@ XrConfig choose_decode_xr(int fmt, const GemmDesc& d, size_t ws_cap) {
       if (s == 1 && wgs * 2u < cus && total_slabs(d, t) * 2u <= cus * per_cu && d.nkb >= 2 && d.M <= 4u) break;
       c = XrConfig{t, u, wk, s, lds, false};
       found = true;
+      one_round = wgs <= cus * per_cu;
       break;
     }
   }
-  if (!forced && (!found || (tiles > 2u * cus && d.M > 8u))) return c;
+  // Wide weights at more than eight rows: the lockstep kernel unless one round of slabs of at
+  // most four tiles (eight wavefronts) fits.
+  const bool wide_rows = tiles > 2u * cus && d.M > 8u && (c.T > 4 || !one_round);
+  if (!forced && (!found || wide_rows)) return c;
   if (eT == 1 || eT == 2 || eT == 4 || eT == 8) c.T = eT;
   if (eWK >= 1) c.WK = eWK;
   if (eU >= 2) c.U = eU;

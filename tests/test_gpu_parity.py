@@ -527,6 +527,22 @@ def test_xr_lds_limits(cuda, M, K):
     check(y, P.reference(threads=16), O.F16, f"xr lds M={M} K={K}", P)
 
 
+@pytest.mark.parametrize("fmt,xdt,M,N", [(O.TERNARY2, O.F16, 12, 14336), (O.INT4, O.BF16, 16, 14336),
+                                         (O.TERNARY2, O.BF16, 9, 16384), (O.INT4, O.F16, 16, 27648)])
+def test_xr_wide_rows_default_plan(cuda, fmt, xdt, M, N):
+    # Wide weights at more than eight rows, as the planner takes them: one round of 4-tile
+    # X-resident slabs (the decoder's fused QKV and SSM projections), the lockstep kernel when
+    # only 8-tile slabs would fit in one round (5120 x 27648).
+    K = 5120
+    P = O.Problem(fmt, M, K, N, 128, xdt, seed=3600 + M)
+    desc = hq.describe(fmt, xdt, M, K, N)
+    if N == 27648:
+        assert desc.startswith("hq_decode_ls_kernel<"), desc
+    else:
+        assert desc.startswith("hq_decode_xr_kernel<") and ",T=4," in desc and "x 1 pieces" in desc, desc
+    check(DeviceProblem(P).run(), P.reference(threads=16), xdt, f"wide rows {desc[:40]} M={M} N={N}", P)
+
+
 # K pieces per slab (S): even and uneven splits of 16 k-blocks, one k-block per piece, and
 # pieces that leave some wavefronts without k-blocks; the last of a slab's workgroups sums
 # the partials in piece order (bit-identical from run to run) and leaves its counter at zero.
