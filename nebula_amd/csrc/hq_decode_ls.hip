@@ -140,7 +140,7 @@ __device__ __forceinline__ void ls_tie(uint32_t& a) { asm volatile("" : "+v"(a))
 template <int FMT, int DT, int KG, int GW, int T, int U, int MT, bool FUSED, bool GEN, bool BAL = false>
 __global__ void __launch_bounds__(64 * KG * GW, KG == 1 && MT > 1 ? 2 : 1)
     hq_decode_ls_kernel(const GemmDesc d, const LsPlan pl) {
-  static_assert(!BAL || (KG > 1 && MT > 1 && !GEN), "the balanced grid is for fast kernels with several row tiles");
+  static_assert(!BAL || (KG > 1 && !GEN), "the balanced grid is for the fast kernels with two k-groups");
   static_assert(KG == 1 || KG == 2 || KG == 4, "one, two or four k-groups");
   static_assert(GW == 2 || GW == 4, "k-groups of two or four wavefronts");
   static_assert(T >= 1 && T <= 4, "the scale load covers at most four tiles");
@@ -856,7 +856,7 @@ hipError_t ls_launch_t(GemmDesc d, const LsConfig& c, void* ws, uint32_t* fault,
     pl.part = reinterpret_cast<float*>(static_cast<char*>(ws) + kCounterBytes);
   }
   if (c.P > 0) {  // balanced grid
-    if constexpr (GEN || KG == 1 || MT == 1) {
+    if constexpr (GEN || KG == 1 || (MT == 1 && !(KG == 2 && GW == 4 && T == 2 && U == 2))) {
       return hipErrorInvalidConfiguration;
     } else {
       const uint32_t P = (uint32_t)c.P;
@@ -1007,13 +1007,18 @@ LsConfig choose_decode_ls(int fmt, const GemmDesc& d, size_t ws_cap) {
   // than two rounds. Measured on MI355X (M = 32 / 80, alternated): int4 5120 x 34816 (272
   // slabs) 36.5 -> 29.8 / 54.7 -> 50.5 us, 4096 x 40960 (320) 28.5 -> 26.8 / 45.9 -> 44.5,
   // ternary 5120 x 69632 (544) 55.8 -> 47.2 / 92.2 -> 84.3; at 432 slabs (int4 5120 x 55296)
-  // two workgroups per CU on most CUs stay 13-17% ahead. HQ_DECODE_LS_BAL = 0 / 1: off / on.
+  // two workgroups per CU on most CUs stay 13-17% ahead. One row tile (M <= 16): int4 up to
+  // 1.25 slabs per CU (int4 5120 x 34816, M = 9..16: 25.3-27.2 -> 23.8-25.5 us; 4096 x 40960
+  // 25.0-25.5 -> 21.7-22.1); ternary weights and 432 slabs measured slower, 544 even.
+  // HQ_DECODE_LS_BAL = 0 / 1: off / on.
   const int ebal = ls_env("HQ_DECODE_LS_BAL", -1);
-  const bool bal_fit = 4u * G <= 5u * cus || G > 2u * cus;
-  if (c.MT > 1 && !d.gen && G > cus && G <= kMaxCounters && (ebal == 1 || (ebal != 0 && bal_fit))) {
+  const bool one_tile = c.MT == 1 && c.GW == 4 && c.T == 2;
+  const bool bal_fit = c.MT > 1 ? (4u * G <= 5u * cus || G > 2u * cus) : (fmt == HQ_FORMAT_INT4 && 4u * G <= 5u * cus);
+  if ((c.MT > 1 || one_tile) && !d.gen && G > cus && G <= kMaxCounters && (ebal == 1 || (ebal != 0 && bal_fit))) {
     c.P = (int)cus;
     c.KG = 2;
     c.S = 1;
+    if (c.MT == 1) c.U = 2;
   }
   // Narrower slabs that would cover every CU measured slower (5120 x 27648, M = 1..16:
   // 247 slabs of 7 tiles 2-15% behind 216 of 8), so slabs stay GW * T tiles wide.

@@ -847,6 +847,26 @@ def test_lockstep_balanced_grid(cuda, fmt, xdt, M, K, slabs):
     check(y, P.reference(), xdt, f"balanced grid fmt={fmt} M={M} K={K} slabs={slabs}", P)
 
 
+# The same with one row tile (M <= 16), as the planner takes int4 weights of up to 1.25 slabs
+# per CU; ternary weights and M = 1 forced.
+@pytest.mark.parametrize("fmt,xdt,M,K,slabs", [(O.INT4, O.F16, 12, 512, 260), (O.INT4, O.BF16, 16, 1024, 300),
+                                                (O.TERNARY2, O.F16, 9, 768, 270), (O.TERNARY2, O.BF16, 16, 384, 520),
+                                                (O.INT4, O.F16, 1, 128, 257)])
+def test_lockstep_balanced_grid_one_row_tile(cuda, fmt, xdt, M, K, slabs):
+    N = 16 * 8 * slabs - 8 * (slabs % 3)
+    P = O.Problem(fmt, M, K, N, 128, xdt, seed=4050 + slabs)
+    D = DeviceProblem(P)
+    with decode_env(KERNEL=1, LS_BAL=1):
+        desc = hq.describe(fmt, xdt, M, K, N, 128)
+        assert "MT=1>" in desc and "balanced grid" in desc, desc
+        y = D.run()
+        assert torch_equal(y, D.run())
+    if fmt == O.INT4 and slabs <= 320:
+        with decode_env(KERNEL=1):
+            assert "balanced grid" in hq.describe(fmt, xdt, M, K, N, 128)  # the planner's own choice
+    check(y, P.reference(), xdt, f"balanced grid one row tile fmt={fmt} M={M} K={K} slabs={slabs}", P)
+
+
 def test_lockstep_balanced_grid_fused_and_counters(cuda):
     # Segment boundaries inside workgroup ranges; the arrival counters return to zero in a
     # caller workspace reused by a second call.
