@@ -4,9 +4,11 @@
 // 327-377, 603-617), which the reference never launches: activations quantised as
 // int8(clamp(x * 127, -128, 127)) converted toward zero (:356-359), int8 weights [K][N]
 // (q * 16 - 128 of its int4 codes, :508), y = scale[n] * sum_k xq w / 127 with one scale per
-// column (:371-375). Two launches:
+// column (:371-375). Two launches, or one when a workgroup's activation rows are small:
 //   1. hq_quantize_x_kernel: the M x K activations once to int8 (the workspace), so the GEMM
-//      copies 1 byte per element instead of re-reading fp32 rows in every workgroup;
+//      copies 1 byte per element instead of re-reading fp32 rows in every workgroup; when the
+//      rows of a workgroup's K piece are at most one 16-element unit per thread (M = 1 at
+//      K = 5120), the GEMM reads them as fp32 and quantises them itself (QX);
 //   2. hq_w8a8_kernel: the X-resident structure of the int4 decode kernel (hq_decode.hip): one
 //      workgroup per (slab of T column tiles, piece of K), the piece's int8 rows copied into
 //      LDS by LDS-DMA, then a barrier-free register ring of weight steps (T tiles x one
@@ -53,6 +55,8 @@ __global__ void __launch_bounds__(256) hq_quantize_x_kernel(const float* __restr
 
 struct W8Plan {
   const int8_t* Xq;  // [M][K] int8 activations
+  const float* X;    // [M][ldx] fp32 activations (QX)
+  uint32_t ldx;
   const int8_t* Wp;  // tile layout
   const float* S;    // [N] scales
   float* Y;
@@ -71,7 +75,13 @@ constexpr int w8_max_wk(int T) { return T >= 4 ? 8 : 16; }
 // (r * nkbp + kb - kb0) * 8 + (j ^ (r & 7)) holds elements 16 j .. 16 j + 15 of k-block kb of row
 // r (j = 0..7); an A fragment read of chunk c (piece j = 4 c + g4) spreads eight rows over every
 // bank. Lanes of rows >= M read row M - 1 (their output rows are never stored).
-template <int T, int U>
+// The quantiser of hq_quantize_x_kernel on one value: clamp(x * 127) toward zero, NaN -> -128.
+__device__ __forceinline__ uint32_t quantize_int8(float v) {
+  const float t = fminf(fmaxf(v * 127.0f, -128.0f), 127.0f);
+  return (uint32_t)(int32_t)t & 0xFFu;
+}
+
+template <int T, int U, bool QX>
 __global__ void __launch_bounds__(64 * w8_max_wk(T)) hq_w8a8_kernel(const W8Plan pl) {
   constexpr uint32_t kCols = 16u * T;
   extern __shared__ __attribute__((aligned(16))) char xs[];
@@ -88,8 +98,23 @@ __global__ void __launch_bounds__(64 * w8_max_wk(T)) hq_w8a8_kernel(const W8Plan
   const uint32_t ct0 = g * T;
   const uint32_t nv = min((uint32_t)T, pl.ntiles - ct0);
 
-  // 1. The piece's int8 rows -> LDS (64 units of 16 bytes per LDS-DMA instruction).
-  {
+  // 1. The piece's int8 rows -> LDS (64 units of 16 bytes per LDS-DMA instruction), or (QX)
+  //    each thread's unit of fp32 elements into registers, quantised once the ring is issued.
+  const uint32_t xu = threadIdx.x;  // QX: this thread's unit (LDS bytes 16 xu .. 16 xu + 15)
+  bool xlive = false;
+  f4 xv[4];
+  if constexpr (QX) {
+    const uint32_t nkb8 = nkbp * 8u;
+    const uint32_t m8 = p < kr ? m_hi : m_lo;
+    const uint32_t r = plan_div(xu, nkb8, m8);
+    const uint32_t rem = xu - r * nkb8;
+    xlive = r < M;
+    const uint32_t voff =
+        xlive ? (r * pl.ldx + (kb0 + (rem >> 3)) * 128u + (((rem & 7u) ^ (r & 7u)) * 16u)) * 4u : kOutOfRange;
+    const __amdgpu_buffer_rsrc_t xf = make_rsrc(pl.X, M * pl.ldx * 4u);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) xv[i] = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(xf, voff, 16u * i, 0));
+  } else {
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(Xq, M * K);
     const uint32_t nkb8 = nkbp * 8u;
     const uint32_t m8 = p < kr ? m_hi : m_lo;
@@ -127,6 +152,16 @@ __global__ void __launch_bounds__(64 * w8_max_wk(T)) hq_w8a8_kernel(const W8Plan
   __builtin_amdgcn_sched_barrier(0);
   // Wait for this wavefront's copies only (the ring's 2 T U loads were issued after them).
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 * T * U));
+  if constexpr (QX) {
+    if (xlive) {
+      u4 q;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        q[i] = quantize_int8(xv[i][0]) | (quantize_int8(xv[i][1]) << 8) | (quantize_int8(xv[i][2]) << 16) |
+               (quantize_int8(xv[i][3]) << 24);
+      *reinterpret_cast<u4*>(xs + xu * 16u) = q;
+    }
+  }
   __syncthreads();
 
   const uint32_t xrow = min(c16, M - 1u);
@@ -227,15 +262,17 @@ uint32_t w8_lds_bytes(uint32_t M, uint32_t nkb, int T, int WK, int S) {
   return std::max(w8_x_bytes(M, nkb, S), (uint32_t)WK * M * 16u * (uint32_t)T * 4u);
 }
 
-template <int T, int U>
+template <int T, int U, bool QX>
 hipError_t w8_launch_t(const W8Config& c, W8Plan pl, hipStream_t stream) {
   static const hipError_t attr =
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&hq_w8a8_kernel<T, U>),
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&hq_w8a8_kernel<T, U, QX>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)kXrLdsMax);
   if (attr != hipSuccess) return attr;
   if (c.WK < 1 || c.WK > w8_max_wk(T)) return hipErrorInvalidValue;
+  // QX: every unit of a piece's rows has a thread (the kernel quantises one unit per thread).
+  if (QX && pl.M * (pl.kq + (pl.kr ? 1u : 0u)) * 8u > 64u * (uint32_t)c.WK) return hipErrorInvalidValue;
   const uint32_t G = (pl.ntiles + T - 1) / T;
-  hipLaunchKernelGGL((hq_w8a8_kernel<T, U>), dim3(G, pl.S_), dim3(64 * c.WK), c.lds, stream, pl);
+  hipLaunchKernelGGL((hq_w8a8_kernel<T, U, QX>), dim3(G, pl.S_), dim3(64 * c.WK), c.lds, stream, pl);
   return hipGetLastError();
 }
 
@@ -272,6 +309,11 @@ W8Config choose_w8a8(uint32_t M, uint32_t K, uint32_t N) {
   if (!found && !(eT || eWK || eS)) return c;
   c.lds = w8_lds_bytes(M, nkb, c.T, c.WK, c.S);
   c.ok = c.lds <= kXrLdsMax && (ntiles + c.T - 1) / c.T <= kMaxCounters;
+  // One launch when each thread has at most one 16-element unit of its piece's rows to
+  // quantise (M = 1 at K = 5120: the separate launch cost ~2 us of 31.8); HQ_W8_QX = 0 keeps
+  // the quantisation launch.
+  const uint32_t nkbp = (nkb + (uint32_t)c.S - 1u) / (uint32_t)c.S;
+  c.qx = c.ok && M * nkbp * 8u <= 64u * (uint32_t)c.WK && w8_env("HQ_W8_QX", 1) != 0;
   return c;
 }
 
@@ -295,12 +337,16 @@ hipError_t launch_w8a8(const float* X, uint32_t ldx, const int8_t* Wp, const flo
   if ((uint64_t)M * K >= (1ull << 31) || (uint64_t)c.T * nkb * 2048u >= (1ull << 31) || part >= (1ull << 31) ||
       (uint64_t)N * 4u >= (1ull << 31))
     return hipErrorInvalidValue;
-  const uint32_t n4 = M * K / 4u;
-  hipLaunchKernelGGL(hq_quantize_x_kernel, dim3((n4 + 255u) / 256u), dim3(256), 0, stream, X, ldx, Xq, M, K);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
+  if (!c.qx) {
+    const uint32_t n4 = M * K / 4u;
+    hipLaunchKernelGGL(hq_quantize_x_kernel, dim3((n4 + 255u) / 256u), dim3(256), 0, stream, X, ldx, Xq, M, K);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
   W8Plan pl{};
   pl.Xq = Xq;
+  pl.X = X;
+  pl.ldx = ldx;
   pl.Wp = Wp;
   pl.S = scales;
   pl.Y = Y;
@@ -319,8 +365,8 @@ hipError_t launch_w8a8(const float* X, uint32_t ldx, const int8_t* Wp, const flo
   pl.cnt = static_cast<uint32_t*>(ws);
   pl.part = reinterpret_cast<int32_t*>(w + kCounterBytes);
   switch (c.T) {
-    case 2: return w8_launch_t<2, 2>(c, pl, stream);
-    case 4: return w8_launch_t<4, 2>(c, pl, stream);
+    case 2: return c.qx ? w8_launch_t<2, 2, true>(c, pl, stream) : w8_launch_t<2, 2, false>(c, pl, stream);
+    case 4: return c.qx ? w8_launch_t<4, 2, true>(c, pl, stream) : w8_launch_t<4, 2, false>(c, pl, stream);
     default: return hipErrorInvalidConfiguration;
   }
 }

@@ -89,6 +89,7 @@ struct W8Config {
   int S;
   uint32_t lds;
   bool ok;
+  bool qx = false;  // the GEMM quantises its own activation rows (one launch)
 };
 W8Config choose_w8a8(uint32_t M, uint32_t K, uint32_t N);
 size_t w8a8_workspace_bytes(uint32_t M, uint32_t K, uint32_t N, const W8Config& c);

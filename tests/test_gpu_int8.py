@@ -127,3 +127,19 @@ def test_w8a8_strided_rows_and_caller_workspace(cuda):
     y = Y.cpu().numpy()
     assert np.all(y[:, N:] == 7.0)  # nothing written past N
     check(y[:, :N], X, W, s, "strided")
+
+
+# One launch: when each thread has at most one 16-element unit of its K piece's rows, the GEMM
+# quantises the fp32 rows itself; bit-identical to the quantisation launch (HQ_W8_QX = 0),
+# including the NaN / infinity / clamp / truncation values of row 0.
+@pytest.mark.parametrize("M,K,N,S", [(1, 5120, 1000, 0), (1, 128, 40, 0), (2, 2048, 700, 0), (3, 4096, 500, 3),
+                                     (1, 27648, 512, 6)])
+def test_w8a8_in_kernel_quantisation(cuda, M, K, N, S):
+    X, W, s = problem(M, K, N, 1300 + M + K)
+    env = {"S": S} if S else {}
+    with w8_env(**env):
+        y1 = run(X, W, s)
+        with w8_env(QX=0):
+            y0 = run(X, W, s)
+    assert np.array_equal(y1.view(np.uint32), y0.view(np.uint32)), (M, K, N, S)
+    check(y1, X, W, s, f"in-kernel quantisation M={M} K={K} S={S}")
