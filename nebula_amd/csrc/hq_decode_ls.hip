@@ -8,9 +8,10 @@
 //
 // Here a workgroup owns a slab of up to 4 * T column tiles (16 columns each) and a
 // contiguous range of 128-deep k-blocks ("piece"); a slab's k-blocks are split over S
-// workgroups (S = 1 for wide weights). With several row tiles and more slabs than CUs, a
-// balanced grid gives every workgroup an equal run of (slab, k-block) units instead: whole
-// slabs in the middle, its first and last slab shared with a neighbour (fix-up as below). The activation rows come in MT tiles of 16 rows
+// workgroups (S = 1 for wide weights). With more slabs than CUs (several row tiles, or int4
+// weights of up to 1.25 slabs per CU at one row tile), a balanced grid gives every workgroup
+// an equal run of (slab, k-block) units instead: whole slabs in the middle, its first and last
+// slab shared with a neighbour (fix-up as below). The activation rows come in MT tiles of 16 rows
 // (M <= 16 MT): every dequantised weight fragment feeds all MT row tiles. The workgroup has KG k-groups of four wavefronts; wavefront i
 // of every k-group streams tiles T i .. T i + T - 1 of the slab, and at step q k-group kg
 // takes k-block q * KG + kg of the piece, so the KG k-groups split K inside the CU and
@@ -1000,7 +1001,7 @@ LsConfig choose_decode_ls(int fmt, const GemmDesc& d, size_t ws_cap) {
   // MI355X (ternary 5120 x 34816, 272 slabs): M = 48 47 -> 41.5 us, M = 80 63 -> 60 us; with
   // slabs for every CU already (216-240) one k-group is 5-20% slower.
   if (c.MT > 1 && eKG == 0 && (uint64_t)G * (uint32_t)c.S > cus && (uint64_t)G * (uint32_t)c.S <= 2ull * cus) c.KG = 1;
-  // Several row tiles and more slabs than CUs: a balanced grid, one workgroup of two k-groups
+  // More slabs than CUs: a balanced grid, one workgroup of two k-groups
   // per CU, each an equal run of (slab, k-block) units (its first and last slab possibly
   // shared with a neighbour through the workspace), where one k-group per workgroup would
   // leave a few CUs with two (up to 1.25 slabs per CU) or where two k-groups would run more
