@@ -171,8 +171,9 @@ __global__ void __launch_bounds__(64 * KG * GW, KG == 1 && MT > 1 ? 2 : 1)
   // tiles, whose correction chains would not fit in 256 VGPRs beside the fragments.
   constexpr bool kAllA = !GEN && MT > 1 && (kFold || !kInt4 || MT <= 4);
   // Ternary fragments from 64-bit shifts of the word pair (dq_tern2_pair) up to three row
-  // tiles; with more, the register pairs the shifts need made some variants spill.
-  constexpr bool kPairTern = !kInt4 && MT <= 3;
+  // tiles, and at four outside the balanced grid; beyond, the register pairs the shifts need
+  // made the kernel spill.
+  constexpr bool kPairTern = !kInt4 && (MT <= 3 || (MT == 4 && !BAL));
   // The register ring holds U steps in flight plus the one being consumed. Activations
   // are staged through two LDS stages: a stage is written just before the barrier of its
   // step and rewritten two steps later, after every wavefront has passed the next barrier
