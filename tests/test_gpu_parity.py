@@ -527,6 +527,16 @@ def test_xr_lds_limits(cuda, M, K):
     check(y, P.reference(threads=16), O.F16, f"xr lds M={M} K={K}", P)
 
 
+@pytest.mark.parametrize("fmt,xdt,M,K,N", [(O.TERNARY2, O.F16, 1, 5120, 34816), (O.INT4, O.BF16, 2, 4096, 40960)])
+def test_xr_spilled_4tile_slabs_take_4wave_2tile_slabs(cuda, fmt, xdt, M, K, N):
+    # More 4-tile slabs than one round holds, at one or two rows: the planner takes 2-tile
+    # slabs of four wavefronts (one round on MI355X by the occupancy query).
+    P = O.Problem(fmt, M, K, N, 128, xdt, seed=3650 + M)
+    desc = hq.describe(fmt, xdt, M, K, N)
+    assert desc.startswith("hq_decode_xr_kernel<") and ",T=2,U=3>" in desc and "x 4 wavefronts" in desc, desc
+    check(DeviceProblem(P).run(), P.reference(threads=16), xdt, f"4-wave 2-tile slabs M={M} N={N}", P)
+
+
 @pytest.mark.parametrize("fmt,xdt,M,N", [(O.TERNARY2, O.F16, 12, 14336), (O.INT4, O.BF16, 16, 14336),
                                          (O.TERNARY2, O.BF16, 9, 16384), (O.INT4, O.F16, 16, 27648)])
 def test_xr_wide_rows_default_plan(cuda, fmt, xdt, M, N):
