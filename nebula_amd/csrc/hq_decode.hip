@@ -1074,6 +1074,19 @@ XrConfig choose_decode_xr(int fmt, const GemmDesc& d, size_t ws_cap) {
       break;
     }
   }
+  // Whole 4-tile slabs at up to eight rows: four wavefronts (one per SIMD, each streaming
+  // twice the k-blocks) instead of eight, when that grid still fits on the CUs in one round.
+  // Measured on MI355X (alternated runs): 5120 x 27648 int4 M = 1..8 14.7-16.3 -> 14.2-15.7 us,
+  // ternary bf16 11.5-12.6 -> 11.4-11.9; ternary 5120 x 34816 M = 4 16.2 -> 14.9. Past one
+  // round it loses (5120 x 34816 at M = 8, 544 slabs on 512 slots: 17.2 -> 18.7).
+  if (!forced && found && c.T == 4 && c.WK == 8 && c.S == 1 && d.M <= 8u) {
+    const uint32_t lds4 = xr_lds_bytes(d, 4, 4, 1);
+    const uint32_t per4 = std::min((uint32_t)xr_waves_per_simd(fmt, 4, 2), kXrLdsMax / lds4);
+    if (lds4 <= kXrLdsMax && per4 >= 1u && total_slabs(d, 4) <= cus * per4) {
+      c.WK = 4;
+      c.lds = lds4;
+    }
+  }
   // Wide weights at more than eight rows: the lockstep kernel unless one round of slabs of at
   // most four tiles (eight wavefronts) fits.
   const bool wide_rows = tiles > 2u * cus && d.M > 8u && (c.T > 4 || !one_round);
