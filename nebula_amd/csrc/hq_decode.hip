@@ -1006,10 +1006,10 @@ static int xr_waves_per_simd(int fmt, int T, int U) {
 // (T = 2, 4 or 8 tiles; 1 when that gives at most one workgroup per CU and fills at least half
 // of them) whose grid fits on the CUs in one round; only when whole slabs of up to
 // four rows leave more than half of the CUs idle does it cut K into pieces (S > 1) to fill
-// them. Pieces for the rows of a long K that do not fit in LDS measured slower than the
-// lockstep kernel (27648 x 5120, M = 8 and 16: 19.0 and 22.3 us against 18.2 and 20.9; each
-// workgroup copies up to 147 KiB of rows before streaming, and the pieces meet through the
-// workspace), so those calls stay with it. Eight wavefronts per workgroup (four with 8-tile slabs), two steps in flight (three
+// them. When the rows of all of K do not fit in LDS (long K), up to eight rows take the K
+// pieces that fill the most CUs in one round; above eight rows those calls stay with the
+// lockstep kernel (27648 x 5120, M = 16: six pieces of 8-tile slabs 19.6 us against 17.8; each
+// workgroup copies 147 KiB of rows before streaming). Eight wavefronts per workgroup (four with 8-tile slabs), two steps in flight (three
 // with 2-tile slabs). Measured on MI355X against the per-wavefront and lockstep kernels
 // (graph-timed, weights rotated past the 256 MiB cache): 5120 x 5120 at M = 1..16 5.7-7.1 us
 // against 7.5-8.4, 27648 x 5120 at M = 1, 2 15.0-15.8 against 16.8-17.3, ternary 5120 x 27648
@@ -1033,6 +1033,28 @@ XrConfig choose_decode_xr(int fmt, const GemmDesc& d, size_t ws_cap) {
   const int eS = env_int("HQ_XR_S", 0);
   const bool forced = eT || eWK || eU || eS;
   bool found = false, one_round = false;
+  // Rows of all of K that do not fit in LDS (long K) at up to eight rows: K pieces, the
+  // one-round grid (at most one workgroup per CU) that keeps the most CUs busy, the fewest
+  // pieces among equals. Measured on MI355X (alternated runs), 27648 x 5120: M = 4 16.3 us with
+  // 4-tile slabs in three pieces (240 workgroups) against 16.8 in two (160); M = 8 17.1 against
+  // 17.2 for the lockstep kernel.
+  if (!forced && xr_x_bytes(d, 1) > kXrLdsMax && d.M <= 8u) {
+    uint32_t best = 0;
+    for (int s = 2; s <= 8; ++s) {
+      if ((uint32_t)s > d.nkb || xr_x_bytes(d, s) > kXrLdsMax) continue;
+      for (int t : {2, 4, 8}) {
+        const int wk = t == 8 ? 4 : 8, u = t == 2 ? 3 : 2;
+        const uint32_t lds = xr_lds_bytes(d, t, wk, s);
+        const uint32_t wgs = total_slabs(d, t) * (uint32_t)s;
+        if (lds > kXrLdsMax || wgs > cus || wgs <= best || total_slabs(d, t) > kMaxCounters) continue;
+        const XrConfig cand{t, u, wk, s, lds, false};
+        if (decode_xr_workspace_bytes(d, cand) > ws_cap) continue;
+        best = wgs;
+        c = cand;
+      }
+    }
+    found = one_round = best > 0;
+  }
   for (int s = 1; s <= 8 && !found; ++s) {
     if ((uint32_t)s > d.nkb || xr_x_bytes(d, s) > kXrLdsMax || (s > 1 && d.M > 4u)) continue;
     for (int t : {1, 2, 4, 8}) {

@@ -126,7 +126,8 @@ def test_workspace_bytes_fused_is_what_the_call_asks_for():
 
 def test_describe_gemm_names_the_kernel_families(monkeypatch):
     assert hq.describe(hq.FORMAT_INT4, hq.DTYPE_F16, 1, 27648, 5120).startswith("hq_decode_xr_kernel<int4,f16,")
-    assert "x 2 pieces" in hq.describe(hq.FORMAT_INT4, hq.DTYPE_F16, 4, 27648, 5120)
+    assert "x 3 pieces" in hq.describe(hq.FORMAT_INT4, hq.DTYPE_F16, 4, 27648, 5120)
+    assert "x 3 pieces" in hq.describe(hq.FORMAT_INT4, hq.DTYPE_F16, 8, 27648, 5120)
     with monkeypatch.context() as m:
         m.setenv("HQ_DECODE_KERNEL", "0")
         assert hq.describe(hq.FORMAT_INT4, hq.DTYPE_F16, 4, 27648, 5120).startswith("hq_decode_kernel<int4,f16,")

@@ -592,7 +592,7 @@ def test_xr_pieces_fused(cuda, fmt, xdt):
         check(y, d.P.reference(), xdt, f"xr pieces fused N={d.P.N}", d.P)
 
 
-@pytest.mark.parametrize("M", [1, 2, 4])
+@pytest.mark.parametrize("M", [1, 2, 4, 8])
 def test_xr_pieces_default_plans(cuda, M):
     # K = 27648, N = 1000: 32 whole slabs would leave most CUs idle (and from M = 3 on the rows
     # of all of K do not fit in LDS); the planner cuts K.
