@@ -98,9 +98,12 @@ size_t hq_packed_words(hq_format fmt, uint32_t K, uint32_t N);
  * column tiles, prefill calls with few output tiles): a 256-byte aligned buffer,
  * zero-filled by the caller before its first use (every call leaves it zero-filled
  * again). Calls sharing one workspace must not overlap in time (same stream, or ordered
- * by events). The value covers calls with and without a bias. For M > 80 it is a bound
- * that holds for every N and segment split; for a fused call with M <= 80 use
- * hq_workspace_bytes_fused, which plans the call's own segment list. Passing NULL instead
+ * by events), and a workspace shared by calls of several shapes needs the largest of their
+ * sizes. The value is exactly what a one-projection call of this shape needs, with or
+ * without a bias; for a fused call use hq_workspace_bytes_fused, which plans the call's own
+ * segment list. Shapes whose operands would span 2 GiB or more (M * K * 2 bytes of X, the
+ * scales, the packed weights) are rejected with HQ_ERR_SHAPE, as the GEMM calls reject them,
+ * since the kernels address each operand with 32-bit offsets. Passing NULL instead
  * makes the library use a buffer of its own per (device, stream), allocated on first need
  * outside stream capture; a call that would need to allocate it during capture fails with
  * HQ_ERR_WORKSPACE. The reference has no workspace: it allocates inside
@@ -249,6 +252,10 @@ hq_status hq_gguf_convert_q4_k(const hq_gguf* g, const char* name, uint32_t* cod
  *   without a bias run the fastest kernels; other groups and biased calls run kernels that
  *   apply one scale (and bias) per 32-wide k chunk.
  * workspace / workspace_bytes: see hq_workspace_bytes (NULL, 0 is always accepted).
+ * Every operand must span less than 2 GiB (M * ldx * 2 bytes of X, M * ldy * 2 of Y, the
+ *   scales, the bias, the packed weights; the kernels address them with 32-bit offsets):
+ *   larger calls fail with HQ_ERR_SHAPE before any device work. (The reference drops a K
+ *   tail silently, marlin_gemm.cu:156-159; this library never returns wrong results.)
  * Up to M = 80 (decode steps, split-fuse steps of decode tokens and a prefill chunk) the
  * HBM-streaming kernels run; larger M the MFMA tile kernel.
  * Results are deterministic: repeated calls with the same shapes give identical bits. */

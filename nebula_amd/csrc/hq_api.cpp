@@ -213,6 +213,32 @@ hq_status check_x(const void* X, int dtype, int64_t ldx, uint32_t K) {
   return HQ_OK;
 }
 
+// Every operand a kernel reads or writes is addressed through a buffer descriptor with 32-bit
+// byte offsets: an operand of 2 GiB or more would wrap, and loads past the wrapped range read
+// zero (silently wrong results), so such calls are rejected. ldx = 0 / ldy = 0: not known yet
+// (the workspace and plan queries check the shape-derived operands only).
+hq_status check_ranges(int fmt, uint32_t M, uint32_t K, uint32_t group, uint32_t N, uint32_t seg, int64_t ldx,
+                       int64_t ldy, bool bias) {
+  constexpr uint64_t kRange = 1ull << 31;
+  const uint64_t rows = K / group, tiles = hq::col_tiles(N);
+  const uint64_t x = (uint64_t)M * (uint64_t)(ldx ? ldx : K) * 2u;
+  const uint64_t y = (uint64_t)M * (uint64_t)(ldy ? ldy : N) * 2u;
+  const uint64_t sc = ((rows - 1u) * N + N) * 2u;
+  const uint64_t w = tiles * (K / hq::kBlockK) * (fmt == HQ_FORMAT_INT4 ? 1024u : 512u);
+  if (x >= kRange)
+    return fail(HQ_ERR_SHAPE, "X spans %llu bytes (M * ldx * 2): operands must stay below 2 GiB", (unsigned long long)x);
+  if (y >= kRange)
+    return fail(HQ_ERR_SHAPE, "segment %u: Y spans %llu bytes (M * ldy * 2): operands must stay below 2 GiB", seg,
+                (unsigned long long)y);
+  if (sc >= kRange || (bias && sc * 2u >= kRange))
+    return fail(HQ_ERR_SHAPE, "segment %u: the scales%s of K=%u, N=%u, group=%u span 2 GiB or more", seg,
+                bias ? " or bias" : "", K, N, group);
+  if (w >= kRange)
+    return fail(HQ_ERR_SHAPE, "segment %u: the packed weights of K=%u, N=%u span %llu bytes (2 GiB or more)", seg, K,
+                N, (unsigned long long)w);
+  return HQ_OK;
+}
+
 hq_status check_segment(const hq_segment& s, uint32_t i) {
   if (!s.Wp || !s.scales || !s.Y) return fail(HQ_ERR_INVALID_ARG, "segment %u: null pointer", i);
   if (s.N == 0) return fail(HQ_ERR_SHAPE, "segment %u: N must be >= 1", i);
@@ -348,6 +374,8 @@ hq_status prepare(const void* X, hq_dtype dtype, int64_t ldx, hq_format fmt, con
   }
   if ((st = check_shape(fmt, M, K, group, bias)) != HQ_OK) return st;
   if ((st = check_x(X, dtype, ldx, K)) != HQ_OK) return st;
+  for (uint32_t i = 0; i < nseg; ++i)
+    if ((st = check_ranges(fmt, M, K, group, Ns[i], i, ldx, segs[i].ldy, segs[i].bias != nullptr)) != HQ_OK) return st;
   hq::GemmDesc d = make_desc(M, K, group, Ns, nseg, bias);
   if (d.gen && !hq::kGeneralKernels)
     return fail(HQ_ERR_UNSUPPORTED, "group=%u%s needs the general kernels, which this build lacks", group,
@@ -543,12 +571,10 @@ hq_status hq_workspace_bytes(hq_format fmt, uint32_t M, uint32_t K, uint32_t N, 
   hq_status st = check_shape(fmt, M, K, group, false);
   if (st != HQ_OK) return st;
   if (N == 0) return fail(HQ_ERR_SHAPE, "N must be >= 1");
+  if ((st = check_ranges(fmt, M, K, group, N, 0, 0, 0, false)) != HQ_OK) return st;
   *bytes = 0;
-  if (M > decode_max_m()) {
-    *bytes = hq::prefill_workspace_bound(fmt, M, K / hq::kBlockK);
-    return ok();
-  }
-  // The larger of the plans without and (int4) with a bias.
+  // The larger of the plans without and (int4) with a bias: exactly what a one-projection call
+  // of this shape needs, at any M.
   for (int b = 0; b < (fmt == HQ_FORMAT_INT4 ? 2 : 1); ++b) {
     const hq::GemmDesc d = make_desc(M, K, group, &N, 1, b != 0);
     *bytes = std::max(*bytes, make_plan(fmt, d).need);
@@ -562,8 +588,10 @@ hq_status hq_workspace_bytes_fused(hq_format fmt, uint32_t M, uint32_t K, uint32
   if (nseg == 0 || nseg > HQ_MAX_SEGMENTS) return fail(HQ_ERR_INVALID_ARG, "need 1..%d segments, got %u", HQ_MAX_SEGMENTS, nseg);
   hq_status st = check_shape(fmt, M, K, group, with_bias != 0);
   if (st != HQ_OK) return st;
-  for (uint32_t i = 0; i < nseg; ++i)
+  for (uint32_t i = 0; i < nseg; ++i) {
     if (Ns[i] == 0) return fail(HQ_ERR_SHAPE, "segment %u: N must be >= 1", i);
+    if ((st = check_ranges(fmt, M, K, group, Ns[i], i, 0, 0, with_bias != 0)) != HQ_OK) return st;
+  }
   *bytes = make_plan(fmt, make_desc(M, K, group, Ns, nseg, with_bias != 0)).need;
   return ok();
 }

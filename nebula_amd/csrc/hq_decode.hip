@@ -955,7 +955,6 @@ hipError_t xr_launch_fd(const GemmDesc& d, const XrConfig& c, void* ws, hipStrea
   switch (c.T * 10 + c.U) {
     case 82: return xr_launch_t<FMT, DT, 8, 2>(d, c, ws, stream);
     case 42: return xr_launch_t<FMT, DT, 4, 2>(d, c, ws, stream);
-    case 43: return xr_launch_t<FMT, DT, 4, 3>(d, c, ws, stream);
     case 23: return xr_launch_t<FMT, DT, 2, 3>(d, c, ws, stream);
     case 24: return xr_launch_t<FMT, DT, 2, 4>(d, c, ws, stream);
     case 14: return xr_launch_t<FMT, DT, 1, 4>(d, c, ws, stream);
@@ -1119,7 +1118,7 @@ XrConfig choose_decode_xr(int fmt, const GemmDesc& d, size_t ws_cap) {
   if (eS >= 1) c.S = eS;
   // Snap to an instantiated (T, U).
   if (c.T == 8) c.U = 2;
-  if (c.T == 4) c.U = std::min(std::max(c.U, 2), 3);
+  if (c.T == 4) c.U = 2;
   if (c.T == 2) c.U = std::min(std::max(c.U, 3), 4);
   if (c.T == 1) c.U = c.U >= 6 ? 6 : 4;
   c.WK = std::max(1, std::min(c.WK, xr_max_wk(c.T)));

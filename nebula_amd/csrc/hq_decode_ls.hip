@@ -47,6 +47,7 @@
 
 #include <algorithm>
 #include <cstdlib>
+#include <utility>
 
 #include "hq_device.hpp"
 #include "hq_internal.hpp"
@@ -81,8 +82,17 @@ __device__ __forceinline__ u4 ls_load_b128(__amdgpu_buffer_rsrc_t r, uint32_t vo
   asm volatile("buffer_load_dwordx4 %0, %1, %2, %3 offen" : "=v"(v) : "v"(voff), "s"(r), "s"(soff));
   return v;
 }
-__device__ __forceinline__ void ls_lds_write_b128(uint32_t addr, const u4& v) {
-  asm volatile("ds_write_b128 %0, %1" ::"v"(addr), "v"(v) : "memory");
+// 16 bytes to LDS at addr + OFF (the instruction's 16-bit offset field): one address register
+// serves several writes.
+template <uint32_t OFF>
+__device__ __forceinline__ void ls_lds_write_b128_at(uint32_t addr, const u4& v) {
+  static_assert(OFF < 65536u, "ds offset field");
+  asm volatile("ds_write_b128 %0, %1 offset:%2" ::"v"(addr), "v"(v), "i"(OFF) : "memory");
+}
+// Ring slot v[0 .. XL) of activation loads to addr + 1024 x.
+template <int... X>
+__device__ __forceinline__ void ls_lds_write_rows(uint32_t addr, const u4* v, std::integer_sequence<int, X...>) {
+  (ls_lds_write_b128_at<1024u * X>(addr, v[X]), ...);
 }
 __device__ __forceinline__ u4 ls_lds_read_b128(uint32_t addr) {
   u4 v;
@@ -169,7 +179,7 @@ __global__ void __launch_bounds__(64 * KG * GW, KG == 1 && MT > 1 ? 2 : 1)
   // left the LDS latency exposed MT times per step). Measured on MI355X: ternary 5120 x 34816
   // at M = 80 61.4 -> 52.9 us, 5120 x 14336 31.6 -> 28.6 us. Not for int4 bf16 at five row
   // tiles, whose correction chains would not fit in 256 VGPRs beside the fragments.
-  constexpr bool kAllA = !GEN && MT > 1 && (kFold || !kInt4 || MT <= 4);
+  constexpr bool kAllA = !GEN && MT > 1 && (kFold || !kInt4 || MT <= 4) && !(BAL && (MT == 5 || (kInt4 && DT == HQ_DTYPE_BF16 && MT == 4)));
   // Ternary fragments from 64-bit shifts of the word pair (dq_tern2_pair) up to three row
   // tiles, and at four outside the balanced grid; beyond, the register pairs the shifts need
   // made the kernel spill.
@@ -270,13 +280,14 @@ __global__ void __launch_bounds__(64 * KG * GW, KG == 1 && MT > 1 ? 2 : 1)
   // k-group's stage slot.
   const __amdgpu_buffer_rsrc_t xr = make_rsrc(d.X, M * (uint32_t)d.ldx * 2u);
   const uint32_t xs0 = (uint32_t)(uintptr_t)xs + kg * kXStage;
-  uint32_t xvo[XL], xwo[XL];
+  uint32_t xvo[XL];
 #pragma unroll
   for (int x = 0; x < XL; ++x) {
     const uint32_t xrow = 4u * (XL * wi + x) + g4;
     xvo[x] = xrow < M ? xrow * (uint32_t)d.ldx * 2u + ((c16 ^ (xrow & 15u)) * 16u) : kOutOfRange;
-    xwo[x] = xs0 + (XL * wi + x) * 1024u + lane * 16u;
   }
+  // LDS address of load x: xwo + x * 1024 (the write's offset field carries x * 1024).
+  const uint32_t xwo = xs0 + XL * wi * 1024u + lane * 16u;
   // A fragment of row tile r, chunk c: row 16 r + c16, 16-byte piece 4c + g4, at
   // r * 4096 + c16 * 256 + 16 * (piece ^ c16).
   uint32_t xro[4];
@@ -463,6 +474,22 @@ __global__ void __launch_bounds__(64 * KG * GW, KG == 1 && MT > 1 ? 2 : 1)
     }
     float sc[T];
     float gs_[GEN ? T : 1][4], ge_[GEN ? T : 1][4];  // GEN: scale and e = 8 s + b of (tile, chunk)
+    if constexpr (GEN) {
+      // The scale and bias bits become floats before the row tiles: the permuted bits then die
+      // (at five row tiles of bf16 they kept the kernel two registers past 256).
+      ls_wait_lgkmcnt0();
+#pragma unroll
+      for (int t = 0; t < T; ++t)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          ls_tie(gsb[t][c]);
+          ls_tie(gbb[t][c]);
+          float sv = f16_to_f32((uint16_t)gsb[t][c]);
+          if constexpr (!kInt4) sv = __builtin_isfinite(sv) ? 0.5f * sv : 0.0f;  // fields hold 2t
+          gs_[t][c] = sv;
+          ge_[t][c] = has_bias ? __builtin_fmaf(8.0f, sv, __builtin_bit_cast(float, gbb[t][c])) : 0.0f;
+        }
+    }
 #pragma unroll
     for (int r = 0; r < MT; ++r) {
       u4 xf[4];
@@ -472,19 +499,6 @@ __global__ void __launch_bounds__(64 * KG * GW, KG == 1 && MT > 1 ? 2 : 1)
 #pragma unroll
       for (int c = 0; c < 4; ++c) ls_tie(xf[c]);
       if constexpr (GEN) {
-        if (r == 0) {
-#pragma unroll
-          for (int t = 0; t < T; ++t)
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-              ls_tie(gsb[t][c]);
-              ls_tie(gbb[t][c]);
-              float sv = f16_to_f32((uint16_t)gsb[t][c]);
-              if constexpr (!kInt4) sv = __builtin_isfinite(sv) ? 0.5f * sv : 0.0f;  // fields hold 2t
-              gs_[t][c] = sv;
-              ge_[t][c] = has_bias ? __builtin_fmaf(8.0f, sv, __builtin_bit_cast(float, gbb[t][c])) : 0.0f;
-            }
-        }
         // Per chunk: the tiles' sums x (q - 8) (or x 2t), scaled, and the row sum times e.
 #pragma unroll
         for (int c = 0; c < 4; ++c) {
@@ -591,8 +605,7 @@ __global__ void __launch_bounds__(64 * KG * GW, KG == 1 && MT > 1 ? 2 : 1)
 #pragma unroll
         for (int x = 0; x < XL; ++x) ls_tie(xring[s][x]);
         issue((s + U) % R, i + s + U);
-#pragma unroll
-        for (int x = 0; x < XL; ++x) ls_lds_write_b128(xwo[x] + st * kStep, xring[s][x]);
+        ls_lds_write_rows(xwo + st * kStep, xring[s], std::make_integer_sequence<int, XL>{});
         kgroup_barrier();  // every wavefront's activation rows of step i + s are in LDS
         if constexpr (kAllA) compute_all(s, st);
         else compute(s, st);

@@ -161,9 +161,6 @@ PrefillConfig choose_prefill(int fmt, const GemmDesc& d, size_t ws_cap = SIZE_MA
 // Workspace bytes of a prefill call (0 without stream-K): the counter area, then two fp32
 // partial tiles per stream-K workgroup.
 size_t prefill_workspace_bytes(const GemmDesc& d, const PrefillConfig& c);
-// Upper bound of prefill_workspace_bytes over every N and segment split for this M and
-// K / 128 (what hq_workspace_bytes reports for M > 16).
-size_t prefill_workspace_bound(int fmt, uint32_t M, uint32_t nkb);
 // Prefill (M > 16): MFMA tile kernel.
 hipError_t launch_prefill(int fmt, int dtype, const PrefillConfig& c, void* ws, hipStream_t stream);
 

@@ -650,11 +650,8 @@ int env_int(const char* name, int dflt) {
 // (two row waves, one workgroup per CU) by 3-8% from M = 512 to 4096.
 void prefill_shape(uint32_t M, int& RT, int& WM) {
   const int eWM = env_int("HQ_PREFILL_WM", 0);  // tuning override: 128 (1) or 256 (2) rows
-  const int eRT = env_int("HQ_PREFILL_RT", 0);  // tuning override: 4 = 64 rows, 16 = 256 rows, one row wave
-  if (eRT == 16 && M > 128) {
-    RT = 16;
-    WM = 1;
-  } else if (eRT == 4) {
+  const int eRT = env_int("HQ_PREFILL_RT", 0);  // tuning override: 4 = 64 rows
+  if (eRT == 4) {
     RT = 4;
     WM = 1;
   } else if (eWM == 1 || eWM == 2) {
@@ -674,15 +671,13 @@ void prefill_shape(uint32_t M, int& RT, int& WM) {
 int prefill_slots(int fmt, int RT, int WM) {
   int occ = 1;
   if (fmt == HQ_FORMAT_INT4) {
-    occ = RT == 4    ? prefill_occupancy<HQ_FORMAT_INT4, HQ_DTYPE_F16, 4, 1>()
-          : RT == 16 ? prefill_occupancy<HQ_FORMAT_INT4, HQ_DTYPE_F16, 16, 1>()
-                     : (WM == 1 ? prefill_occupancy<HQ_FORMAT_INT4, HQ_DTYPE_F16, 8, 1>()
-                                : prefill_occupancy<HQ_FORMAT_INT4, HQ_DTYPE_F16, 8, 2>());
+    occ = RT == 4 ? prefill_occupancy<HQ_FORMAT_INT4, HQ_DTYPE_F16, 4, 1>()
+                  : (WM == 1 ? prefill_occupancy<HQ_FORMAT_INT4, HQ_DTYPE_F16, 8, 1>()
+                             : prefill_occupancy<HQ_FORMAT_INT4, HQ_DTYPE_F16, 8, 2>());
   } else {
-    occ = RT == 4    ? prefill_occupancy<HQ_FORMAT_TERNARY2, HQ_DTYPE_F16, 4, 1>()
-          : RT == 16 ? prefill_occupancy<HQ_FORMAT_TERNARY2, HQ_DTYPE_F16, 16, 1>()
-                     : (WM == 1 ? prefill_occupancy<HQ_FORMAT_TERNARY2, HQ_DTYPE_F16, 8, 1>()
-                                : prefill_occupancy<HQ_FORMAT_TERNARY2, HQ_DTYPE_F16, 8, 2>());
+    occ = RT == 4 ? prefill_occupancy<HQ_FORMAT_TERNARY2, HQ_DTYPE_F16, 4, 1>()
+                  : (WM == 1 ? prefill_occupancy<HQ_FORMAT_TERNARY2, HQ_DTYPE_F16, 8, 1>()
+                             : prefill_occupancy<HQ_FORMAT_TERNARY2, HQ_DTYPE_F16, 8, 2>());
   }
   return cu_count() * occ;
 }
@@ -692,7 +687,6 @@ hipError_t launch_fd(const PrefillLaunch& c, void* ws, hipStream_t stream) {
   if (c.d.gen) return c.RT == 4 && c.WM == 1 ? launch_rt<FMT, DT, 4, 1, true>(c, ws, stream) : hipErrorInvalidConfiguration;
   if (c.KS == 2) return c.RT == 8 && c.WM == 1 ? launch_ks2<FMT, DT>(c, stream) : hipErrorInvalidConfiguration;
   if (c.RT == 4) return launch_rt<FMT, DT, 4, 1>(c, ws, stream);
-  if (c.RT == 16) return launch_rt<FMT, DT, 16, 1>(c, ws, stream);
   if (c.WM == 1) return launch_rt<FMT, DT, 8, 1>(c, ws, stream);
   return launch_rt<FMT, DT, 8, 2>(c, ws, stream);
 }
@@ -859,17 +853,6 @@ size_t prefill_workspace_bytes(const GemmDesc& d, const PrefillConfig& c) {
     if (c.l[i].psk)
       b = std::max(b, kCounterBytes + (size_t)c.l[i].psk * 2u * (16u * c.l[i].RT * c.l[i].WM) * 256u * sizeof(float));
   return b;
-}
-
-// Stream-K grids never exceed the workgroup slots (unless forced by HQ_PREFILL_PSK).
-size_t prefill_workspace_bound(int fmt, uint32_t M, uint32_t nkb) {
-  if (env_int("HQ_PREFILL_SK", 1) == 0 || nkb < 8u) return 0;
-  int RT = 8, WM = 2;
-  prefill_shape(M, RT, WM);
-  size_t b = (size_t)prefill_slots(fmt, RT, WM) * 2u * (16u * RT * WM) * 256u * sizeof(float);
-  if (RT == 8 && WM == 1)  // choose_prefill may take 64-row tiles instead
-    b = std::max(b, (size_t)prefill_slots(fmt, 4, 1) * 2u * 64u * 256u * sizeof(float));
-  return kCounterBytes + b;
 }
 
 hipError_t launch_prefill(int fmt, int dtype, const PrefillConfig& c, void* ws, hipStream_t stream) {

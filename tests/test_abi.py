@@ -74,17 +74,23 @@ def test_workspace_bytes():
         biased = workspace_bytes_fused(hq.FORMAT_INT4, M, 27648, [5120], bias=1)[1]
         assert workspace_bytes(hq.FORMAT_INT4, M, 27648, 5120) == (hq.HQ_OK, max(plain, biased))
     # Up to M = 80 the streaming kernel runs (row tiles of 16): its partials grow with the
-    # row tiles. Prefill shapes (M > 80) report one bound for every N: the counter area plus
-    # two fp32 tiles of 128 rows per concurrent workgroup (or 64-row ones, whichever is
-    # more); K < 1024 is never split along K and needs none.
+    # row tiles.
     _, d16 = workspace_bytes(hq.FORMAT_INT4, 16, 4096, 4096)
     _, d80 = workspace_bytes(hq.FORMAT_INT4, 80, 4096, 4096)
     assert d16 > 65536 and d80 - 65536 == 5 * (d16 - 65536)
-    st, p81 = workspace_bytes(hq.FORMAT_INT4, 81, 4096, 4096)
-    _, p2048 = workspace_bytes(hq.FORMAT_TERNARY2, 2048, 5120, 27648)
-    assert st == hq.HQ_OK and p81 > 65536 and (p81 - 65536) % (2 * 64 * 256 * 4) == 0
-    assert p2048 == p81 and (p2048 - 65536) % (2 * 128 * 256 * 4) == 0
-    assert workspace_bytes(hq.FORMAT_TERNARY2, 2048, 5120, 16) == (hq.HQ_OK, p2048)
+    # Prefill shapes (M > 80) too get exactly what the call asks for (with or without a bias):
+    # grids of whole tiles need none, stream-K grids the counter area plus two fp32 partial
+    # tiles per stream-K workgroup; K < 1024 is never split along K.
+    for fmt, M, K, N in [(hq.FORMAT_INT4, 81, 4096, 4096), (hq.FORMAT_INT4, 300, 5120, 16),
+                         (hq.FORMAT_TERNARY2, 2048, 5120, 27648), (hq.FORMAT_TERNARY2, 2048, 5120, 16),
+                         (hq.FORMAT_INT4, 1024, 5120, 7168), (hq.FORMAT_INT4, 2048, 896, 4096)]:
+        exact = workspace_bytes_fused(fmt, M, K, [N])[1]
+        if fmt == hq.FORMAT_INT4:
+            exact = max(exact, workspace_bytes_fused(fmt, M, K, [N], bias=1)[1])
+        assert workspace_bytes(fmt, M, K, N) == (hq.HQ_OK, exact), (fmt, M, K, N)
+    assert workspace_bytes(hq.FORMAT_TERNARY2, 2048, 5120, 27648) == (hq.HQ_OK, 0)  # 1728 whole tiles
+    _, p16 = workspace_bytes(hq.FORMAT_TERNARY2, 2048, 5120, 16)  # 32 tiles on 256 stream-K workgroups
+    assert p16 > 65536 and (p16 - 65536) % (2 * 64 * 256 * 4) == 0
     assert workspace_bytes(hq.FORMAT_INT4, 2048, 896, 4096) == (hq.HQ_OK, 0)
     # Groups that are multiples of 32 are sized (the general kernels), bad shapes reported.
     assert workspace_bytes(hq.FORMAT_INT4, 16, 4096, 4096, group=64)[0] == hq.HQ_OK
@@ -187,6 +193,43 @@ def test_gemm_rejects_bad_arguments(kw, status):
     for fn in ("hq_gemm_w4a16", "hq_gemm_w2a16"):
         assert call_gemm(fn=fn, **kw) == status
         assert hq.lib().hq_last_error().decode()
+
+
+# Operands of 2 GiB or more: the kernels address every operand with 32-bit byte offsets, so
+# the entry points reject such shapes (HQ_ERR_SHAPE, no device work) instead of reading zeros
+# past the wrapped range.
+@pytest.mark.parametrize("kw,what", [
+    (dict(M=16, ldx=1 << 26), "X spans"),                                  # 16 * 2^26 * 2 = 2 GiB
+    (dict(M=16, ldy=1 << 26), "Y spans"),
+    (dict(M=1, K=4096, N=1 << 26, ldy=1 << 26), "scales"),                 # 32 rows * 2^26 * 2 B
+    (dict(M=1, K=1 << 16, ldx=1 << 16, N=1 << 16, ldy=1 << 16), "packed weights"),  # 2^12 tiles * 512 * 1 KiB
+])
+def test_gemm_rejects_operands_beyond_32_bit_offsets(kw, what):
+    assert call_gemm(**kw) == hq.HQ_ERR_SHAPE
+    assert what in hq.lib().hq_last_error().decode()
+    # One below each limit passes validation (and fails later only for the fake pointers).
+    if what == "X spans":
+        assert call_gemm(M=16, ldx=(1 << 26) - 8) != hq.HQ_ERR_SHAPE
+    if what == "packed weights":  # ternary packs half the bytes: the same shape is in range
+        assert call_gemm(fn="hq_gemm_w2a16", **kw) != hq.HQ_ERR_SHAPE
+        assert call_gemm(fn="hq_gemm_w2a16", M=1, K=1 << 16, ldx=1 << 16, N=1 << 17, ldy=1 << 17) == hq.HQ_ERR_SHAPE
+
+
+def test_range_limits_in_bias_fused_and_workspace_queries():
+    L = hq.lib()
+    # (The packed weights, K N / 2 or K N / 4 bytes, outgrow the scales and a bias, 2 or 4 K N /
+    # group bytes, first for every group >= 32.)
+    assert call_gemm(M=1, K=4096, N=1 << 26, ldy=1 << 26, bias=0x5000) == hq.HQ_ERR_SHAPE
+    segs = (hq.Segment * 2)()
+    segs[0] = hq.Segment(0x2000, 0x3000, None, 0x4000, 64, 64)
+    segs[1] = hq.Segment(0x2000, 0x3000, None, 0x4000, 1 << 26, 1 << 26)
+    assert L.hq_gemm_fused(0x1000, 1, 4096, 1, segs, 2, 1, 4096, 128, None, 0, None) == hq.HQ_ERR_SHAPE
+    assert "segment 1" in L.hq_last_error().decode()
+    assert L.hq_gemm_fused_noalloc(0x1000, 1, 4096, 1, segs, 2, 1, 4096, 128, None) == hq.HQ_ERR_SHAPE
+    assert workspace_bytes(hq.FORMAT_INT4, 1, 1 << 16, 1 << 16)[0] == hq.HQ_ERR_SHAPE
+    assert workspace_bytes(hq.FORMAT_TERNARY2, 1, 1 << 16, 1 << 16)[0] == hq.HQ_OK
+    assert workspace_bytes(hq.FORMAT_INT4, 1 << 15, 1 << 15, 64)[0] == hq.HQ_ERR_SHAPE  # X: 2^31 bytes
+    assert workspace_bytes_fused(hq.FORMAT_INT4, 1, 4096, [64, 1 << 26])[0] == hq.HQ_ERR_SHAPE
 
 
 def test_bias_validation():
