@@ -85,11 +85,15 @@ def check(y, X, W, s, what):
 @pytest.mark.parametrize("M", [1, 3, 8, 16])
 @pytest.mark.parametrize("K,N", [(128, 40), (1024, 1000), (5120, 5120), (4096, 4096), (27648, 512), (5120, 27648)])
 def test_w8a8_default_plans(cuda, M, K, N):
-    if K * N > 5120 * 5120 and M not in (1, 8):
-        pytest.skip("large shapes at M = 1 and 8 only (oracle time)")
     X, W, s = problem(M, K, N, M * 7 + K + N)
     y = run(X, W, s)
-    check(y, X, W, s, f"M={M} K={K} N={N}")
+    if K * N > 5120 * 5120 and M not in (1, 8):
+        # The call runs all M rows; the oracle checks the first, a middle and the last one (an
+        # output row depends only on its own activation row; row 0 holds the special values).
+        rows = sorted({0, M // 2, M - 1})
+        check(y[rows], X[rows], W, s, f"M={M} K={K} N={N} rows {rows}")
+    else:
+        check(y, X, W, s, f"M={M} K={K} N={N}")
 
 
 # Forced decompositions: slab widths, wavefront counts (some without k-blocks), K pieces
