@@ -7,8 +7,10 @@ Workload (one "step"): the W4A16 decode sweep, group 128, fp16 activations,
 (GB/s). Every launch reads a weight copy that no launch of the previous ~640 MiB read
 (copies rotate per launch over >= 640 MiB per shape), so the 256 MiB Infinity Cache cannot
 serve them. Steps are replayed as HIP graphs, which keeps host launch cost off the GPU
-timeline; inputs are resident in HBM before the timed region. The default 50 warm-up steps
-bring the GPU to its steady clocks (after 5, the first timed steps ran up to 5% slower).
+timeline; inputs are resident in HBM before the timed region. After the warm-up steps,
+untimed steps continue until 100 ms of them have run (the "settle" entry), whatever --warmup
+is: the clock reaches its steady state only under lasting load (after 5 warm-up steps alone
+the first timed steps ran up to 5% slower).
 
 The same JSON line also carries:
   cases         per launch shape: average launch duration (HIP events on the launch stream
@@ -16,7 +18,7 @@ The same JSON line also carries:
                 GB/s and fraction of the 8 TB/s HBM peak, and the plan (kernel, tiling) that
                 ran. The decode sweep's 15 shapes, the single W4A16 GEMM (M=16, K=N=4096),
                 the ternary bf16 decode (K=5120, N=27648, M in {1, 8}) and the int8 path
-                (fp32 activations, int8 weights, K=5120, N=27648, M in {1, 8}; bytes = int8
+                (fp32 activations, int8 weights, K=5120, N=27648, M in {1, 8, 16}; bytes = int8
                 weights + fp32 scales);
   roofline      the dominant decode kernel (the kernel with the largest share of the step
                 time): its algorithmic bytes (packed weights + scales) per launch / its
@@ -38,7 +40,9 @@ The same JSON line also carries:
 
 Usage:
   python bench.py [--gpus 1] [--steps 100] [--warmup 50] [--no-cpu] [--no-prefill] [--no-traffic] [--no-ceiling]
-  python bench.py --roofline-only --case K N M  # one decode shape only (for rocprofv3 --pmc)
+  (after the warm-up steps, untimed decode steps run until 100 ms have passed: the "settle"
+  entry of the JSON line; the clock needs lasting load to reach its steady state)
+  python bench.py --roofline-only --case K N M [--case-fmt ternary]  # one decode shape (rocprofv3 --pmc)
   python bench.py --copy-bytes 268435456        # a plain device copy of known size (counter calibration)
   python bench.py --prefill-only 2048           # W4A16 prefill M=2048, K=5120, N=27648 only (for counters)
 """
@@ -66,6 +70,8 @@ SHAPES = [(5120, 5120), (5120, 27648), (27648, 5120)]
 MS = [1, 2, 4, 8, 16]
 GROUP = 128
 ROTATE_BYTES = 640 << 20  # per shape, > 2x the 256 MiB MALL
+SETTLE_MS = 100.0         # untimed decode steps run before the timed region, whatever --warmup is
+BACKLOG = 10              # untimed steps queued right ahead of the timed region's start event
 COPY_BYTES = 268435456    # counter calibration copy
 FMT_INT4, FMT_TERN = 1, 2
 
@@ -115,6 +121,7 @@ def graph_time_us(torch, stream, launches, reps: int = 3) -> float:
     torch.cuda.synchronize()
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(stream):
+        g.replay()  # queued ahead of the start event: the GPU is busy when the timing starts
         a.record(stream)
         for _ in range(reps):
             g.replay()
@@ -147,16 +154,18 @@ def kernel_of(plan: str) -> str:
 
 
 # ---------------------------------------------------------------- single-purpose runs (profilers)
-def run_case_only(torch, hq, K: int, N: int, M: int):
-    copies = n_copies(K, N)
-    ws, ss = make_weights(hq, torch, K, N, copies)
-    X = torch.randn((M, K), device="cuda").to(torch.float16)
-    Y = torch.empty((M, N), device="cuda", dtype=torch.float16)
+def run_case_only(torch, hq, K: int, N: int, M: int, ternary: bool = False):
+    """One decode shape: int4 with fp16 activations, or ternary with bf16 ones."""
+    fmt, dt, tdt = (FMT_TERN, 2, torch.bfloat16) if ternary else (FMT_INT4, 1, torch.float16)
+    copies = n_copies(K, N, fmt)
+    ws, ss = make_weights(hq, torch, K, N, copies, fmt)
+    X = torch.randn((M, K), device="cuda").to(tdt)
+    Y = torch.empty((M, N), device="cuda", dtype=tdt)
     torch.cuda.synchronize()
     for r in range(4 * copies):
-        hq.gemm(FMT_INT4, X, ws[r % copies], ss[r % copies], N, GROUP, out=Y)
+        hq.gemm(fmt, X, ws[r % copies], ss[r % copies], N, GROUP, out=Y)
     torch.cuda.synchronize()
-    log(f"case-only: {4 * copies} launches of K={K} N={N} M={M}: {hq.describe(FMT_INT4, 1, M, K, N)}")
+    log(f"case-only: {4 * copies} launches of K={K} N={N} M={M}: {hq.describe(fmt, dt, M, K, N)}")
 
 
 def run_prefill_only(torch, hq, M: int):
@@ -231,14 +240,28 @@ def measure_traffic(K: int, N: int, M: int, kernel: str):
 STREAM_TOOL = ROOT / "nebula_amd" / "bin" / "hq_stream_ceiling"
 
 
-def stream_ceiling(value: float):
+def case_bytes(key: str) -> int:
+    """Algorithmic bytes of one launch of a decode case of the JSON line (0 for other cases)."""
+    if key.startswith("K"):
+        K, N = (int(x[1:]) for x in key.split("_")[:2])
+        return wbytes(K, N)
+    if key.startswith("single_"):
+        return wbytes(4096, 4096)
+    if key.startswith("ternary_"):
+        K, N = (int(x[1:]) for x in key.split("_")[2:4])
+        return wbytes(K, N, FMT_TERN)
+    return 0
+
+
+def stream_ceiling(value: float, cases=None):
     """The practical read ceiling of each decode launch size on this device, measured in this
     run by nebula_amd/bin/hq_stream_ceiling (the fastest of several launch shapes of a kernel
-    that only reads the bytes once, HIP-graph timed over rotating buffers), and the decode
-    sweep's rate if every launch ran at that ceiling."""
+    that only reads the bytes once, HIP-graph timed over rotating buffers), the decode sweep's
+    rate if every launch ran at that ceiling, and each decode case's time over its ceiling
+    (the sweep's three sizes, the single 4096 x 4096 GEMM and the ternary launch)."""
     if not STREAM_TOOL.exists():
         return {"note": f"{STREAM_TOOL.relative_to(ROOT)} not built (run __graft_entry__.build())"}
-    sizes = sorted({wbytes(K, N) for K, N in SHAPES})
+    sizes = sorted({wbytes(K, N) for K, N in SHAPES} | {wbytes(4096, 4096), wbytes(5120, 27648, FMT_TERN)})
     p = subprocess.run(["timeout", "-k", "10", "120", str(STREAM_TOOL), *map(str, sizes)], capture_output=True, text=True)
     if p.returncode != 0:
         return {"note": f"hq_stream_ceiling exited {p.returncode}: {p.stderr[-300:]}"}
@@ -249,8 +272,10 @@ def stream_ceiling(value: float):
     step_bytes = sum(wbytes(K, N) for K, N in SHAPES for _ in MS)
     sweep = step_bytes / step_us / 1e3
     log(f"stream ceiling: {per}; sweep at the ceiling {sweep:.1f} GB/s ({100 * sweep / HBM_PEAK_GBS:.1f}% of peak)")
+    over = {k: round(c["us"] / per[str(case_bytes(k))]["us"], 3) for k, c in (cases or {}).items()
+            if str(case_bytes(k)) in per}
     return {"per_launch": per, "sweep_GBps": round(sweep, 1), "sweep_frac_hbm": round(sweep / HBM_PEAK_GBS, 3),
-            "value_over_ceiling": round(value / sweep, 3),
+            "value_over_ceiling": round(value / sweep, 3), "case_over_ceiling": over,
             "note": "per decode launch size: the fastest plain read of those bytes (grid-stride 16-byte loads, "
                     "1-8 workgroups of 256 threads per CU, unroll 2-8), launch cost included"}
 
@@ -303,13 +328,35 @@ def run_gpu(args):
     for i in range(args.warmup):
         graphs[i % R].replay()
     torch.cuda.synchronize()
+    # Settle: the clock reaches its steady state only after the load has lasted (after 5 warm-up
+    # steps the first timed steps ran up to 5% slower), so untimed steps continue until SETTLE_MS
+    # of them have run, whatever --warmup is; the JSON line reports how many. The copy rotation
+    # continues across the warm-up, the settle and the timed steps.
+    settle_steps, t0 = 0, time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < SETTLE_MS:
+        for i in range(10):
+            graphs[(args.warmup + settle_steps + i) % R].replay()
+        settle_steps += 10
+        torch.cuda.synchronize()
+    settle_ms = (time.perf_counter() - t0) * 1e3
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(stream):
+        # A backlog of BACKLOG untimed steps queued ahead of the start event: a pause of the host
+        # between two replays then never idles the GPU inside the timed region (with an empty
+        # queue a 20-step region measured up to 25% slow on one box).
+        for i in range(BACKLOG):
+            graphs[(args.warmup + settle_steps + i) % R].replay()
+        settle_steps += BACKLOG
+        base = args.warmup + settle_steps
         e0.record(stream)
         for i in range(args.steps):
-            graphs[i % R].replay()
+            graphs[(base + i) % R].replay()
         e1.record(stream)
     torch.cuda.synchronize()
+    settle = {"ms": round(settle_ms, 1), "steps": settle_steps,
+              "note": f"untimed decode steps after the {args.warmup} warm-up steps: until {SETTLE_MS:.0f} ms had run, "
+                      f"then {BACKLOG} queued ahead of the timed region"}
+    log(f"settle: {settle_steps} steps ({settle['ms']} ms, then {BACKLOG} queued)")
     ms_per_step = e0.elapsed_time(e1) / args.steps
     value = step_bytes / (ms_per_step * 1e-3) / 1e9
     log(f"decode sweep: {ms_per_step * 1e3:.1f} us/step, {value:.1f} GB/s")
@@ -378,9 +425,9 @@ def run_gpu(args):
     w8 = [packed.cuda() for _ in range(copies)]
     del packed
     s8 = torch.rand(N, device="cuda") * 0.1 + 0.05
-    X8 = torch.randn((8, K), device="cuda") * 0.5
-    Y8 = torch.empty((8, N), device="cuda")
-    for M in (1, 8):
+    X8 = torch.randn((16, K), device="cuda") * 0.5
+    Y8 = torch.empty((16, N), device="cuda")
+    for M in (1, 8, 16):
         def launches(M=M):
             reps = copies * max(1, 64 // copies)
             for r in range(reps):
@@ -390,7 +437,8 @@ def run_gpu(args):
         gbs = (K * N + N * 4) / (us * 1e-6) / 1e9
         cases[f"int8_w8a8_K{K}_N{N}_M{M}"] = {"us": round(us, 2), "GBps": round(gbs, 1),
                                              "pct_hbm": round(100 * gbs / HBM_PEAK_GBS, 1),
-                                             "plan": "hq_quantize_x_kernel + hq_w8a8_kernel (two launches)"}
+                                             "plan": "hq_gemm_w8a8: hq_w8a8_kernel, after hq_quantize_x_kernel "
+                                                     "unless it quantises its own rows (one launch)"}
         log(f"int8 K={K} N={N} M={M}: {us:.2f} us, {gbs:.0f} GB/s")
     del w8
     torch.cuda.empty_cache()
@@ -522,7 +570,7 @@ def run_gpu(args):
     # Token-by-token prefill (the reference runs prompt tokens one at a time) against one call.
     layer_res["prefill_512_speedup_vs_token_by_token"] = round(512 * layer_res["M1"]["us"] / layer_res["M512"]["us"], 1)
     del layer
-    return value, ms_per_step, roofline, cases, prefill, tq1, layer_res
+    return value, ms_per_step, settle, roofline, cases, prefill, tq1, layer_res
 
 
 # ---------------------------------------------------------------- CPU baseline
@@ -595,6 +643,8 @@ def main():
     ap.add_argument("--cpu-reps", type=int, default=5)
     ap.add_argument("--roofline-only", action="store_true")
     ap.add_argument("--case", type=int, nargs=3, default=[5120, 27648, 16], metavar=("K", "N", "M"))
+    ap.add_argument("--case-fmt", choices=["int4", "ternary"], default="int4",
+                    help="--roofline-only: int4 weights with fp16 activations, or ternary with bf16 ones")
     ap.add_argument("--copy-bytes", type=int, default=0)
     ap.add_argument("--prefill-only", type=int, default=0)
     args = ap.parse_args()
@@ -612,10 +662,10 @@ def main():
         elif args.prefill_only:
             run_prefill_only(torch, hq, args.prefill_only)
         else:
-            run_case_only(torch, hq, *args.case)
+            run_case_only(torch, hq, *args.case, ternary=args.case_fmt == "ternary")
         return
-    value, ms_per_step, roofline, cases, prefill, tq1, layer_res = run_gpu(args)
-    ceiling = None if args.no_ceiling else stream_ceiling(value)
+    value, ms_per_step, settle, roofline, cases, prefill, tq1, layer_res = run_gpu(args)
+    ceiling = None if args.no_ceiling else stream_ceiling(value, cases)
     if not args.no_traffic:
         K, N, M = (int(x[1:]) for x in roofline["traffic_case"].split("_"))
         roofline["traffic"], roofline["traffic_note"] = measure_traffic(K, N, M, roofline["kernel"])
@@ -628,6 +678,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "settle": settle,
         "ms_per_step": round(ms_per_step, 4),
         "higher_is_better": True,
         "scaling": "weak",
