@@ -3,21 +3,24 @@
 // Replaces kernel_marlin_gemm_int4_templated / _dynamic
 // (hydrogen/src/model/marlin_gemm.cu:130-237, 242-322). The reference gives each
 // thread one output column and does 32 x M scalar FMAs per 16-byte weight load,
-// then merges 16 fixed K-splits with fp32 atomics into a pre-zeroed Y. Here:
-//   * the work is cut into units of (slab of T column tiles) x (128-deep k-block) and
-//     every workgroup streams an equal contiguous range of units (hq_plan.hpp), so all
-//     CUs finish together whatever N and K are; slabs cut by a range boundary are
-//     completed by a last-arriver fix-up through the workspace, in workgroup order;
-//   * inside a workgroup the WK wavefronts take the units of each slab in turn
-//     (unit j -> wavefront j mod WK), each with U k-blocks of weights, scales and
-//     activations in flight in a register ring, and meet only once, at the end, to sum
-//     their per-slab results through LDS in wavefront order;
-//   * weights are dequantised in registers straight into MFMA B fragments and
-//     multiplied against the activation rows (M padded to 16) with
-//     v_mfma_f32_16x16x32_{f16,bf16}. int4 uses the biased form (magic + q, one
-//     v_and_or_b32 per fragment word) and removes the bias with one extra MFMA per
-//     chunk whose result seeds every tile's accumulator;
-//   * the group scale multiplies the fp32 k-block sum once per (column, k-block).
+// then merges 16 fixed K-splits with fp32 atomics into a pre-zeroed Y. Two kernels here,
+// both dequantising weights in registers straight into MFMA B fragments multiplied
+// against the activation rows (M padded to 16) with v_mfma_f32_16x16x32_{f16,bf16}; int4 uses
+// the biased form (magic + q, one v_and_or_b32 per fragment word) and removes the bias with
+// one extra MFMA per chunk whose result seeds every tile's accumulator; the group scale
+// multiplies the fp32 k-block sum once per (column, k-block).
+//   * hq_decode_xr_kernel, the default for M <= 16: one workgroup per (slab of T column
+//     tiles, piece of K); the piece's activation rows are copied into LDS once, then the
+//     wavefronts stream the slab's weights through a barrier-free register ring and meet
+//     once, at the end, in LDS (pieces of a slab: a last-arriver fix-up in piece order);
+//   * hq_decode_kernel, the per-wavefront kernel, at up to four rows when the X-resident
+//     kernel has no plan (rows too long even in eight pieces, or pieces beyond a workspace
+//     cap) and when tests force it: the work is cut into units of
+//     (slab of T column tiles) x (128-deep k-block) and every workgroup streams an equal
+//     contiguous range of units (hq_plan.hpp); inside a workgroup the WK wavefronts take the
+//     units of each slab in turn, each with U k-blocks of weights, scales and activations in
+//     flight in a register ring, and meet once to sum their per-slab results through LDS;
+//     slabs cut by a range boundary are completed by a last-arriver fix-up in workgroup order.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
