@@ -166,10 +166,17 @@ bool use_resident(int fmt, const hq::GemmDesc& d, size_t cap, hq::XrConfig* c) {
   return c->ok;
 }
 
-// Slabs of T tiles over the segments of d (the X-resident grid).
-uint32_t xr_slabs(const hq::GemmDesc& d, int T) {
-  uint32_t g = 0;
-  for (uint32_t i = 0; i < d.nseg; ++i) g += (d.seg[i].ntiles + T - 1) / T;
+// Slabs of the X-resident grid over the segments of d (up to T tiles each; at least G in
+// all when G > 0, as hq::assign_slabs cuts them).
+uint32_t xr_slabs(const hq::GemmDesc& d, int T, uint32_t G) {
+  uint32_t tiles = 0, g = 0;
+  for (uint32_t i = 0; i < d.nseg; ++i) tiles += d.seg[i].ntiles;
+  for (uint32_t i = 0; i < d.nseg; ++i) {
+    const uint32_t nt = d.seg[i].ntiles;
+    uint32_t ns = (nt + T - 1) / T;
+    if (G) ns = std::max<uint32_t>(ns, (uint32_t)(((uint64_t)G * nt + tiles - 1) / tiles));
+    g += std::min(ns, nt);
+  }
   return g;
 }
 
@@ -486,7 +493,7 @@ std::string describe(int fmt, int dtype, const hq::GemmDesc& d, const Plan& p) {
   if (p.kind == Kind::kResident) {
     std::snprintf(b, sizeof b,
                   "hq_decode_xr_kernel<%s,%s,T=%d,U=%d> workgroups=%u slabs x %d pieces x %d wavefronts lds=%u ws=%zu",
-                  fmt_name(fmt), dt_name(dtype), p.xc.T, p.xc.U, xr_slabs(d, p.xc.T), p.xc.S, p.xc.WK, p.xc.lds,
+                  fmt_name(fmt), dt_name(dtype), p.xc.T, p.xc.U, xr_slabs(d, p.xc.T, p.xc.G), p.xc.S, p.xc.WK, p.xc.lds,
                   p.need);
   } else if (p.kind == Kind::kDecode) {
     std::snprintf(b, sizeof b, "hq_decode_kernel<%s,%s,T=%d,U=%d> workgroups=%d x %d wavefronts%s%s ws=%zu",

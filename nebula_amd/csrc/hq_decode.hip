@@ -557,11 +557,16 @@ __global__ void __launch_bounds__(64 * xr_max_wk(T)) hq_decode_xr_kernel(const G
     u4 a[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) a[c] = *reinterpret_cast<const u4*>(xs + xa[c] + kbl * 256u);
+    // Ternary: a non-finite group scale drops the group, checked once per loaded scale
+    // (before it is handed to the lanes of its tiles) and replaced by +0.
+    uint32_t sl[kSL];
+#pragma unroll
+    for (int jj = 0; jj < kSL; ++jj)
+      sl[jj] = kInt4 || (sr[u][jj] & 0x7C00u) != 0x7C00u ? sr[u][jj] : 0u;
     uint32_t sbits[T];
 #pragma unroll
     for (int t = 0; t < T; ++t)
-      sbits[t] = T == 1 ? sr[u][0]
-                        : (uint32_t)__builtin_amdgcn_ds_bpermute((int)((16u * (t % 4) + c16) * 4u), (int)sr[u][t / 4]);
+      sbits[t] = T == 1 ? sl[0] : (uint32_t)__builtin_amdgcn_ds_bpermute((int)((16u * (t % 4) + c16) * 4u), (int)sl[t / 4]);
     f4 seed = f4{0.f, 0.f, 0.f, 0.f};
     if constexpr (kInt4) {
 #pragma unroll
@@ -593,8 +598,8 @@ __global__ void __launch_bounds__(64 * xr_max_wk(T)) hq_decode_xr_kernel(const G
     }
 #pragma unroll
     for (int t = 0; t < T; ++t) {
-      float sc = f16_to_f32((uint16_t)sbits[t]);
-      if constexpr (!kInt4) sc = __builtin_isfinite(sc) ? 0.5f * sc : 0.0f;  // fields hold 2t; non-finite drops
+      // Ternary fields hold 2t: the sums are halved once after the loop (exact).
+      const float sc = f16_to_f32((uint16_t)sbits[t]);
 #pragma unroll
       for (int v = 0; v < 4; ++v) acc[t][v] = __builtin_fmaf(gs[t][v], sc, acc[t][v]);
     }
@@ -610,6 +615,14 @@ __global__ void __launch_bounds__(64 * xr_max_wk(T)) hq_decode_xr_kernel(const G
   // Loads past this wavefront's k-blocks read nothing; retire them before the registers
   // and the LDS are reused.
   __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  if constexpr (!kInt4) {
+    // Halving commutes with fp32 rounding (no overflow or underflow at these magnitudes), so
+    // this equals scaling every term by s / 2.
+#pragma unroll
+    for (int t = 0; t < T; ++t)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[t][v] *= 0.5f;
+  }
 
   // 3. Reduction: park each wavefront's sums (rows < M) over the activation rows, then
   //    sum them in wavefront order, four consecutive columns per thread.
@@ -918,7 +931,7 @@ uint32_t xr_lds_bytes(const GemmDesc& d, int T, int WK, int S) {
 template <int FMT, int DT, int T, int U>
 hipError_t xr_launch_t(GemmDesc d, const XrConfig& c, void* ws, hipStream_t stream) {
   if (c.WK < 1 || c.WK > xr_max_wk(T) || d.M > 16u || c.S < 1 || (uint32_t)c.S > d.nkb) return hipErrorInvalidValue;
-  const uint32_t G = assign_slabs(d, T, 0);
+  const uint32_t G = assign_slabs(d, T, c.G);
   XrPlan pl{};
   pl.S = (uint32_t)c.S;
   pl.kq = d.nkb / pl.S;
@@ -1024,7 +1037,7 @@ static int xr_waves_per_simd(int fmt, int T, int U) {
 // 8.8-9.1 us, int4 bf16 14.4-14.8 -> 10.2-10.9, 5120 x 10240 and 16384 7-15% faster), and at
 // five to eight rows the 4-tile slabs still fit two workgroups per CU and win (M = 5, 8:
 // 15.5-16.3 against 16.6-17.7 us; ternary bf16 M = 8: 13.5 against 15.0).
-// HQ_XR_T / _WK / _U / _S override (tuning and tests).
+// HQ_XR_T / _WK / _U / _S / _G (slab count) override (tuning and tests).
 XrConfig choose_decode_xr(int fmt, const GemmDesc& d, size_t ws_cap) {
   XrConfig c{2, 3, 8, 1, 0, false};
   if (d.M > 16u || d.gen) return c;
@@ -1032,8 +1045,8 @@ XrConfig choose_decode_xr(int fmt, const GemmDesc& d, size_t ws_cap) {
   uint32_t tiles = 0;
   for (uint32_t i = 0; i < d.nseg; ++i) tiles += d.seg[i].ntiles;
   const int eT = env_int("HQ_XR_T", 0), eWK = env_int("HQ_XR_WK", 0), eU = env_int("HQ_XR_U", 0);
-  const int eS = env_int("HQ_XR_S", 0);
-  const bool forced = eT || eWK || eU || eS;
+  const int eS = env_int("HQ_XR_S", 0), eG = env_int("HQ_XR_G", 0);
+  const bool forced = eT || eWK || eU || eS || eG;
   bool found = false, one_round = false;
   // Rows of all of K that do not fit in LDS (long K) at up to eight rows: K pieces, the
   // one-round grid (at most one workgroup per CU) that keeps the most CUs busy, the fewest
@@ -1119,6 +1132,7 @@ XrConfig choose_decode_xr(int fmt, const GemmDesc& d, size_t ws_cap) {
   if (eWK >= 1) c.WK = eWK;
   if (eU >= 2) c.U = eU;
   if (eS >= 1) c.S = eS;
+  if (eG >= 1) c.G = (uint32_t)eG;
   // Snap to an instantiated (T, U).
   if (c.T == 8) c.U = 2;
   if (c.T == 4) c.U = 2;
@@ -1126,7 +1140,8 @@ XrConfig choose_decode_xr(int fmt, const GemmDesc& d, size_t ws_cap) {
   if (c.T == 1) c.U = c.U >= 6 ? 6 : 4;
   c.WK = std::max(1, std::min(c.WK, xr_max_wk(c.T)));
   c.S = std::max(1, std::min<int>(c.S, (int)d.nkb));
-  if (c.S > 1 && (total_slabs(d, c.T) > kMaxCounters || decode_xr_workspace_bytes(d, c) > ws_cap)) return c;
+  if (c.G && total_slabs(d, c.T, c.G) > 65535u) return c;
+  if (c.S > 1 && (total_slabs(d, c.T, c.G) > kMaxCounters || decode_xr_workspace_bytes(d, c) > ws_cap)) return c;
   c.lds = xr_lds_bytes(d, c.T, c.WK, c.S);
   c.ok = c.lds <= kXrLdsMax;
   return c;
@@ -1134,7 +1149,7 @@ XrConfig choose_decode_xr(int fmt, const GemmDesc& d, size_t ws_cap) {
 
 size_t decode_xr_workspace_bytes(const GemmDesc& d, const XrConfig& c) {
   if (c.S <= 1) return 0;
-  return kCounterBytes + (size_t)total_slabs(d, c.T) * (size_t)c.S * d.M * 16u * (size_t)c.T * 4u;
+  return kCounterBytes + (size_t)total_slabs(d, c.T, c.G) * (size_t)c.S * d.M * 16u * (size_t)c.T * 4u;
 }
 
 hipError_t launch_decode_xr(int fmt, int dtype, GemmDesc d, const XrConfig& c, void* ws, hipStream_t stream) {

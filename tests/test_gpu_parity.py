@@ -460,7 +460,8 @@ def test_lockstep_matches_per_wavefront(cuda, M):
 # ---------------------------------------------------------------- X-resident decode kernel
 class xr_env(decode_env):
     """Force the X-resident decode kernel (activation rows in LDS) and its tiling for a block:
-    slab width T, wavefronts WK (splitting the slab's k-blocks), ring depth U."""
+    slab width T, wavefronts WK (splitting the slab's k-blocks), ring depth U, pieces S, slab
+    count G (slabs of fewer than T tiles)."""
 
     def __init__(self, **kv):
         self.kv = {f"HQ_XR_{k}": str(v) for k, v in kv.items()}
@@ -511,6 +512,22 @@ def test_xr_fused(cuda, T):
         outs = hq.gemm_fused(O.INT4, devs[0].X, [(d.Wp, d.S, d.P.N) for d in devs])
     for d, y in zip(devs, outs):
         check(y, d.P.reference(), O.F16, f"xr fused T={T} N={d.P.N}", d.P)
+
+
+@pytest.mark.parametrize("fmt,xdt", [(O.INT4, O.F16), (O.TERNARY2, O.BF16)])
+@pytest.mark.parametrize("T,G,WK", [(4, 30, 4), (8, 20, 8), (2, 50, 8)])
+def test_xr_variable_width_slabs(cuda, fmt, xdt, T, G, WK):
+    # A slab count above ceil(tiles / T) (HQ_XR_G) cuts slabs of fewer than T tiles, of two
+    # widths: 63 tiles in 30 slabs of 2-3 tiles (T = 4), 20 of 3-4 (T = 8), 50 of 1-2 (T = 2).
+    # The missing tiles' loads read nothing and their columns are never stored.
+    M, K, N = 5, 2048, 1000
+    P = O.Problem(fmt, M, K, N, 128, xdt, seed=3520 + T)
+    D = DeviceProblem(P)
+    with xr_env(T=T, G=G, WK=WK):
+        desc = hq.describe(fmt, xdt, M, K, N)
+        assert desc.startswith("hq_decode_xr_kernel<") and f",T={T}," in desc and f"workgroups={G} slabs" in desc, desc
+        y = D.run()
+    check(y, P.reference(), xdt, f"xr variable slabs T={T} G={G}", P)
 
 
 @pytest.mark.parametrize("M,K", [(16, 5120), (8, 5120), (3, 5120), (2, 27648), (1, 27648)])
