@@ -357,11 +357,14 @@ bool take_fault() {
 }
 hq_status fault_status() {
   return fail(HQ_ERR_DEVICE,
-              "a lockstep decode launch gave up waiting at its k-group barrier: the outputs of that launch "
-              "are wrong (fault word reported by the device)");
+              "a launch gave up waiting at a k-group barrier (the lockstep decode kernel's k-groups, or the "
+              "two K halves of a prefill tile): the outputs of that launch are wrong (fault word reported by "
+              "the device)");
 }
 uint32_t ls_spin() {
-  const char* v = std::getenv("HQ_DECODE_LS_SPIN");  // tests: a small limit forces the fault path
+  // Polls of the kernels' bounded barriers (lockstep k-groups, prefill K halves); tests: a
+  // small limit forces the fault path.
+  const char* v = std::getenv("HQ_DECODE_LS_SPIN");
   return v && *v ? (uint32_t)std::strtoul(v, nullptr, 10) : hq::kLsSpinLimit;
 }
 
@@ -403,7 +406,7 @@ hq_status prepare(const void* X, hq_dtype dtype, int64_t ldx, hq_format fmt, con
 hq_status launch_plan(int fmt, int dtype, const hq::GemmDesc& d, const Plan& p, void* w, uint32_t* fault,
                       hipStream_t s) {
   switch (p.kind) {
-    case Kind::kPrefill: return from_hip(hq::launch_prefill(fmt, dtype, p.pc, w, s), "prefill launch");
+    case Kind::kPrefill: return from_hip(hq::launch_prefill(fmt, dtype, p.pc, w, fault, ls_spin(), s), "prefill launch");
     case Kind::kLockstep:
       return from_hip(hq::launch_decode_ls(fmt, dtype, d, p.lc, w, fault, ls_spin(), s), "decode launch");
     case Kind::kResident: return from_hip(hq::launch_decode_xr(fmt, dtype, d, p.xc, w, s), "decode launch");

@@ -163,7 +163,9 @@ PrefillConfig choose_prefill(int fmt, const GemmDesc& d, size_t ws_cap = SIZE_MA
 // partial tiles per stream-K workgroup.
 size_t prefill_workspace_bytes(const GemmDesc& d, const PrefillConfig& c);
 // Prefill (M > 16): MFMA tile kernel.
-hipError_t launch_prefill(int fmt, int dtype, const PrefillConfig& c, void* ws, hipStream_t stream);
+// fault / spin: the fault word and the poll bound of the K halves' barrier (KS = 2 launches).
+hipError_t launch_prefill(int fmt, int dtype, const PrefillConfig& c, void* ws, uint32_t* fault, uint32_t spin,
+                          hipStream_t stream);
 
 // Whether this build has the general kernels (a bias, groups that are multiples of 32 but
 // not of 128); without them such calls fail with HQ_ERR_UNSUPPORTED.

@@ -77,6 +77,8 @@ struct PrefillPlan {
   uint32_t gb;      // whole tiles are visited in groups of gb row bands, column-block major
   float* part;      // [psk][2][tile] fp32 partial tiles (null when psk == 0)
   uint32_t* cnt;    // [tiles - dp] arrival counters, zero between launches
+  uint32_t* fault;  // host-visible word set to 1 when a bounded wait gives up (may be null)
+  uint32_t spin;    // polls before the K halves' k-block barrier gives up (KS = 2)
 };
 
 // Exact u / d for any 32-bit u without a divide instruction: m = floor((2^32 - 1) / d)

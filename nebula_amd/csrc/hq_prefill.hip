@@ -158,6 +158,41 @@ __global__ void __launch_bounds__(256 * WM * KS, WM == 1 && RT == 8 && KS == 1 ?
 
   const uint32_t bid = blockIdx.x;
 
+  // KS = 2: the two K halves meet separately at every k-block, so that the wavefronts sharing
+  // a SIMD (one per half) drift apart and hide each other's waits (a workgroup barrier kept
+  // them in step: the fused QKV tile ran at half the MFMA rate of two independent workgroups
+  // on a CU). A half's barrier is an LDS arrival count (sh_last[kh]): each wavefront adds one
+  // once its own copies of the k-block have landed and its reads of the previous stage are
+  // done, and waits until the half's four have arrived. The wait is bounded: every wavefront
+  // of a half executes the same steps, so a correct launch never reaches the bound; one that
+  // gives up sets the host-visible fault word (reported as HQ_ERR_DEVICE) and carries on.
+  uint32_t arrivals = 0;
+  const uint32_t harr = (uint32_t)(uintptr_t)(sh_last + kh);
+  if constexpr (KS > 1) {
+    if (threadIdx.x < 2u) sh_last[threadIdx.x] = 0u;
+    __syncthreads();
+  }
+  auto kblock_barrier = [&]() {
+    if constexpr (KS == 1) {
+      __syncthreads();
+    } else {
+      arrivals += 4u;
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      if (lane == 0) asm volatile("ds_add_u32 %0, %1" ::"v"(harr), "v"(1u) : "memory");
+      bool met = false;
+      for (uint32_t spin = 0; spin < pp.spin; ++spin) {
+        uint32_t got;
+        asm volatile("ds_read_b32 %0, %1\n\ts_waitcnt lgkmcnt(0)" : "=v"(got) : "v"(harr) : "memory");
+        if (__builtin_amdgcn_readfirstlane(got) >= arrivals) {
+          met = true;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+      }
+      if (!met && lane == 0 && pp.fault) __hip_atomic_store(pp.fault, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+    }
+  };
+
   // The wave's RT activation load instructions per k-block (BM / 4 in all): instruction i
   // fills LDS rows 4q..4q+3, q = wave * RT + i; lane -> row 4q + g4, 16-byte slot c16
   // holding unit c16 ^ (row & 15). The k-block goes in the uniform offset; the row stays
@@ -317,7 +352,7 @@ __global__ void __launch_bounds__(256 * WM * KS, WM == 1 && RT == 8 && KS == 1 ?
     constexpr int kBLoads = (GEN ? 3 : 2) * kTilesPerWave;  // weight, scale (and bias) loads per k-block
     auto step = [&](uint32_t kb, int slot) {
       __builtin_amdgcn_s_waitcnt(vmcnt_imm((kRing - 2) * kBLoads));  // A(kb), B(kb) landed for this wave
-      __syncthreads();                                            // ... for every wave; stage (kb+1)&1 is free
+      kblock_barrier();  // ... for every wave (of the half); stage (kb+1)&1 is free
       load_a((kb + 1) & 1u, kb + 1);
       load_b((slot + kRing - 1) % kRing, kb + kRing - 1);
       // Keep this step's loads ahead of its compute: vmcnt retires in issue order, so a load
@@ -620,9 +655,11 @@ hipError_t launch_rt(const PrefillLaunch& c, void* ws, hipStream_t stream) {
 
 // Whole 128-row tiles with the K split inside the workgroup (KS = 2): one tile per workgroup.
 template <int FMT, int DT>
-hipError_t launch_ks2(const PrefillLaunch& c, hipStream_t stream) {
+hipError_t launch_ks2(const PrefillLaunch& c, uint32_t* fault, uint32_t spin, hipStream_t stream) {
   GemmDesc d = c.d;
   PrefillPlan pp{};
+  pp.fault = fault;
+  pp.spin = spin;
   pp.nb = assign_blocks(d);
   if ((d.M + 127u) / 128u * pp.nb != c.tiles || c.psk != 0 || c.dp != c.tiles || d.nkb % 2u != 0 || d.nkb < 2u)
     return hipErrorInvalidValue;
@@ -683,9 +720,9 @@ int prefill_slots(int fmt, int RT, int WM) {
 }
 
 template <int FMT, int DT>
-hipError_t launch_fd(const PrefillLaunch& c, void* ws, hipStream_t stream) {
+hipError_t launch_fd(const PrefillLaunch& c, void* ws, uint32_t* fault, uint32_t spin, hipStream_t stream) {
   if (c.d.gen) return c.RT == 4 && c.WM == 1 ? launch_rt<FMT, DT, 4, 1, true>(c, ws, stream) : hipErrorInvalidConfiguration;
-  if (c.KS == 2) return c.RT == 8 && c.WM == 1 ? launch_ks2<FMT, DT>(c, stream) : hipErrorInvalidConfiguration;
+  if (c.KS == 2) return c.RT == 8 && c.WM == 1 ? launch_ks2<FMT, DT>(c, fault, spin, stream) : hipErrorInvalidConfiguration;
   if (c.RT == 4) return launch_rt<FMT, DT, 4, 1>(c, ws, stream);
   if (c.WM == 1) return launch_rt<FMT, DT, 8, 1>(c, ws, stream);
   return launch_rt<FMT, DT, 8, 2>(c, ws, stream);
@@ -855,16 +892,17 @@ size_t prefill_workspace_bytes(const GemmDesc& d, const PrefillConfig& c) {
   return b;
 }
 
-hipError_t launch_prefill(int fmt, int dtype, const PrefillConfig& c, void* ws, hipStream_t stream) {
+hipError_t launch_prefill(int fmt, int dtype, const PrefillConfig& c, void* ws, uint32_t* fault, uint32_t spin,
+                          hipStream_t stream) {
   for (int i = 0; i < c.n; ++i) {
     const PrefillLaunch& l = c.l[i];
     hipError_t e;
     if (fmt == HQ_FORMAT_INT4)
-      e = dtype == HQ_DTYPE_F16 ? launch_fd<HQ_FORMAT_INT4, HQ_DTYPE_F16>(l, ws, stream)
-                                : launch_fd<HQ_FORMAT_INT4, HQ_DTYPE_BF16>(l, ws, stream);
+      e = dtype == HQ_DTYPE_F16 ? launch_fd<HQ_FORMAT_INT4, HQ_DTYPE_F16>(l, ws, fault, spin, stream)
+                                : launch_fd<HQ_FORMAT_INT4, HQ_DTYPE_BF16>(l, ws, fault, spin, stream);
     else
-      e = dtype == HQ_DTYPE_F16 ? launch_fd<HQ_FORMAT_TERNARY2, HQ_DTYPE_F16>(l, ws, stream)
-                                : launch_fd<HQ_FORMAT_TERNARY2, HQ_DTYPE_BF16>(l, ws, stream);
+      e = dtype == HQ_DTYPE_F16 ? launch_fd<HQ_FORMAT_TERNARY2, HQ_DTYPE_F16>(l, ws, fault, spin, stream)
+                                : launch_fd<HQ_FORMAT_TERNARY2, HQ_DTYPE_BF16>(l, ws, fault, spin, stream);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
