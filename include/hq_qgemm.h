@@ -120,7 +120,8 @@ hq_status hq_workspace_bytes_fused(hq_format fmt, uint32_t M, uint32_t K, uint32
 hq_status hq_describe_gemm(hq_format fmt, hq_dtype dtype, uint32_t M, uint32_t K, uint32_t N,
                            uint32_t group, int with_bias, char* buf, size_t buf_len);
 /* Faults that kernels report after their launch returned: a bounded wait inside a kernel
- * (the lockstep decode kernel's k-group barrier) that gave up sets a host-visible fault
+ * (the lockstep decode kernel's k-group barrier, the barrier of a prefill tile's two K
+ * halves) that gave up sets a host-visible fault
  * word, and that launch's outputs are wrong. This call waits for `stream`, then returns
  * HQ_ERR_DEVICE (and clears the word) if one was reported since the last check, HQ_OK
  * otherwise. Every hq_gemm_* call also checks the word first and fails with HQ_ERR_DEVICE
