@@ -493,7 +493,14 @@ int decode_ring(int T, int U) {
 
 std::string describe(int fmt, int dtype, const hq::GemmDesc& d, const Plan& p) {
   char b[512];
-  if (p.kind == Kind::kResident) {
+  if (p.kind == Kind::kResident && p.xc.SG > 1) {
+    const uint32_t slabs = xr_slabs(d, p.xc.T, p.xc.G);
+    std::snprintf(b, sizeof b,
+                  "hq_decode_xr_kernel<%s,%s,T=%d,U=%d,SG=%d> workgroups=%u of %d slabs (%u slabs) x %d pieces x %d "
+                  "wavefronts per slab lds=%u ws=%zu",
+                  fmt_name(fmt), dt_name(dtype), p.xc.T, p.xc.U, p.xc.SG, (slabs + p.xc.SG - 1) / p.xc.SG, p.xc.SG,
+                  slabs, p.xc.S, p.xc.WK, p.xc.lds, p.need);
+  } else if (p.kind == Kind::kResident) {
     std::snprintf(b, sizeof b,
                   "hq_decode_xr_kernel<%s,%s,T=%d,U=%d> workgroups=%u slabs x %d pieces x %d wavefronts lds=%u ws=%zu",
                   fmt_name(fmt), dt_name(dtype), p.xc.T, p.xc.U, xr_slabs(d, p.xc.T, p.xc.G), p.xc.S, p.xc.WK, p.xc.lds,

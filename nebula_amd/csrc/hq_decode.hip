@@ -10,9 +10,10 @@
 // one extra MFMA per chunk whose result seeds every tile's accumulator; the group scale
 // multiplies the fp32 k-block sum once per (column, k-block).
 //   * hq_decode_xr_kernel, the default for M <= 16: one workgroup per (slab of T column
-//     tiles, piece of K); the piece's activation rows are copied into LDS once, then the
-//     wavefronts stream the slab's weights through a barrier-free register ring and meet
-//     once, at the end, in LDS (pieces of a slab: a last-arriver fix-up in piece order);
+//     tiles, piece of K), or per pair of whole slabs; the piece's activation rows are copied
+//     into LDS once, then the wavefronts stream the slab's weights through a barrier-free
+//     register ring and meet once, at the end, in LDS (pieces of a slab: a last-arriver
+//     fix-up in piece order);
 //   * hq_decode_kernel, the per-wavefront kernel, at up to four rows when the X-resident
 //     kernel has no plan (rows too long even in eight pieces, or pieces beyond a workspace
 //     cap) and when tests force it: the work is cut into units of
@@ -422,6 +423,9 @@ __global__ void __launch_bounds__(64 * max_wk(T)) hq_decode_kernel(const GemmDes
 // order (deterministic), after the activation rows are no longer needed. With S > 1 pieces
 // per slab each workgroup stores its partial tile to the workspace and the last of the
 // slab's workgroups to arrive (per-slab counter) sums the S partials in piece order.
+// Slab groups (GRP, whole slabs only): a workgroup of SG groups of WK wavefronts, group h
+// streaming slab blockIdx.x + h * gridDim.x over the one copy of the rows, so that a CU that
+// would hold two workgroups copies the rows once and starts both streams at once.
 //
 // LDS layout of the activation rows of a piece of nkbp k-blocks from kb0: 16-byte units,
 // unit (r * nkbp + kb - kb0) * 16 + (j ^ r) holds elements 8 j .. 8 j + 7 of k-block kb of
@@ -430,7 +434,7 @@ __global__ void __launch_bounds__(64 * max_wk(T)) hq_decode_kernel(const GemmDes
 // in every group of 16 lanes, i.e. every bank once. Lanes of rows >= M read row M - 1:
 // an MFMA output row depends only on its own A row, and rows >= M are never stored.
 struct XrPlan {
-  uint32_t wk;       // wavefronts per workgroup
+  uint32_t wk;       // wavefronts per slab (per slab group)
   uint32_t S;        // pieces per slab (grid y)
   uint32_t kq, kr;   // piece p covers k-blocks [p * kq + min(p, kr), ...), kq + (p < kr) of them
   uint32_t m_lo;     // plan_div_magic(16 * kq)
@@ -438,11 +442,14 @@ struct XrPlan {
   uint32_t gmul;     // plan_gmul(gkb)
   uint32_t* cnt;     // [G] arrival counters, zero between launches (S > 1)
   float* part;       // [G][S][M * 16 * T] partial tiles (S > 1)
+  uint32_t sg;       // slab groups per workgroup (S = 1): group h of workgroup b takes slab b + h * gridDim.x
+  uint32_t nslabs;   // slabs over all segments
 };
 
 constexpr int xr_max_wk(int T) { return T >= 8 ? 8 : 16; }
 
-template <int FMT, int DT, int T, int U, bool FUSED>
+// GRP: slab groups (pl.sg of them per workgroup); without it one slab per workgroup.
+template <int FMT, int DT, int T, int U, bool FUSED, bool GRP = false>
 __global__ void __launch_bounds__(64 * xr_max_wk(T)) hq_decode_xr_kernel(const GemmDesc d, const XrPlan pl) {
   using W = typename WTraits<FMT>::V;
   constexpr uint32_t WPL = WTraits<FMT>::wpl;
@@ -457,19 +464,28 @@ __global__ void __launch_bounds__(64 * xr_max_wk(T)) hq_decode_xr_kernel(const G
   const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t c16 = lane & 15u;
   const uint32_t g4 = lane >> 4;
-  const uint32_t g = blockIdx.x;  // slab
   const uint32_t p = blockIdx.y;  // piece
   // Every scalar the prologue needs, read from the kernel arguments in one batch: the empty
   // asm uses them all, so the loads issue together and are waited for once (left to itself
   // the compiler waited for the plan fields, then the shape, then the activation pointer:
   // three round trips before the first copy, 0.2-0.3 us on 5120 x 5120).
-  const uint32_t WK = pl.wk, nkb = d.nkb, M = d.M, gkb = d.gkb, ldx = (uint32_t)d.ldx;
+  const uint32_t WK = pl.wk, SG = GRP ? pl.sg : 1u, nkb = d.nkb, M = d.M, gkb = d.gkb, ldx = (uint32_t)d.ldx;
   const uint32_t kq = pl.kq, kr = pl.kr, m_lo = pl.m_lo, m_hi = pl.m_hi, gmul = pl.gmul;
   const void* const Xp = d.X;
-  asm volatile("" ::"s"(WK), "s"(nkb), "s"(M), "s"(gkb), "s"(ldx), "s"(kq), "s"(kr), "s"(m_lo), "s"(m_hi),
-               "s"(gmul), "s"(Xp));
+  asm volatile("" ::"s"(WK), "s"(SG), "s"(nkb), "s"(M), "s"(gkb), "s"(ldx), "s"(kq), "s"(kr), "s"(m_lo),
+               "s"(m_hi), "s"(gmul), "s"(Xp));
   const uint32_t kb0 = p * kq + min(p, kr);
   const uint32_t nkbp = kq + (p < kr ? 1u : 0u);
+  // Slab groups: the workgroup's SG * WK wavefronts are SG groups of WK, group h streaming
+  // slab blockIdx.x + h * gridDim.x over the one copy of the activation rows (wi: the
+  // wavefront within its group). A group past the last slab loads and stores nothing.
+  uint32_t h = 0;
+  if constexpr (GRP)
+    while (h + 1u < SG && wave >= (h + 1u) * WK) ++h;
+  const uint32_t wi = wave - h * WK;
+  const uint32_t graw = blockIdx.x + h * gridDim.x;
+  const bool gl = !GRP || graw < pl.nslabs;
+  const uint32_t g = gl ? graw : pl.nslabs - 1u;  // slab
 
   uint32_t s = 0;
   if constexpr (FUSED) {
@@ -491,7 +507,7 @@ __global__ void __launch_bounds__(64 * xr_max_wk(T)) hq_decode_xr_kernel(const G
     const uint32_t nkb16 = nkbp * 16u;
     const uint32_t m16 = p < kr ? m_hi : m_lo;
     const uint32_t nq = (M * nkb16 + 63u) / 64u;
-    for (uint32_t q = wave; q < nq; q += WK) {
+    for (uint32_t q = wave; q < nq; q += WK * SG) {
       const uint32_t u = q * 64u + lane;
       const uint32_t r = plan_div(u, nkb16, m16);
       const uint32_t rem = u - r * nkb16;
@@ -503,8 +519,8 @@ __global__ void __launch_bounds__(64 * xr_max_wk(T)) hq_decode_xr_kernel(const G
   // The ring's first loads must be issued after the copies (vmcnt retires in order).
   __builtin_amdgcn_sched_barrier(0);
 
-  // 2. Weight ring: step j of this wavefront is k-block kb = kb0 + wave + j * WK, T tiles.
-  const uint32_t nj = wave < nkbp ? (nkbp - wave + WK - 1u) / WK : 0u;
+  // 2. Weight ring: step j of this wavefront is k-block kb = kb0 + wi + j * WK, T tiles.
+  const uint32_t nj = gl && wi < nkbp ? (nkbp - wi + WK - 1u) / WK : 0u;
   const __amdgpu_buffer_rsrc_t wrs =
       make_rsrc(sg.Wp + (size_t)ct0 * nkb * 64u * WPL, __builtin_amdgcn_readfirstlane(nv * nkb * kBlockBytes));
   const __amdgpu_buffer_rsrc_t srs = make_rsrc(sg.S, __builtin_amdgcn_readfirstlane(((nkb / gkb - 1u) * sg.lds + N) * 2u));
@@ -520,7 +536,7 @@ __global__ void __launch_bounds__(64 * xr_max_wk(T)) hq_decode_xr_kernel(const G
   uint32_t sr[U][kSL];
   auto load = [&](int slot, uint32_t j) {
     const bool live = j < nj;
-    const uint32_t kb = kb0 + wave + j * WK;
+    const uint32_t kb = kb0 + wi + j * WK;
     const uint32_t kbo = __builtin_amdgcn_readfirstlane(live ? kb * kBlockBytes : 0u);
     const uint32_t so = __builtin_amdgcn_readfirstlane(live ? plan_group_of_kb(kb, gmul) * lsrow : 0u);
 #pragma unroll
@@ -553,7 +569,7 @@ __global__ void __launch_bounds__(64 * xr_max_wk(T)) hq_decode_xr_kernel(const G
   for (int t = 0; t < T; ++t) acc[t] = f4{0.f, 0.f, 0.f, 0.f};
 
   auto compute = [&](int u, uint32_t j) {
-    const uint32_t kbl = wave + j * WK;  // k-block within the piece
+    const uint32_t kbl = wi + j * WK;  // k-block within the piece
     u4 a[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) a[c] = *reinterpret_cast<const u4*>(xs + xa[c] + kbl * 256u);
@@ -639,13 +655,15 @@ __global__ void __launch_bounds__(64 * xr_max_wk(T)) hq_decode_xr_kernel(const G
   __syncthreads();
   const uint32_t col0 = ct0 * 16u, ncols = nv * 16u;
   const uint32_t nthr = WK * 64u;
+  const uint32_t tg = threadIdx.x - h * nthr;  // thread within the slab group
+  red += h * WK * SL;                          // the group's parked sums
   // Workspace partials, accessed 16 bytes at a time with the sc1 cache policy: agent-coherent
   // (visible across XCDs once the store has completed).
   constexpr int kCoherent = 16;
   const uint32_t S = pl.S;
   const __amdgpu_buffer_rsrc_t partr = make_rsrc(pl.part, S > 1u ? gridDim.x * S * SL * 4u : 0u);
   if (S > 1u) {
-    for (uint32_t o4 = threadIdx.x; o4 < SL / 4u; o4 += nthr) {
+    for (uint32_t o4 = tg; o4 < SL / 4u; o4 += nthr) {
       f4 v = f4{0.f, 0.f, 0.f, 0.f};
       for (uint32_t w = 0; w < WK; ++w) v += *reinterpret_cast<const f4*>(red + w * SL + 4u * o4);
       __builtin_amdgcn_raw_buffer_store_b128(v, partr, ((g * S + p) * SL + 4u * o4) * 4u, 0, kCoherent);
@@ -665,7 +683,8 @@ __global__ void __launch_bounds__(64 * xr_max_wk(T)) hq_decode_xr_kernel(const G
     __syncthreads();
     if (*flag == 0u) return;
   }
-  for (uint32_t o4 = threadIdx.x; o4 < SL / 4u; o4 += nthr) {
+  if (!gl) return;
+  for (uint32_t o4 = tg; o4 < SL / 4u; o4 += nthr) {
     f4 v = f4{0.f, 0.f, 0.f, 0.f};
     if (S > 1u) {
       for (uint32_t q = 0; q < S; ++q)  // pieces in order
@@ -922,16 +941,19 @@ uint32_t xr_x_bytes(const GemmDesc& d, int S) {
   return (d.M * nkbp * 16u + 63u) / 64u * 1024u;
 }
 
-uint32_t xr_lds_bytes(const GemmDesc& d, int T, int WK, int S) {
+uint32_t xr_lds_bytes(const GemmDesc& d, int T, int WK, int S, int SG = 1) {
   const uint32_t x = xr_x_bytes(d, S);
-  const uint32_t red = (uint32_t)WK * d.M * 16u * (uint32_t)T * 4u;
+  const uint32_t red = (uint32_t)(WK * SG) * d.M * 16u * (uint32_t)T * 4u;
   return std::max(x, red);
 }
 
-template <int FMT, int DT, int T, int U>
+template <int FMT, int DT, int T, int U, bool GRP = false>
 hipError_t xr_launch_t(GemmDesc d, const XrConfig& c, void* ws, hipStream_t stream) {
-  if (c.WK < 1 || c.WK > xr_max_wk(T) || d.M > 16u || c.S < 1 || (uint32_t)c.S > d.nkb) return hipErrorInvalidValue;
+  if (c.WK < 1 || c.SG < 1 || c.WK * c.SG > xr_max_wk(T) || d.M > 16u || c.S < 1 || (uint32_t)c.S > d.nkb ||
+      (c.SG > 1 && (c.S > 1 || !GRP)))
+    return hipErrorInvalidValue;
   const uint32_t G = assign_slabs(d, T, c.G);
+  const uint32_t GW = (G + (uint32_t)c.SG - 1u) / (uint32_t)c.SG;  // workgroups along x
   XrPlan pl{};
   pl.S = (uint32_t)c.S;
   pl.kq = d.nkb / pl.S;
@@ -940,6 +962,8 @@ hipError_t xr_launch_t(GemmDesc d, const XrConfig& c, void* ws, hipStream_t stre
   pl.m_hi = plan_div_magic(16u * (pl.kq + 1u));
   pl.gmul = plan_gmul(d.gkb);
   pl.wk = (uint32_t)c.WK;
+  pl.sg = (uint32_t)c.SG;
+  pl.nslabs = G;
   if (pl.S > 1) {
     if (!ws || G > kMaxCounters) return hipErrorInvalidValue;
     pl.cnt = static_cast<uint32_t*>(ws);
@@ -947,22 +971,24 @@ hipError_t xr_launch_t(GemmDesc d, const XrConfig& c, void* ws, hipStream_t stre
   }
   // Byte offsets into X, a slab's weights, Y and the partials are 32-bit buffer or LDS offsets.
   bool fits = G >= 1 && G <= 65535 && (uint64_t)d.M * (uint64_t)d.ldx * 2u < (1ull << 31) && c.lds <= kXrLdsMax &&
-              c.lds >= xr_lds_bytes(d, T, c.WK, c.S) && (uint64_t)G * pl.S * d.M * 64u * T < (1ull << 31);
+              c.lds >= xr_lds_bytes(d, T, c.WK, c.S, c.SG) && (uint64_t)G * pl.S * d.M * 64u * T < (1ull << 31);
   for (uint32_t i = 0; i < d.nseg; ++i)
     fits = fits && (uint64_t)(d.seg[i].slab_w + 1u) * d.nkb * 64u * WTraits<FMT>::wpl * 4u < (1ull << 31);
   if (!fits) return hipErrorInvalidValue;
   static const hipError_t attr =
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&hq_decode_xr_kernel<FMT, DT, T, U, false>),
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&hq_decode_xr_kernel<FMT, DT, T, U, false, GRP>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)kXrLdsMax) != hipSuccess
           ? hipErrorInvalidConfiguration
-          : hipFuncSetAttribute(reinterpret_cast<const void*>(&hq_decode_xr_kernel<FMT, DT, T, U, true>),
+          : hipFuncSetAttribute(reinterpret_cast<const void*>(&hq_decode_xr_kernel<FMT, DT, T, U, true, GRP>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, (int)kXrLdsMax);
   if (attr != hipSuccess) return attr;
-  const dim3 grid(G, pl.S);
+  const dim3 grid(GW, pl.S);
   if (d.nseg > 1)
-    hipLaunchKernelGGL((hq_decode_xr_kernel<FMT, DT, T, U, true>), grid, dim3(64 * c.WK), c.lds, stream, d, pl);
+    hipLaunchKernelGGL((hq_decode_xr_kernel<FMT, DT, T, U, true, GRP>), grid, dim3(64 * c.WK * c.SG), c.lds, stream, d,
+                       pl);
   else
-    hipLaunchKernelGGL((hq_decode_xr_kernel<FMT, DT, T, U, false>), grid, dim3(64 * c.WK), c.lds, stream, d, pl);
+    hipLaunchKernelGGL((hq_decode_xr_kernel<FMT, DT, T, U, false, GRP>), grid, dim3(64 * c.WK * c.SG), c.lds, stream,
+                       d, pl);
   return hipGetLastError();
 }
 
@@ -970,7 +996,9 @@ template <int FMT, int DT>
 hipError_t xr_launch_fd(const GemmDesc& d, const XrConfig& c, void* ws, hipStream_t stream) {
   switch (c.T * 10 + c.U) {
     case 82: return xr_launch_t<FMT, DT, 8, 2>(d, c, ws, stream);
-    case 42: return xr_launch_t<FMT, DT, 4, 2>(d, c, ws, stream);
+    case 42:
+      if (c.SG > 1) return xr_launch_t<FMT, DT, 4, 2, true>(d, c, ws, stream);
+      return xr_launch_t<FMT, DT, 4, 2>(d, c, ws, stream);
     case 23: return xr_launch_t<FMT, DT, 2, 3>(d, c, ws, stream);
     case 24: return xr_launch_t<FMT, DT, 2, 4>(d, c, ws, stream);
     case 14: return xr_launch_t<FMT, DT, 1, 4>(d, c, ws, stream);
@@ -1037,7 +1065,7 @@ static int xr_waves_per_simd(int fmt, int T, int U) {
 // 8.8-9.1 us, int4 bf16 14.4-14.8 -> 10.2-10.9, 5120 x 10240 and 16384 7-15% faster), and at
 // five to eight rows the 4-tile slabs still fit two workgroups per CU and win (M = 5, 8:
 // 15.5-16.3 against 16.6-17.7 us; ternary bf16 M = 8: 13.5 against 15.0).
-// HQ_XR_T / _WK / _U / _S / _G (slab count) override (tuning and tests).
+// HQ_XR_T / _WK / _U / _S / _G (slab count) / _SG (slab groups per workgroup) override (tuning and tests).
 XrConfig choose_decode_xr(int fmt, const GemmDesc& d, size_t ws_cap) {
   XrConfig c{2, 3, 8, 1, 0, false};
   if (d.M > 16u || d.gen) return c;
@@ -1045,8 +1073,8 @@ XrConfig choose_decode_xr(int fmt, const GemmDesc& d, size_t ws_cap) {
   uint32_t tiles = 0;
   for (uint32_t i = 0; i < d.nseg; ++i) tiles += d.seg[i].ntiles;
   const int eT = env_int("HQ_XR_T", 0), eWK = env_int("HQ_XR_WK", 0), eU = env_int("HQ_XR_U", 0);
-  const int eS = env_int("HQ_XR_S", 0), eG = env_int("HQ_XR_G", 0);
-  const bool forced = eT || eWK || eU || eS || eG;
+  const int eS = env_int("HQ_XR_S", 0), eG = env_int("HQ_XR_G", 0), eSG = env_int("HQ_XR_SG", 0);
+  const bool forced = eT || eWK || eU || eS || eG || eSG;
   bool found = false, one_round = false;
   // Rows of all of K that do not fit in LDS (long K) at up to eight rows: K pieces, the
   // one-round grid (at most one workgroup per CU) that keeps the most CUs busy, the fewest
@@ -1124,25 +1152,45 @@ XrConfig choose_decode_xr(int fmt, const GemmDesc& d, size_t ws_cap) {
       c.lds = lds4;
     }
   }
+  // Pairs of whole 4-tile slabs per workgroup (two groups of four wavefronts over one copy of
+  // the rows) when the slabs number 1.5 to 2 times the CUs: a CU then holds one workgroup
+  // instead of two, each of which would copy the rows, the second's copy queued behind the
+  // first's weight loads (timestamps: its stream starting up to 2 us later). Measured on MI355X
+  // (alternated runs), 5120 x 27648 int4: M = 1..8 14.4-15.8 -> 14.2-14.9 us, M = 12 and 16
+  // 17.0-17.7 -> 15.4-15.9 (against the lockstep kernel), 5120 x 27648 ternary bf16 at M = 16
+  // 13.4-13.7 -> 12.4-12.5; ternary at up to eight rows, whose steps are bound by their VALU
+  // work, keeps all CUs busy instead (M = 1: 11.7 -> 12.3 us in pairs).
+  if (!forced && found && (c.T == 4 || c.T == 8) && c.S == 1 && one_round &&
+      (fmt == HQ_FORMAT_INT4 || d.M > 8u)) {
+    const uint32_t sl4 = total_slabs(d, 4);
+    const uint32_t ldsp = xr_lds_bytes(d, 4, 4, 1, 2);
+    if (2u * sl4 >= 3u * cus && sl4 <= 2u * cus && ldsp <= kXrLdsMax && xr_waves_per_simd(fmt, 4, 2) >= 2) {
+      c = XrConfig{4, 2, 4, 1, ldsp, false};
+      c.SG = 2;
+    }
+  }
   // Wide weights at more than eight rows: the lockstep kernel unless one round of slabs of at
   // most four tiles (eight wavefronts) fits.
-  const bool wide_rows = tiles > 2u * cus && d.M > 8u && (c.T > 4 || !one_round);
+  const bool wide_rows = tiles > 2u * cus && d.M > 8u && (c.T > 4 || !one_round) && c.SG == 1;
   if (!forced && (!found || wide_rows)) return c;
   if (eT == 1 || eT == 2 || eT == 4 || eT == 8) c.T = eT;
   if (eWK >= 1) c.WK = eWK;
   if (eU >= 2) c.U = eU;
   if (eS >= 1) c.S = eS;
   if (eG >= 1) c.G = (uint32_t)eG;
+  if (eSG >= 1) c.SG = eSG;
   // Snap to an instantiated (T, U).
   if (c.T == 8) c.U = 2;
   if (c.T == 4) c.U = 2;
   if (c.T == 2) c.U = std::min(std::max(c.U, 3), 4);
   if (c.T == 1) c.U = c.U >= 6 ? 6 : 4;
   c.WK = std::max(1, std::min(c.WK, xr_max_wk(c.T)));
+  c.SG = std::max(1, std::min(c.SG, xr_max_wk(c.T) / c.WK));
+  if (c.S > 1 || c.T != 4) c.SG = 1;  // slab groups: whole 4-tile slabs only
   c.S = std::max(1, std::min<int>(c.S, (int)d.nkb));
   if (c.G && total_slabs(d, c.T, c.G) > 65535u) return c;
   if (c.S > 1 && (total_slabs(d, c.T, c.G) > kMaxCounters || decode_xr_workspace_bytes(d, c) > ws_cap)) return c;
-  c.lds = xr_lds_bytes(d, c.T, c.WK, c.S);
+  c.lds = xr_lds_bytes(d, c.T, c.WK, c.S, c.SG);
   c.ok = c.lds <= kXrLdsMax;
   return c;
 }

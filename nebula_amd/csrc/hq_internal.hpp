@@ -73,6 +73,7 @@ struct XrConfig {
   uint32_t lds;  // dynamic LDS bytes per workgroup
   bool ok;       // the rows fit in LDS and the kernel takes the call
   uint32_t G = 0;  // slabs over all segments; 0: ceil(tiles / T) per segment (else up to T tiles each)
+  int SG = 1;      // slab groups of WK wavefronts per workgroup sharing one copy of the rows (S = 1)
 };
 // LDS one X-resident workgroup may use (the whole 160 KiB of a gfx950 CU).
 constexpr uint32_t kXrLdsMax = 160u * 1024u;

@@ -137,7 +137,10 @@ def test_describe_gemm_names_the_kernel_families(monkeypatch):
     with monkeypatch.context() as m:
         m.setenv("HQ_DECODE_KERNEL", "0")
         assert hq.describe(hq.FORMAT_INT4, hq.DTYPE_F16, 4, 27648, 5120).startswith("hq_decode_kernel<int4,f16,")
-    assert hq.describe(hq.FORMAT_INT4, hq.DTYPE_F16, 16, 5120, 27648).startswith("hq_decode_ls_kernel<int4,f16,")
+    assert hq.describe(hq.FORMAT_INT4, hq.DTYPE_F16, 16, 5120, 27648).startswith(
+        "hq_decode_xr_kernel<int4,f16,T=4,U=2,SG=2>")
+    assert hq.describe(hq.FORMAT_INT4, hq.DTYPE_F16, 16, 5120, 34816).startswith("hq_decode_ls_kernel<int4,f16,")
+    assert hq.describe(hq.FORMAT_INT4, hq.DTYPE_F16, 20, 5120, 27648).startswith("hq_decode_ls_kernel<int4,f16,")
     assert hq.describe(hq.FORMAT_TERNARY2, hq.DTYPE_BF16, 2048, 5120, 27648).startswith(
         "hq_prefill_kernel<ternary2,bf16")
     assert "general" in hq.describe(hq.FORMAT_INT4, hq.DTYPE_F16, 4, 4096, 4096, group=32)

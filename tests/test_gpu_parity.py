@@ -461,7 +461,7 @@ def test_lockstep_matches_per_wavefront(cuda, M):
 class xr_env(decode_env):
     """Force the X-resident decode kernel (activation rows in LDS) and its tiling for a block:
     slab width T, wavefronts WK (splitting the slab's k-blocks), ring depth U, pieces S, slab
-    count G (slabs of fewer than T tiles)."""
+    count G (slabs of fewer than T tiles), slab groups SG per workgroup."""
 
     def __init__(self, **kv):
         self.kv = {f"HQ_XR_{k}": str(v) for k, v in kv.items()}
@@ -530,6 +530,42 @@ def test_xr_variable_width_slabs(cuda, fmt, xdt, T, G, WK):
     check(y, P.reference(), xdt, f"xr variable slabs T={T} G={G}", P)
 
 
+# Slab groups: SG groups of WK wavefronts per workgroup over one copy of the activation rows,
+# group h of workgroup b streaming slab b + h * gridDim.x; a ragged last workgroup (an odd slab
+# count) has a group with no slab, which loads and stores nothing.
+@pytest.mark.parametrize("fmt,xdt", [(O.INT4, O.F16), (O.TERNARY2, O.BF16), (O.INT4, O.BF16)])
+@pytest.mark.parametrize("WK,SG,G", [(4, 2, 0), (4, 2, 31), (2, 4, 33), (4, 3, 0), (8, 2, 0), (1, 4, 0)])
+@pytest.mark.parametrize("M", [1, 8, 16])
+def test_xr_slab_groups(cuda, fmt, xdt, WK, SG, G, M):
+    import torch
+
+    K, N = 2048, 1000  # 63 tiles: 16 slabs of 4 tiles, the last one of 3
+    P = O.Problem(fmt, M, K, N, 128, xdt, seed=3580 + 7 * M + SG + G)
+    D = DeviceProblem(P)
+    kw = dict(T=4, WK=WK, SG=SG, S=1, **({"G": G} if G else {}))
+    with xr_env(**kw):
+        desc = hq.describe(fmt, xdt, M, K, N)
+        assert desc.startswith("hq_decode_xr_kernel<") and f",T=4,U=2,SG={SG}>" in desc, desc
+        y = D.run()
+        y2 = D.run()
+    assert torch.equal(y, y2)
+    check(y, P.reference(), xdt, f"xr slab groups {kw} M={M}", P)
+
+
+def test_xr_slab_groups_fused(cuda):
+    # The groups of one workgroup may stream slabs of different segments.
+    Ns, K, M = [600, 130, 1000], 1024, 5
+    probs = [O.Problem(O.INT4, M, K, n, 128, O.F16, seed=3590 + i) for i, n in enumerate(Ns)]
+    for p in probs[1:]:
+        p.X = probs[0].X
+    devs = [DeviceProblem(p) for p in probs]
+    for kw in (dict(T=4, WK=4, SG=2, S=1), dict(T=4, WK=4, SG=3, S=1, G=41)):
+        with xr_env(**kw):
+            outs = hq.gemm_fused(O.INT4, devs[0].X, [(d.Wp, d.S, d.P.N) for d in devs])
+        for d, y in zip(devs, outs):
+            check(y, d.P.reference(), O.F16, f"xr slab groups fused {kw} N={d.P.N}", d.P)
+
+
 @pytest.mark.parametrize("M,K", [(16, 5120), (8, 5120), (3, 5120), (2, 27648), (1, 27648)])
 def test_xr_lds_limits(cuda, M, K):
     # Whole-K plans whose activation rows fill the LDS (16 x 5120 halves = 160 KiB), half of
@@ -570,15 +606,13 @@ def test_xr_whole_4tile_slabs_take_4_wavefronts(cuda, fmt, xdt, M, N):
                                          (O.TERNARY2, O.BF16, 9, 16384), (O.INT4, O.F16, 16, 27648)])
 def test_xr_wide_rows_default_plan(cuda, fmt, xdt, M, N):
     # Wide weights at more than eight rows, as the planner takes them: one round of 4-tile
-    # X-resident slabs (the decoder's fused QKV and SSM projections), the lockstep kernel when
-    # only 8-tile slabs would fit in one round (5120 x 27648).
+    # X-resident slabs (the decoder's fused QKV and SSM projections), pairs of 4-tile slabs per
+    # workgroup when single slabs would take more than one round (5120 x 27648: 432 slabs).
     K = 5120
     P = O.Problem(fmt, M, K, N, 128, xdt, seed=3600 + M)
     desc = hq.describe(fmt, xdt, M, K, N)
-    if N == 27648:
-        assert desc.startswith("hq_decode_ls_kernel<"), desc
-    else:
-        assert desc.startswith("hq_decode_xr_kernel<") and ",T=4," in desc and "x 1 pieces" in desc, desc
+    assert desc.startswith("hq_decode_xr_kernel<") and ",T=4," in desc and "x 1 pieces" in desc, desc
+    assert (",SG=2>" in desc) == (N == 27648), desc
     check(DeviceProblem(P).run(), P.reference(threads=16), xdt, f"wide rows {desc[:40]} M={M} N={N}", P)
 
 
