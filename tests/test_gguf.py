@@ -163,6 +163,33 @@ def test_oracle_q4_k_matches_the_block_encoder():
     assert not np.array_equal(O.dequant_q4_k(blk, 256, 1)[:, 0], np.float32(np.float16(1e-2)) * q[::-1])
 
 
+def test_oracle_q4_k_known_answer_block():
+    # One block written byte by byte (no encoder): d = 1.0, dmin = 0.5 (fp16), scale bytes whose
+    # top two bits feed sub-blocks 4..7. Sub-block scales and mins worked out by hand from GGML's
+    # published layout (get_scale_min_k4: j < 4 from bytes j and j + 4, low six bits; j >= 4 the
+    # low / high nibble of byte j + 4 below the top two bits of byte j - 4 / j):
+    #   scales 1, 2, 3, 4, 26, 12, 14, 48 and mins 5, 6, 7, 8, 9, 11, 29, 47.
+    # Codes: byte l of qs holds l % 16 in its low nibble and 15 - l % 16 in its high nibble; the
+    # 64 weights of chunk c are the 32 low nibbles of bytes 32c.. (sub-block 2c), then their
+    # 32 high nibbles (sub-block 2c + 1). Every weight sc * q - 0.5 * m is exact in float32.
+    scale_bytes = [0x41, 0x02, 0x03, 0xC4, 0x05, 0x06, 0x47, 0x88, 0x9A, 0xBC, 0xDE, 0xF0]
+    qs = [(l % 16) | ((15 - l % 16) << 4) for l in range(128)]
+    blk = np.frombuffer(bytes([0x00, 0x3C, 0x00, 0x38] + scale_bytes + qs), dtype=np.uint8)
+    assert blk.size == 144
+    sc = [1, 2, 3, 4, 26, 12, 14, 48]
+    mn = [5, 6, 7, 8, 9, 11, 29, 47]
+    want = np.empty(256, dtype=np.float32)
+    for i in range(256):
+        c, l, hi = i // 64, i % 32, (i % 64) >= 32
+        q = 15 - l % 16 if hi else l % 16
+        j = 2 * c + (1 if hi else 0)
+        want[i] = sc[j] * q - 0.5 * mn[j]
+    got = O.dequant_q4_k(blk, 256, 1)[:, 0]
+    assert np.array_equal(got, want), np.flatnonzero(got != want)[:8]
+    # Spot values: weight 0 is 1 * 0 - 2.5, weight 32 is 2 * 15 - 3, weight 255 is 48 * 0 - 23.5.
+    assert (got[0], got[32], got[255]) == (-2.5, 27.0, -23.5)
+
+
 @pytest.mark.parametrize("K,N", [(256, 1), (512, 3), (1024, 40)])
 def test_convert_q4_k_is_the_published_weight(K, N):
     raw, W = MG.random_q4_k(RNG, K, N)

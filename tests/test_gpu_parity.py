@@ -181,16 +181,17 @@ def test_prefill_group_256(cuda):
     check(DeviceProblem(P).run(), P.reference(), O.F16, "prefill g256", P)
 
 
-@pytest.mark.parametrize("M", [512, 2048])
-def test_prefill_27b_rows_subset(cuda, M):
-    # The prefill shape (K=5120, N=27648). Rows are independent, so a random subset of rows
-    # is compared against the oracle at full size.
+@pytest.mark.parametrize("M,nrows", [(512, 0), (2048, 0)])
+def test_prefill_27b(cuda, M, nrows):
+    # The prefill shape (K=5120, N=27648) at M = 512 and 2048, every row against the oracle,
+    # normwise and element by element.
     P = O.Problem(O.INT4, M, 5120, 27648, 128, O.F16, seed=880 + M)
     y = to_host_f32(DeviceProblem(P).run())
-    rows = np.sort(np.random.default_rng(M).choice(M, size=24, replace=False))
+    rows = np.arange(M) if nrows == 0 else np.sort(np.random.default_rng(M).choice(M, size=nrows, replace=False))
     ref = P.reference(rows=rows, threads=16)
     err = O.normwise_error(y[rows], ref)
     assert err <= OUT_TOL[O.F16], f"prefill K=5120 N=27648 M={M}: {err:.3e}"
+    elementwise_bound_check(y[rows], ref, P, rows=rows)
 
 
 def test_rows_independent_and_deterministic(cuda):
