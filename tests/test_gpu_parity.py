@@ -594,11 +594,12 @@ def test_xr_spilled_4tile_slabs_take_4wave_2tile_slabs(cuda, fmt, xdt, M, K, N):
 @pytest.mark.parametrize("fmt,xdt,M,N", [(O.INT4, O.F16, 1, 27648), (O.INT4, O.F16, 8, 27648), (O.TERNARY2, O.BF16, 4, 34816)])
 def test_xr_whole_4tile_slabs_take_4_wavefronts(cuda, fmt, xdt, M, N):
     # Whole 4-tile slabs at up to eight rows whose grid still fits on the CUs in one round run
-    # with four wavefronts (one per SIMD) instead of eight: the decode sweep's 5120 x 27648 and
-    # the decoder's fused gate||up width.
+    # with four wavefronts per slab (one per SIMD) instead of eight: the decode sweep's 5120 x
+    # 27648 (int4: two such slabs per workgroup) and the decoder's fused gate||up width.
     K = 5120
     desc = hq.describe(fmt, xdt, M, K, N)
     assert desc.startswith("hq_decode_xr_kernel<") and ",T=4," in desc and "x 1 pieces x 4 wavefronts" in desc, desc
+    assert (",SG=2>" in desc) == (fmt == O.INT4 and N == 27648), desc
     P = O.Problem(fmt, M, K, N, 128, xdt, seed=3660 + M)
     check(DeviceProblem(P).run(), P.reference(threads=16), xdt, f"4-wave 4-tile slabs M={M} N={N}", P)
 
