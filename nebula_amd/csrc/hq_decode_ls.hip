@@ -1001,12 +1001,18 @@ LsConfig choose_decode_ls(int fmt, const GemmDesc& d, size_t ws_cap) {
   // steps, four k-groups (16 wavefronts) keep more of them in flight. Measured on MI355X:
   // 5120 x 27648 20% faster, 17408 x 5120 13% faster; shorter pieces (5120 x 14336 cut in
   // three) or two rounds (5120 x 34816) are slower so.
-  if (fmt == HQ_FORMAT_TERNARY2 && c.MT == 1 && eKG == 0 && eT == 0 && eU == 0 && c.T == 2 && c.KG == 2 &&
-      (uint64_t)G * (uint32_t)c.S <= cus) {
+  // Int4 weights take four k-groups (two steps in flight) when each still gets eight or more
+  // steps. Measured on MI355X (alternated runs): 27648 x 5120 (nine steps per k-group) M = 9 /
+  // 12 / 16 18.6 / 18.4 / 17.8 -> 17.8 / 17.8 / 17.7 us (bf16 M = 16 20.3 -> 18.6); 17408 x 5120
+  // (six steps) no gain.
+  if (c.MT == 1 && eKG == 0 && eT == 0 && eU == 0 && c.T == 2 && c.KG == 2 && (uint64_t)G * (uint32_t)c.S <= cus) {
     const uint32_t steps4 = (d.nkb / (uint32_t)c.S + 3u) / 4u;
-    if (steps4 >= 5u) {
+    if (fmt == HQ_FORMAT_TERNARY2 && steps4 >= 5u) {
       c.KG = 4;
       c.U = steps4 >= 8u ? 3 : 2;
+    } else if (fmt == HQ_FORMAT_INT4 && steps4 >= 8u) {
+      c.KG = 4;
+      c.U = 2;
     }
   }
   // Several row tiles: one workgroup per CU (two k-groups of four wavefronts near 256 VGPRs
