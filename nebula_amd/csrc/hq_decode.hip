@@ -500,7 +500,8 @@ __global__ void __launch_bounds__(64 * xr_max_wk(T)) hq_decode_xr_kernel(const G
   const uint32_t N = sg.N;
 
   // 1. Activation rows -> LDS: 64 units per LDS-DMA instruction, instruction q by
-  //    wavefront q mod WK; lane i of instruction q fetches the element piece of unit 64 q + i.
+  //    wavefront q mod (WK * SG); lane i of instruction q fetches the element piece of unit
+  //    64 q + i.
   {
     const uint32_t ldx2 = ldx * 2u;
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(Xp, M * ldx2);
