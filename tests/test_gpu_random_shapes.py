@@ -8,7 +8,8 @@ tiles, whole and stream-K), ragged N (1..3000), K up to 6144 in multiples of 128
 group, groups 32 / 64 (general kernels) and 128 / 256, and the int4 caller bias. Each case is
 checked against the oracle with the bars of the general-kernel tests: normwise error within the
 output rounding (2e-3 fp16, 8e-3 bf16) and, per element, |y - r| <= rel * |X| (|W| + |E|) +
-ulp(r) (rel = 2^-10 fp16, 2^-7 bf16; E the weight of code 8 of each int4 group).
+ulp(r) (rel = 2^-10 fp16, 2^-7 bf16; E the weight of code 8 of each int4 group). A second set
+draws wide decode calls (M 1-16, N 24576-32768) that the planner streams in slab pairs.
 """
 import numpy as np
 import pytest
@@ -49,4 +50,40 @@ def test_random_shape(cuda, fmt, xdt, M, K, N, group, bias, seed):
     P = O.Problem(fmt, M, K, N, group, xdt, seed=seed, bias=bias)
     label = f"fmt={fmt} dt={xdt} M={M} K={K} N={N} g={group} bias={bias} seed={seed}"
     print(label, flush=True)
+    check(Dev(P).run(), P, label)
+
+
+def _wide_cases(n: int = 16, seed: int = 20261203):
+    # Wide decode calls whose 4-tile slabs number 1.5 to 2 times the CUs (N = 24576..32768 on
+    # 256 CUs): the default planner streams them in slab pairs (int4 at any M, ternary above
+    # eight rows), with an odd slab count leaving the last workgroup one slab.
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        fmt = (O.INT4, O.TERNARY2)[i % 2]
+        xdt = (O.F16, O.BF16)[(i // 2) % 2]
+        M = int(rng.integers(1, 17))
+        group = int(rng.choice([128, 256]))
+        K = 256 * int(rng.integers(1, 9))
+        N = int(rng.integers(24576, 32769))
+        cases.append((fmt, xdt, M, K, N, group, 9500 + i))
+    return cases
+
+
+WIDE = _wide_cases()
+
+
+@pytest.mark.parametrize("fmt,xdt,M,K,N,group,seed", WIDE,
+                         ids=[f"f{c[0]}-d{c[1]}-M{c[2]}-K{c[3]}-N{c[4]}-g{c[5]}" for c in WIDE])
+def test_random_wide_decode(cuda, fmt, xdt, M, K, N, group, seed):
+    import torch
+
+    from nebula_amd import hq
+
+    P = O.Problem(fmt, M, K, N, group, xdt, seed=seed)
+    desc = hq.describe(fmt, xdt, M, K, N, group=group)
+    label = f"fmt={fmt} dt={xdt} M={M} K={K} N={N} g={group} seed={seed}: {desc}"
+    print(label, flush=True)
+    if torch.cuda.get_device_properties(0).multi_processor_count == 256:
+        assert (",SG=2>" in desc) == (fmt == O.INT4 or M > 8), label
     check(Dev(P).run(), P, label)
