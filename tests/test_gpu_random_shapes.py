@@ -9,7 +9,8 @@ group, groups 32 / 64 (general kernels) and 128 / 256, and the int4 caller bias.
 checked against the oracle with the bars of the general-kernel tests: normwise error within the
 output rounding (2e-3 fp16, 8e-3 bf16) and, per element, |y - r| <= rel * |X| (|W| + |E|) +
 ulp(r) (rel = 2^-10 fp16, 2^-7 bf16; E the weight of code 8 of each int4 group). A second set
-draws wide decode calls (M 1-16, N 24576-32768) that the planner streams in slab pairs.
+draws wide decode calls (M 1-16, N 24576-32768) that the planner streams in slab pairs, a third
+long-K decode calls (K 8192-32768) that it cuts into K pieces.
 """
 import numpy as np
 import pytest
@@ -86,4 +87,36 @@ def test_random_wide_decode(cuda, fmt, xdt, M, K, N, group, seed):
     print(label, flush=True)
     if torch.cuda.get_device_properties(0).multi_processor_count == 256:
         assert (",SG=2>" in desc) == (fmt == O.INT4 or M > 8), label
+    check(Dev(P).run(), P, label)
+
+
+def _long_k_cases(n: int = 16, seed: int = 20261204):
+    # Long K at decode row counts: rows of all of K that do not fit in LDS at several rows, so
+    # the planner cuts K into pieces (X-resident, even and uneven, up to eight rows; lockstep
+    # above, with four k-groups where each gets eight or more steps), N ragged.
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        fmt = (O.INT4, O.TERNARY2)[i % 2]
+        xdt = (O.F16, O.BF16)[(i // 2) % 2]
+        M = int(rng.integers(1, 17))
+        group = int(rng.choice([128, 256]))
+        K = 256 * int(rng.integers(32, 129))
+        N = int(rng.integers(64, 6001))
+        N = max(64, min(N, int(MAX_MACS // (M * K))))
+        cases.append((fmt, xdt, M, K, N, group, 9700 + i))
+    return cases
+
+
+LONG_K = _long_k_cases()
+
+
+@pytest.mark.parametrize("fmt,xdt,M,K,N,group,seed", LONG_K,
+                         ids=[f"f{c[0]}-d{c[1]}-M{c[2]}-K{c[3]}-N{c[4]}-g{c[5]}" for c in LONG_K])
+def test_random_long_k_decode(cuda, fmt, xdt, M, K, N, group, seed):
+    from nebula_amd import hq
+
+    P = O.Problem(fmt, M, K, N, group, xdt, seed=seed)
+    label = f"fmt={fmt} dt={xdt} M={M} K={K} N={N} g={group} seed={seed}: {hq.describe(fmt, xdt, M, K, N, group=group)}"
+    print(label, flush=True)
     check(Dev(P).run(), P, label)
