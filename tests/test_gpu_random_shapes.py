@@ -10,7 +10,8 @@ checked against the oracle with the bars of the general-kernel tests: normwise e
 output rounding (2e-3 fp16, 8e-3 bf16) and, per element, |y - r| <= rel * |X| (|W| + |E|) +
 ulp(r) (rel = 2^-10 fp16, 2^-7 bf16; E the weight of code 8 of each int4 group). A second set
 draws wide decode calls (M 1-16, N 24576-32768) that the planner streams in slab pairs, a third
-long-K decode calls (K 8192-32768) that it cuts into K pieces.
+long-K decode calls (K 8192-32768) that it cuts into K pieces, a fourth prefill calls of
+301-2048 rows.
 """
 import numpy as np
 import pytest
@@ -118,5 +119,38 @@ def test_random_long_k_decode(cuda, fmt, xdt, M, K, N, group, seed):
 
     P = O.Problem(fmt, M, K, N, group, xdt, seed=seed)
     label = f"fmt={fmt} dt={xdt} M={M} K={K} N={N} g={group} seed={seed}: {hq.describe(fmt, xdt, M, K, N, group=group)}"
+    print(label, flush=True)
+    check(Dev(P).run(), P, label)
+
+
+def _prefill_cases(n: int = 8, seed: int = 20261205):
+    # Prefill row counts past the random band above (301-2048 rows): 64-, 128- and 256-row tiles,
+    # the half-height tail launch and stream-K as the planner picks them, ragged N.
+    rng = np.random.default_rng(seed)
+    cases = []
+    for i in range(n):
+        fmt = (O.INT4, O.TERNARY2)[i % 2]
+        xdt = (O.F16, O.BF16)[(i // 2) % 2]
+        M = int(rng.integers(301, 2049))
+        group = int(rng.choice([64, 128, 256])) if fmt == O.INT4 else int(rng.choice([128, 256]))
+        K = 256 * int(rng.integers(4, 7))
+        N = int(rng.integers(2048, 8193)) if i % 3 else int(rng.integers(256, 2049))
+        N = max(256, min(N, int(1e10 // (M * K))))
+        bias = "random" if fmt == O.INT4 and i % 4 == 0 else None
+        cases.append((fmt, xdt, M, K, N, group, bias, 9800 + i))
+    return cases
+
+
+PREFILL = _prefill_cases()
+
+
+@pytest.mark.parametrize("fmt,xdt,M,K,N,group,bias,seed", PREFILL,
+                         ids=[f"f{c[0]}-d{c[1]}-M{c[2]}-K{c[3]}-N{c[4]}-g{c[5]}-{c[6] or 'nobias'}" for c in PREFILL])
+def test_random_prefill(cuda, fmt, xdt, M, K, N, group, bias, seed):
+    from nebula_amd import hq
+
+    P = O.Problem(fmt, M, K, N, group, xdt, seed=seed, bias=bias)
+    desc = hq.describe(fmt, xdt, M, K, N, group=group, with_bias=bias is not None)
+    label = f"fmt={fmt} dt={xdt} M={M} K={K} N={N} g={group} bias={bias} seed={seed}: {desc}"
     print(label, flush=True)
     check(Dev(P).run(), P, label)
