@@ -137,7 +137,9 @@ hq_status get_internal_ws(hipStream_t stream, size_t need, void** out) {
   return HQ_OK;
 }
 
-// Streaming kernel family. With at most four activation rows the activation traffic is
+// Streaming kernel family for the calls the X-resident kernel does not take (rows of all of
+// K that do not fit in LDS even in pieces, pieces beyond a workspace cap, more than 16 rows,
+// the general kernels). With at most four activation rows the activation traffic is
 // small and the per-wavefront kernel (hq_decode.hip) is as fast or faster (M = 4, same-run
 // order-swapped timings on MI355X: 5120 x 5120 7.7 against 8.1 us, 5120 x 27648 15.9 against
 // 16.15 us, 27648 x 5120 even); from five rows on, the lockstep kernel (hq_decode_ls.hip),
