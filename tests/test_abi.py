@@ -428,3 +428,24 @@ def test_int8_shapes_and_workspace():
     need = hq.workspace_bytes_w8a8(4, 1024, 64)
     assert L.hq_gemm_w8a8(0x1000, 1024, 0x1000, 0x2000, 0x3000, 64, 4, 1024, 64, 0x10000, need - 1, None) == \
         hq.HQ_ERR_WORKSPACE
+
+
+@pytest.mark.parametrize("fmt,dt,M,slabs,pairs", [
+    (hq.FORMAT_INT4, hq.DTYPE_F16, 8, 383, False), (hq.FORMAT_INT4, hq.DTYPE_F16, 8, 384, True),
+    (hq.FORMAT_INT4, hq.DTYPE_F16, 8, 512, True), (hq.FORMAT_INT4, hq.DTYPE_F16, 8, 513, False),
+    (hq.FORMAT_INT4, hq.DTYPE_BF16, 1, 432, True), (hq.FORMAT_INT4, hq.DTYPE_F16, 16, 432, True),
+    (hq.FORMAT_TERNARY2, hq.DTYPE_BF16, 8, 432, False), (hq.FORMAT_TERNARY2, hq.DTYPE_BF16, 9, 432, True)])
+def test_slab_pairs_planned_between_one_and_a_half_and_two_slabs_per_cu(fmt, dt, M, slabs, pairs):
+    # The planner's rule on a 256-CU device (the count the library assumes without a device):
+    # whole 4-tile slabs numbering 384..512 run in pairs per workgroup, int4 at any M <= 16,
+    # ternary above eight rows; outside that band, or ternary at up to eight rows, one slab per
+    # workgroup.
+    import torch
+
+    if torch.cuda.is_available() and torch.cuda.get_device_properties(0).multi_processor_count != 256:
+        pytest.skip("the boundaries are those of a 256-CU device")
+    desc = hq.describe(fmt, dt, M, 5120, 64 * slabs)
+    assert desc.startswith("hq_decode_xr_kernel<") and ",T=4,U=2" in desc, desc
+    assert (",SG=2>" in desc) == pairs, desc
+    if pairs:
+        assert f"workgroups={(slabs + 1) // 2} of 2 slabs ({slabs} slabs)" in desc, desc
