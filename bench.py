@@ -45,6 +45,7 @@ Usage:
   python bench.py --roofline-only --case K N M [--case-fmt ternary]  # one decode shape (rocprofv3 --pmc)
   python bench.py --copy-bytes 268435456        # a plain device copy of known size (counter calibration)
   python bench.py --prefill-only 2048           # W4A16 prefill M=2048, K=5120, N=27648 only (for counters)
+  python bench.py --fused-only qkv|gateup       # the split-fuse batch's fused call at M=1024 only (for counters)
 """
 from __future__ import annotations
 
@@ -177,6 +178,23 @@ def run_prefill_only(torch, hq, M: int):
         hq.gemm(FMT_INT4, X, ws[0], ss[0], N, GROUP, out=Y)
     torch.cuda.synchronize()
     log(f"prefill-only: 5 launches of M={M} K={K} N={N}")
+
+
+def run_fused_only(torch, hq, which: str):
+    """The split-fuse batch's fused call at M = 1024: QKV (int4, N = 5120 + 1024 + 1024) or
+    gate||up (ternary, N = 2 x 27648), K = 5120, fp16 activations; 5 launches."""
+    M, K = 1024, 5120
+    fmt, ns = (FMT_INT4, (5120, 1024, 1024)) if which == "qkv" else (FMT_TERN, (27648, 27648))
+    X = torch.randn((M, K), device="cuda").to(torch.float16)
+    segs = []
+    for n in ns:
+        w, sc = make_weights(hq, torch, K, n, 1, fmt=fmt)
+        segs.append((w[0], sc[0], n))
+    outs = [torch.empty((M, n), device="cuda", dtype=torch.float16) for n in ns]
+    for _ in range(5):
+        hq.gemm_fused(fmt, X, segs, GROUP, outs=outs)
+    torch.cuda.synchronize()
+    log(f"fused-only: 5 launches of {which} M={M} K={K} N={'+'.join(map(str, ns))}")
 
 
 def run_copy(torch, nbytes: int):
@@ -647,12 +665,13 @@ def main():
                     help="--roofline-only: int4 weights with fp16 activations, or ternary with bf16 ones")
     ap.add_argument("--copy-bytes", type=int, default=0)
     ap.add_argument("--prefill-only", type=int, default=0)
+    ap.add_argument("--fused-only", choices=["qkv", "gateup"], default=None)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}): this qGEMM path runs on a single "
               "GPU and is not sharded here. Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
-    if args.roofline_only or args.copy_bytes or args.prefill_only:
+    if args.roofline_only or args.copy_bytes or args.prefill_only or args.fused_only:
         import torch
 
         from nebula_amd import hq
@@ -661,6 +680,8 @@ def main():
             run_copy(torch, args.copy_bytes)
         elif args.prefill_only:
             run_prefill_only(torch, hq, args.prefill_only)
+        elif args.fused_only:
+            run_fused_only(torch, hq, args.fused_only)
         else:
             run_case_only(torch, hq, *args.case, ternary=args.case_fmt == "ternary")
         return
