@@ -1077,12 +1077,34 @@ XrConfig choose_decode_xr(int fmt, const GemmDesc& d, size_t ws_cap) {
   const int eS = env_int("HQ_XR_S", 0), eG = env_int("HQ_XR_G", 0), eSG = env_int("HQ_XR_SG", 0);
   const bool forced = eT || eWK || eU || eS || eG || eSG;
   bool found = false, one_round = false;
+  // Few tiles (at most half as many as CUs): one-tile slabs of eight wavefronts, whole or in
+  // as many K pieces as keep each wavefront near eight steps (ceil(nkb / 64)), more where the
+  // rows need them to fit in LDS, within one workgroup per CU. Measured on MI355X (best of three
+  // alternated runs, M = 1..16, int4 and ternary): N = 256..2048 at K = 4096..8192 20-30%
+  // faster than 2-tile slabs in two pieces at M <= 4 and 10-20% at M = 8..16 (5120 x 1024
+  // M = 1 5.82 -> 4.34 us, 8192 x 1024 M = 8 7.41 -> 6.00), whole slabs ahead of pieces there;
+  // K = 27648, N = 512 / 1024: four pieces 7.2 / 8.2 us at M = 1 against 10.0 / 10.2 whole and
+  // 10.2 / 10.7 before; K = 14336 M = 16 and K = 8192, N = 2048 M = 16 11-14% ahead of the
+  // lockstep kernel.
+  if (!forced && 2u * tiles <= cus) {
+    const uint32_t s0 = std::min(8u, std::max(1u, (d.nkb + 63u) / 64u));
+    for (uint32_t s = s0; s <= 8u && s <= d.nkb && !found; ++s) {
+      if (xr_x_bytes(d, (int)s) > kXrLdsMax) continue;
+      const uint32_t lds = xr_lds_bytes(d, 1, 8, (int)s);
+      const XrConfig cand{1, 4, 8, (int)s, lds, false};
+      if (lds > kXrLdsMax || total_slabs(d, 1) * s > cus ||
+          (s > 1u && (total_slabs(d, 1) > kMaxCounters || decode_xr_workspace_bytes(d, cand) > ws_cap)))
+        break;
+      c = cand;
+      found = one_round = true;
+    }
+  }
   // Rows of all of K that do not fit in LDS (long K) at up to eight rows: K pieces, the
   // one-round grid (at most one workgroup per CU) that keeps the most CUs busy, the fewest
   // pieces among equals. Measured on MI355X (alternated runs), 27648 x 5120: M = 4 16.3 us with
   // 4-tile slabs in three pieces (240 workgroups) against 16.8 in two (160); M = 8 17.1 against
   // 17.2 for the lockstep kernel.
-  if (!forced && xr_x_bytes(d, 1) > kXrLdsMax && d.M <= 8u) {
+  if (!found && !forced && xr_x_bytes(d, 1) > kXrLdsMax && d.M <= 8u) {
     uint32_t best = 0;
     for (int s = 2; s <= 8; ++s) {
       if ((uint32_t)s > d.nkb || xr_x_bytes(d, s) > kXrLdsMax) continue;
@@ -1102,10 +1124,18 @@ XrConfig choose_decode_xr(int fmt, const GemmDesc& d, size_t ws_cap) {
   for (int s = 1; s <= 8 && !found; ++s) {
     if ((uint32_t)s > d.nkb || xr_x_bytes(d, s) > kXrLdsMax || (s > 1 && d.M > 4u)) continue;
     for (int t : {1, 2, 4, 8}) {
-      // One-tile slabs only when they give every CU at most one and at least half the CUs one
-      // (4096 x 4096, M = 16: 256 workgroups, 5.96 against 6.55-6.69 us with 2-tile slabs; with
-      // more tiles than CUs, 2-tile slabs measured faster: 5120 x 5120, M = 4: 6.08 against 7.14).
+      // One-tile slabs only when they give every CU at most one (4096 x 4096, M = 16: 256
+      // workgroups, 5.96 against 6.55-6.69 us with 2-tile slabs; with more tiles than CUs,
+      // 2-tile slabs measured faster: 5120 x 5120, M = 4: 6.08 against 7.14); fewer tiles than
+      // half the CUs took one-tile slabs above.
       if (t == 1 && (tiles > cus || 2u * tiles <= cus || s > 1)) continue;
+      // 2-tile slabs two to a CU lose to 4-tile slabs one to a CU (eight wavefronts each).
+      // Measured on MI355X (best of three alternated runs, M = 1..8): int4 4096 x 11008 /
+      // 12288 / 14336 and 5120 x 13824 5-13% faster (4096 x 11008 M = 1 8.36 -> 7.26 us),
+      // ternary 2-12%.
+      if (t == 2 && !forced && total_slabs(d, 2) > cus && total_slabs(d, 4) <= cus &&
+          xr_lds_bytes(d, 4, 8, s) <= kXrLdsMax && xr_waves_per_simd(fmt, 4, 2) >= 2)
+        continue;
       const int wk = t == 8 ? 4 : 8, u = t == 1 ? 4 : t == 2 ? 3 : 2;
       const uint32_t lds = xr_lds_bytes(d, t, wk, s);
       if (lds > kXrLdsMax) continue;
@@ -1140,12 +1170,13 @@ XrConfig choose_decode_xr(int fmt, const GemmDesc& d, size_t ws_cap) {
       break;
     }
   }
-  // Whole 4-tile slabs at up to eight rows: four wavefronts (one per SIMD, each streaming
-  // twice the k-blocks) instead of eight, when that grid still fits on the CUs in one round.
-  // Measured on MI355X (alternated runs): 5120 x 27648 int4 M = 1..8 14.7-16.3 -> 14.2-15.7 us,
-  // ternary bf16 11.5-12.6 -> 11.4-11.9; ternary 5120 x 34816 M = 4 16.2 -> 14.9. Past one
-  // round it loses (5120 x 34816 at M = 8, 544 slabs on 512 slots: 17.2 -> 18.7).
-  if (!forced && found && c.T == 4 && c.WK == 8 && c.S == 1 && d.M <= 8u) {
+  // Whole 4-tile slabs at up to eight rows, more of them than CUs: four wavefronts (one per
+  // SIMD, each streaming twice the k-blocks) instead of eight, when that grid still fits on the
+  // CUs in one round. Measured on MI355X (alternated runs): 5120 x 27648 int4 M = 1..8
+  // 14.7-16.3 -> 14.2-15.7 us, ternary bf16 11.5-12.6 -> 11.4-11.9; ternary 5120 x 34816 M = 4
+  // 16.2 -> 14.9. Past one round it loses (5120 x 34816 at M = 8, 544 slabs on 512 slots: 17.2
+  // -> 18.7), and so it does with one slab per CU (4096 x 14336, 224 slabs: 8.26 -> 8.49 us).
+  if (!forced && found && c.T == 4 && c.WK == 8 && c.S == 1 && d.M <= 8u && total_slabs(d, 4) > cus) {
     const uint32_t lds4 = xr_lds_bytes(d, 4, 4, 1);
     const uint32_t per4 = std::min((uint32_t)xr_waves_per_simd(fmt, 4, 2), kXrLdsMax / lds4);
     if (lds4 <= kXrLdsMax && per4 >= 1u && total_slabs(d, 4) <= cus * per4) {

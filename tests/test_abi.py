@@ -449,3 +449,32 @@ def test_slab_pairs_planned_between_one_and_a_half_and_two_slabs_per_cu(fmt, dt,
     assert (",SG=2>" in desc) == pairs, desc
     if pairs:
         assert f"workgroups={(slabs + 1) // 2} of 2 slabs ({slabs} slabs)" in desc, desc
+
+
+@pytest.mark.parametrize("fmt,dt,M,K,N,want", [
+    # few tiles (at most 128 on 256 CUs): one-tile slabs of eight wavefronts, whole up to 64
+    # k-blocks, in ceil(k-blocks / 64) pieces beyond, more where the rows need them to fit
+    (hq.FORMAT_INT4, hq.DTYPE_F16, 1, 5120, 1024, "T=1,U=4> workgroups=64 slabs x 1 pieces x 8 wavefronts"),
+    (hq.FORMAT_INT4, hq.DTYPE_F16, 16, 5120, 1024, "T=1,U=4> workgroups=64 slabs x 1 pieces x 8 wavefronts"),
+    (hq.FORMAT_TERNARY2, hq.DTYPE_BF16, 8, 5120, 2048, "T=1,U=4> workgroups=128 slabs x 1 pieces x 8 wavefronts"),
+    (hq.FORMAT_INT4, hq.DTYPE_F16, 16, 8192, 1024, "T=1,U=4> workgroups=64 slabs x 2 pieces x 8 wavefronts"),
+    (hq.FORMAT_INT4, hq.DTYPE_F16, 1, 27648, 1024, "T=1,U=4> workgroups=64 slabs x 4 pieces x 8 wavefronts"),
+    (hq.FORMAT_INT4, hq.DTYPE_F16, 8, 27648, 512, "T=1,U=4> workgroups=32 slabs x 4 pieces x 8 wavefronts"),
+    (hq.FORMAT_TERNARY2, hq.DTYPE_BF16, 16, 14336, 1024, "T=1,U=4> workgroups=64 slabs x 3 pieces x 8 wavefronts"),
+    # ... unless no one-round grid of them exists (16 rows of K = 27648 need six pieces)
+    (hq.FORMAT_INT4, hq.DTYPE_F16, 16, 27648, 1024, "hq_decode_ls_kernel<"),
+    # 2-tile slabs two to a CU give way to 4-tile slabs one to a CU, of eight wavefronts
+    (hq.FORMAT_INT4, hq.DTYPE_F16, 1, 4096, 14336, "T=4,U=2> workgroups=224 slabs x 1 pieces x 8 wavefronts"),
+    (hq.FORMAT_TERNARY2, hq.DTYPE_BF16, 8, 4096, 11008, "T=4,U=2> workgroups=172 slabs x 1 pieces x 8 wavefronts"),
+    # ... while 2-tile slabs one to a CU stay (5120 x 7168: 224 slabs)
+    (hq.FORMAT_INT4, hq.DTYPE_F16, 4, 5120, 7168, "T=2,U=3> workgroups=224 slabs x 1 pieces x 8 wavefronts"),
+])
+def test_decode_plans_by_tile_count(fmt, dt, M, K, N, want):
+    # The planner's tile-count rules on a 256-CU device (the count the library assumes without
+    # a device).
+    import torch
+
+    if torch.cuda.is_available() and torch.cuda.get_device_properties(0).multi_processor_count != 256:
+        pytest.skip("the boundaries are those of a 256-CU device")
+    desc = hq.describe(fmt, dt, M, K, N)
+    assert want in desc, desc

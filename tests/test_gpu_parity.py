@@ -669,6 +669,33 @@ def test_xr_pieces_default_plans(cuda, M):
     check(D.run(), P.reference(threads=16), O.F16, f"xr default pieces M={M}", P)
 
 
+@pytest.mark.parametrize("fmt,xdt,M,K,N,plan", [
+    (O.INT4, O.F16, 1, 5120, 1024, "T=1,U=4> workgroups=64 slabs x 1 pieces"),
+    (O.INT4, O.F16, 8, 5120, 1000, "T=1,U=4> workgroups=63 slabs x 1 pieces"),
+    (O.TERNARY2, O.BF16, 16, 5120, 1024, "T=1,U=4> workgroups=64 slabs x 1 pieces"),
+    (O.INT4, O.BF16, 16, 8192, 2048, "T=1,U=4> workgroups=128 slabs x 2 pieces"),
+    (O.INT4, O.F16, 1, 27648, 1024, "T=1,U=4> workgroups=64 slabs x 4 pieces"),
+    (O.TERNARY2, O.F16, 8, 27648, 520, "T=1,U=4> workgroups=33 slabs x 4 pieces"),
+    (O.INT4, O.F16, 16, 14336, 1024, "T=1,U=4> workgroups=64 slabs x 3 pieces"),
+    (O.INT4, O.F16, 1, 4096, 14336, "T=4,U=2> workgroups=224 slabs x 1 pieces x 8 wavefronts"),
+    (O.TERNARY2, O.BF16, 4, 4096, 11008, "T=4,U=2> workgroups=172 slabs x 1 pieces x 8 wavefronts"),
+])
+def test_xr_default_plans_by_tile_count(cuda, fmt, xdt, M, K, N, plan):
+    # Few tiles (GQA key/value widths): one-tile slabs, whole or in K pieces; 4-tile slabs one
+    # to a CU where 2-tile slabs would take two (plans asserted on 256-CU devices).
+    import torch
+
+    desc = hq.describe(fmt, xdt, M, K, N)
+    assert desc.startswith("hq_decode_xr_kernel<"), desc
+    if torch.cuda.get_device_properties(0).multi_processor_count == 256:
+        assert plan in desc, desc
+    P = O.Problem(fmt, M, K, N, 128, xdt, seed=4100 + M + K // 1024)
+    D = DeviceProblem(P)
+    y = D.run()
+    assert torch_equal(y, D.run())
+    check(y, P.reference(threads=16), xdt, f"default plan M={M} K={K} N={N}: {desc}", P)
+
+
 @pytest.mark.parametrize("M", [1, 4, 16])
 def test_xr_matches_other_decode_kernels(cuda, M):
     # The three decode kernels compute the same values up to fp32 summation order.
