@@ -819,6 +819,12 @@ PrefillConfig choose_prefill(int fmt, const GemmDesc& d, size_t ws_cap) {
       // tiles 7% faster, at M = 2048 128-row tiles 10% faster; int4 N = 27648 at M = 384
       // 128-row tiles 12% faster.
       const uint32_t t64 = make_launch(4, 1, d).tiles, s64 = (uint32_t)prefill_slots(fmt, 4, 1);
+      // 128-row tiles a few past one per CU, when 64-row tiles fit two per CU: the CUs that
+      // take a second 128-row tile set the time. Measured on MI355X (best of three alternated
+      // runs, M = 136..192): int4 5120 x 34816 / 36864 and 4096 x 40960 (272-320 128-row
+      // tiles) 17-20% faster with 64-row tiles (4096 x 40960 M = 160: 80.3 -> 64.8 us); at
+      // M = 224, 256 (64-row tiles past two per CU) 128-row tiles stay 4% ahead.
+      if (t128 > cus && t64 <= 2u * cus) RT = 4;
       const double rate64 = fmt == HQ_FORMAT_INT4 ? 0.76 : 0.915;
       const double round64 = (double)s64 * 64.0 / ((double)s128 * 128.0) / rate64;
       auto rounds = [](uint32_t t, uint32_t sl, double full) {

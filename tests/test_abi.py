@@ -478,3 +478,16 @@ def test_decode_plans_by_tile_count(fmt, dt, M, K, N, want):
         pytest.skip("the boundaries are those of a 256-CU device")
     desc = hq.describe(fmt, dt, M, K, N)
     assert want in desc, desc
+
+
+@pytest.mark.parametrize("K,N,M,tiles", [(4096, 40960, 136, 480), (4096, 40960, 192, 480), (5120, 34816, 160, 408),
+                                         (5120, 36864, 192, 432)])
+def test_prefill_64_row_tiles_past_one_128_row_tile_per_cu(K, N, M, tiles):
+    # 128-row tiles a few past one per CU (272-320 on 256 CUs) when 64-row tiles fit two per
+    # CU: 64-row tiles (a rule on the CU count alone, not on the occupancy query).
+    import torch
+
+    if torch.cuda.is_available() and torch.cuda.get_device_properties(0).multi_processor_count != 256:
+        pytest.skip("the boundaries are those of a 256-CU device")
+    desc = hq.describe(hq.FORMAT_INT4, hq.DTYPE_F16, M, K, N)
+    assert f"64-row tiles={tiles} whole={tiles}" in desc, desc

@@ -181,6 +181,23 @@ def test_prefill_group_256(cuda):
     check(DeviceProblem(P).run(), P.reference(), O.F16, "prefill g256", P)
 
 
+@pytest.mark.parametrize("fmt,xdt,M,K,N", [(O.INT4, O.F16, 160, 4096, 40960), (O.INT4, O.BF16, 136, 5120, 34816)])
+def test_prefill_64_row_tiles_default_plan(cuda, fmt, xdt, M, K, N):
+    # 128-row tiles a few past one per CU: the default plan runs 64-row tiles, two per CU
+    # (asserted on 256-CU devices); rows at every band boundary against the oracle.
+    import torch
+
+    desc = hq.describe(fmt, xdt, M, K, N)
+    if torch.cuda.get_device_properties(0).multi_processor_count == 256:
+        assert "64-row tiles=" in desc and "stream-K workgroups=0" in desc, desc
+    P = O.Problem(fmt, M, K, N, 128, xdt, seed=4200 + M)
+    y = to_host_f32(DeviceProblem(P).run())
+    rows = np.array(sorted({0, 1, 63, 64, 65, 127, 128, M - 2, M - 1}))
+    ref = P.reference(rows=rows, threads=16)
+    assert O.normwise_error(y[rows], ref) <= OUT_TOL[xdt], desc
+    elementwise_bound_check(y[rows], ref, P, rows=rows)
+
+
 @pytest.mark.parametrize("M,nrows", [(512, 0), (2048, 0)])
 def test_prefill_27b(cuda, M, nrows):
     # The prefill shape (K=5120, N=27648) at M = 512 and 2048, every row against the oracle,
