@@ -793,8 +793,13 @@ PrefillConfig choose_prefill(int fmt, const GemmDesc& d, size_t ws_cap) {
   // 128-row tiles too few for the slots would be split along K; when those pieces would be
   // short (under 64 k-blocks) 64-row tiles do better: twice the tiles, split half as often
   // or not at all. Measured on MI355X: fused QKV (N = 7168) M = 256..1024 7-38% faster,
-  // K = 27648 x N = 5120 at M = 256 17% faster; with long pieces (K = 27648, M = 1024) the
-  // 128-row split stays (64-row tiles there: 40% slower).
+  // 27648 x 4096 at M = 192..512 2-33% faster, 28672 x 8192 at M = 192 and 320 7-20%
+  // faster; with long pieces (K = 27648, M = 1024) the 128-row split stays (64-row tiles
+  // there: 40% slower). Except over a long K (64 k-blocks or more) where the 64-row tiles
+  // would cover three quarters of the CUs and so run whole (no stream-K), each streaming all
+  // of K: there the 128-row split (at most eight ways) measured 8-39% faster in every case
+  // (best of two alternated runs, M = 384..512: 8192 x 8192 87.2 -> 77.6 us, 10240 x 8192
+  // 107 -> 75-90, 16384 x 8192 168 -> 118-127, 28672 x 8192 289 -> 177-195).
   const uint32_t cus = (uint32_t)cu_count();
   if (RT == 8 && WM == 1 && env_int("HQ_PREFILL_RT", 0) == 0 && env_int("HQ_PREFILL_WM", 0) == 0) {
     const uint32_t t128 = make_launch(8, 1, d).tiles, s128 = (uint32_t)prefill_slots(fmt, 8, 1);
@@ -805,7 +810,8 @@ PrefillConfig choose_prefill(int fmt, const GemmDesc& d, size_t ws_cap) {
       // tiles: 77.5 us against 82.5 with 448 64-row tiles; N = 27648 M = 256, 216 tiles: 75.9
       // against 80.9.
     } else if (split >= 2u && d.nkb / split < 64u) {
-      RT = 4;
+      const uint32_t t64 = make_launch(4, 1, d).tiles;
+      if (!(d.nkb >= 64u && split <= 8u && 4u * t64 >= 3u * cus)) RT = 4;
     } else if (split < 2u) {
       // Whole tiles either way: compare rounds, in units of a full 128-row round. A part-empty
       // last round that leaves at most one workgroup per CU costs 0.35 + 0.45 x its fill (its
