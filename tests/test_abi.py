@@ -431,13 +431,16 @@ def test_int8_shapes_and_workspace():
 
 
 @pytest.mark.parametrize("fmt,dt,M,slabs,pairs", [
-    (hq.FORMAT_INT4, hq.DTYPE_F16, 8, 383, False), (hq.FORMAT_INT4, hq.DTYPE_F16, 8, 384, True),
+    (hq.FORMAT_INT4, hq.DTYPE_F16, 8, 256, False), (hq.FORMAT_INT4, hq.DTYPE_F16, 8, 257, True),
+    (hq.FORMAT_INT4, hq.DTYPE_F16, 8, 383, True), (hq.FORMAT_INT4, hq.DTYPE_F16, 8, 384, True),
     (hq.FORMAT_INT4, hq.DTYPE_F16, 8, 512, True), (hq.FORMAT_INT4, hq.DTYPE_F16, 8, 513, False),
     (hq.FORMAT_INT4, hq.DTYPE_BF16, 1, 432, True), (hq.FORMAT_INT4, hq.DTYPE_F16, 16, 432, True),
+    (hq.FORMAT_INT4, hq.DTYPE_F16, 16, 272, True), (hq.FORMAT_TERNARY2, hq.DTYPE_BF16, 12, 320, True),
+    (hq.FORMAT_TERNARY2, hq.DTYPE_BF16, 8, 320, False),
     (hq.FORMAT_TERNARY2, hq.DTYPE_BF16, 8, 432, False), (hq.FORMAT_TERNARY2, hq.DTYPE_BF16, 9, 432, True)])
-def test_slab_pairs_planned_between_one_and_a_half_and_two_slabs_per_cu(fmt, dt, M, slabs, pairs):
+def test_slab_pairs_planned_between_one_and_two_slabs_per_cu(fmt, dt, M, slabs, pairs):
     # The planner's rule on a 256-CU device (the count the library assumes without a device):
-    # whole 4-tile slabs numbering 384..512 run in pairs per workgroup, int4 at any M <= 16,
+    # whole 4-tile slabs numbering 257..512 run in pairs per workgroup, int4 at any M <= 16,
     # ternary above eight rows; outside that band, or ternary at up to eight rows, one slab per
     # workgroup.
     import torch

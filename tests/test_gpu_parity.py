@@ -621,6 +621,20 @@ def test_xr_whole_4tile_slabs_take_4_wavefronts(cuda, fmt, xdt, M, N):
     check(DeviceProblem(P).run(), P.reference(threads=16), xdt, f"4-wave 4-tile slabs M={M} N={N}", P)
 
 
+@pytest.mark.parametrize("fmt,xdt,M,K,N", [(O.INT4, O.F16, 9, 5120, 17408), (O.INT4, O.BF16, 1, 4096, 22528),
+                                           (O.TERNARY2, O.BF16, 12, 4096, 18432), (O.INT4, O.F16, 16, 5120, 20480)])
+def test_xr_slab_pairs_just_past_one_slab_per_cu(cuda, fmt, xdt, M, K, N):
+    # 272-352 whole 4-tile slabs (just past one per CU): pairs per workgroup (asserted on
+    # 256-CU devices), the grid one round; against the oracle.
+    import torch
+
+    desc = hq.describe(fmt, xdt, M, K, N)
+    if torch.cuda.get_device_properties(0).multi_processor_count == 256:
+        assert desc.startswith("hq_decode_xr_kernel<") and ",SG=2>" in desc, desc
+    P = O.Problem(fmt, M, K, N, 128, xdt, seed=4300 + M)
+    check(DeviceProblem(P).run(), P.reference(threads=16), xdt, f"pairs M={M} K={K} N={N}: {desc}", P)
+
+
 @pytest.mark.parametrize("fmt,xdt,M,N", [(O.TERNARY2, O.F16, 12, 14336), (O.INT4, O.BF16, 16, 14336),
                                          (O.TERNARY2, O.BF16, 9, 16384), (O.INT4, O.F16, 16, 27648)])
 def test_xr_wide_rows_default_plan(cuda, fmt, xdt, M, N):
