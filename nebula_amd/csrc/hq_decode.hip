@@ -1184,26 +1184,32 @@ XrConfig choose_decode_xr(int fmt, const GemmDesc& d, size_t ws_cap) {
       c.lds = lds4;
     }
   }
-  // Pairs of whole 4-tile slabs per workgroup (two groups of four wavefronts over one copy of
-  // the rows) when the slabs number more than the CUs and at most twice as many: a CU then
-  // holds one workgroup instead of two, each of which would copy the rows, the second's copy
-  // queued behind the first's weight loads (timestamps: its stream starting up to 2 us later),
-  // and the grid fits in one round where single slabs would spill past it. Measured on MI355X
-  // (alternated runs), 5120 x 27648 int4: M = 1..8 14.4-15.8 -> 14.2-14.9 us, M = 12 and 16
-  // 17.0-17.7 -> 15.4-15.9 (against the lockstep kernel), 5120 x 27648 ternary bf16 at M = 16
-  // 13.4-13.7 -> 12.4-12.5; 272-352 slabs (N = 17408..22528, K = 4096..8192, best of two
-  // runs): int4 M = 1..8 4-25% faster (8192 x 20480 M = 8 24.3 -> 18.3 us), int4 and ternary
-  // M = 9..16 14-28% faster than the lockstep kernel (5120 x 17408 int4 M = 9 16.4 -> 12.5).
-  // Ternary at up to eight rows, whose steps are bound by their VALU work, keeps all CUs
-  // busy instead (5120 x 27648 M = 1: 11.7 -> 12.3 us in pairs; 272-352 slabs within 3%).
-  if (!forced && found && (c.T == 4 || c.T == 8) && c.S == 1 && (one_round || c.T == 4) &&
-      (fmt == HQ_FORMAT_INT4 || d.M > 8u)) {
+  // Groups of whole 4-tile slabs per workgroup (SG groups of four wavefronts over one copy of
+  // the rows, SG = the slabs per CU, 2 to 4) when the slabs number more than the CUs: a CU
+  // then holds one workgroup instead of SG, each of which would copy the rows, the later
+  // copies queued behind the first's weight loads (timestamps: a second workgroup's stream
+  // starting up to 2 us later), and the grid fits in one round where single slabs would not.
+  // Measured on MI355X (alternated runs, best of two or three). Pairs: 5120 x 27648 int4 M =
+  // 1..8 14.4-15.8 -> 14.2-14.9 us, M = 12 and 16 17.0-17.7 -> 15.4-15.9 (against the lockstep
+  // kernel), ternary bf16 at M = 16 13.4-13.7 -> 12.4-12.5; 272-352 slabs (N = 17408..22528,
+  // K = 4096..8192): int4 M = 1..8 4-25% faster (8192 x 20480 M = 8 24.3 -> 18.3 us), int4 and
+  // ternary M = 9..16 14-28% faster than the lockstep kernel. Triples (544-640 slabs, 5120 x
+  // 34816 / 40960, 4096 x 40960): int4 M = 4..16 8-27% faster (5120 x 34816 M = 12 25.2 ->
+  // 18.4), ternary M = 8..16 13-28%, M = 4 3-4%. Quads (864-896 slabs, 5120 x 55296, 4096 x
+  // 57344): 4-15% at M = 1..16, int4 and ternary (ternary M = 1 16.8 -> 15.9 us). Ternary in
+  // pairs at up to eight rows, whose steps are bound by their VALU work, keeps all CUs busy
+  // instead (5120 x 27648 M = 1: 11.7 -> 12.3 us in pairs; 272-352 slabs within 3%), and in
+  // triples below four rows (M = 1: 11.8 -> 12.6 us); so do one or two rows where 2-tile slabs
+  // of four wavefronts fit in one round (above; int4 triples no faster there).
+  if (!forced && xr_x_bytes(d, 1) <= kXrLdsMax && !(found && (c.T < 4 || c.S > 1))) {
     const uint32_t sl4 = total_slabs(d, 4);
-    const uint32_t ldsp = xr_lds_bytes(d, 4, 4, 1, 2);
-    if (sl4 > cus && sl4 <= 2u * cus && ldsp <= kXrLdsMax && xr_waves_per_simd(fmt, 4, 2) >= 2) {
-      c = XrConfig{4, 2, 4, 1, ldsp, false};
-      c.SG = 2;
-      one_round = true;
+    const uint32_t sg = (sl4 + cus - 1u) / cus;
+    const bool rows_ok = fmt == HQ_FORMAT_INT4 || sg >= 4u || (sg == 3u ? d.M >= 4u : d.M > 8u);
+    const uint32_t ldsg = xr_lds_bytes(d, 4, 4, 1, (int)sg);
+    if (sl4 > cus && sg <= 4u && rows_ok && ldsg <= kXrLdsMax && (uint32_t)xr_waves_per_simd(fmt, 4, 2) >= sg) {
+      c = XrConfig{4, 2, 4, 1, ldsg, false};
+      c.SG = (int)sg;
+      found = one_round = true;
     }
   }
   // Wide weights at more than eight rows: the lockstep kernel unless one round of slabs of at

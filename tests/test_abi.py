@@ -139,7 +139,7 @@ def test_describe_gemm_names_the_kernel_families(monkeypatch):
         assert hq.describe(hq.FORMAT_INT4, hq.DTYPE_F16, 4, 27648, 5120).startswith("hq_decode_kernel<int4,f16,")
     assert hq.describe(hq.FORMAT_INT4, hq.DTYPE_F16, 16, 5120, 27648).startswith(
         "hq_decode_xr_kernel<int4,f16,T=4,U=2,SG=2>")
-    assert hq.describe(hq.FORMAT_INT4, hq.DTYPE_F16, 16, 5120, 34816).startswith("hq_decode_ls_kernel<int4,f16,")
+    assert hq.describe(hq.FORMAT_INT4, hq.DTYPE_F16, 16, 5120, 69632).startswith("hq_decode_ls_kernel<int4,f16,")
     assert hq.describe(hq.FORMAT_INT4, hq.DTYPE_F16, 20, 5120, 27648).startswith("hq_decode_ls_kernel<int4,f16,")
     assert hq.describe(hq.FORMAT_TERNARY2, hq.DTYPE_BF16, 2048, 5120, 27648).startswith(
         "hq_prefill_kernel<ternary2,bf16")
@@ -430,28 +430,35 @@ def test_int8_shapes_and_workspace():
         hq.HQ_ERR_WORKSPACE
 
 
-@pytest.mark.parametrize("fmt,dt,M,slabs,pairs", [
-    (hq.FORMAT_INT4, hq.DTYPE_F16, 8, 256, False), (hq.FORMAT_INT4, hq.DTYPE_F16, 8, 257, True),
-    (hq.FORMAT_INT4, hq.DTYPE_F16, 8, 383, True), (hq.FORMAT_INT4, hq.DTYPE_F16, 8, 384, True),
-    (hq.FORMAT_INT4, hq.DTYPE_F16, 8, 512, True), (hq.FORMAT_INT4, hq.DTYPE_F16, 8, 513, False),
-    (hq.FORMAT_INT4, hq.DTYPE_BF16, 1, 432, True), (hq.FORMAT_INT4, hq.DTYPE_F16, 16, 432, True),
-    (hq.FORMAT_INT4, hq.DTYPE_F16, 16, 272, True), (hq.FORMAT_TERNARY2, hq.DTYPE_BF16, 12, 320, True),
-    (hq.FORMAT_TERNARY2, hq.DTYPE_BF16, 8, 320, False),
-    (hq.FORMAT_TERNARY2, hq.DTYPE_BF16, 8, 432, False), (hq.FORMAT_TERNARY2, hq.DTYPE_BF16, 9, 432, True)])
-def test_slab_pairs_planned_between_one_and_two_slabs_per_cu(fmt, dt, M, slabs, pairs):
+@pytest.mark.parametrize("fmt,dt,M,slabs,sg", [
+    (hq.FORMAT_INT4, hq.DTYPE_F16, 8, 256, 1), (hq.FORMAT_INT4, hq.DTYPE_F16, 8, 257, 2),
+    (hq.FORMAT_INT4, hq.DTYPE_F16, 8, 383, 2), (hq.FORMAT_INT4, hq.DTYPE_F16, 8, 384, 2),
+    (hq.FORMAT_INT4, hq.DTYPE_F16, 8, 512, 2), (hq.FORMAT_INT4, hq.DTYPE_F16, 8, 513, 3),
+    (hq.FORMAT_INT4, hq.DTYPE_BF16, 1, 432, 2), (hq.FORMAT_INT4, hq.DTYPE_F16, 16, 432, 2),
+    (hq.FORMAT_INT4, hq.DTYPE_F16, 16, 272, 2), (hq.FORMAT_TERNARY2, hq.DTYPE_BF16, 12, 320, 2),
+    (hq.FORMAT_TERNARY2, hq.DTYPE_BF16, 8, 320, 1),
+    (hq.FORMAT_TERNARY2, hq.DTYPE_BF16, 8, 432, 1), (hq.FORMAT_TERNARY2, hq.DTYPE_BF16, 9, 432, 2),
+    (hq.FORMAT_INT4, hq.DTYPE_F16, 4, 544, 3), (hq.FORMAT_INT4, hq.DTYPE_F16, 16, 768, 3),
+    (hq.FORMAT_INT4, hq.DTYPE_F16, 12, 769, 4), (hq.FORMAT_INT4, hq.DTYPE_BF16, 1, 864, 4),
+    (hq.FORMAT_INT4, hq.DTYPE_F16, 16, 1024, 4), (hq.FORMAT_INT4, hq.DTYPE_F16, 4, 1025, 1),
+    (hq.FORMAT_TERNARY2, hq.DTYPE_BF16, 4, 544, 3), (hq.FORMAT_TERNARY2, hq.DTYPE_BF16, 3, 640, 1),
+    (hq.FORMAT_TERNARY2, hq.DTYPE_F16, 16, 640, 3), (hq.FORMAT_TERNARY2, hq.DTYPE_BF16, 1, 896, 4)])
+def test_slab_groups_planned_by_slabs_per_cu(fmt, dt, M, slabs, sg):
     # The planner's rule on a 256-CU device (the count the library assumes without a device):
-    # whole 4-tile slabs numbering 257..512 run in pairs per workgroup, int4 at any M <= 16,
-    # ternary above eight rows; outside that band, or ternary at up to eight rows, one slab per
-    # workgroup.
+    # whole 4-tile slabs numbering 257..1024 run in groups of ceil(slabs / 256) per workgroup,
+    # int4 at any M <= 16 (one or two rows may take 2-tile slabs first on a device), ternary in
+    # pairs above eight rows, in triples from four rows, in quads at any row count; otherwise
+    # one slab per workgroup.
     import torch
 
     if torch.cuda.is_available() and torch.cuda.get_device_properties(0).multi_processor_count != 256:
         pytest.skip("the boundaries are those of a 256-CU device")
     desc = hq.describe(fmt, dt, M, 5120, 64 * slabs)
-    assert desc.startswith("hq_decode_xr_kernel<") and ",T=4,U=2" in desc, desc
-    assert (",SG=2>" in desc) == pairs, desc
-    if pairs:
-        assert f"workgroups={(slabs + 1) // 2} of 2 slabs ({slabs} slabs)" in desc, desc
+    assert desc.startswith("hq_decode_xr_kernel<") or sg == 1, desc
+    assert ",SG=" not in desc if sg == 1 else f",T=4,U=2,SG={sg}>" in desc, desc
+    if sg > 1:
+        assert f"workgroups={(slabs + sg - 1) // sg} of {sg} slabs ({slabs} slabs)" in desc, desc
+        assert "x 1 pieces x 4 wavefronts" in desc, desc
 
 
 @pytest.mark.parametrize("fmt,dt,M,K,N,want", [

@@ -612,11 +612,13 @@ def test_xr_spilled_4tile_slabs_take_4wave_2tile_slabs(cuda, fmt, xdt, M, K, N):
 def test_xr_whole_4tile_slabs_take_4_wavefronts(cuda, fmt, xdt, M, N):
     # Whole 4-tile slabs at up to eight rows whose grid still fits on the CUs in one round run
     # with four wavefronts per slab (one per SIMD) instead of eight: the decode sweep's 5120 x
-    # 27648 (int4: two such slabs per workgroup) and the decoder's fused gate||up width.
+    # 27648 (int4: two such slabs per workgroup) and the decoder's fused gate||up width (three
+    # per workgroup at four rows).
     K = 5120
     desc = hq.describe(fmt, xdt, M, K, N)
     assert desc.startswith("hq_decode_xr_kernel<") and ",T=4," in desc and "x 1 pieces x 4 wavefronts" in desc, desc
     assert (",SG=2>" in desc) == (fmt == O.INT4 and N == 27648), desc
+    assert (",SG=3>" in desc) == (N == 34816), desc
     P = O.Problem(fmt, M, K, N, 128, xdt, seed=3660 + M)
     check(DeviceProblem(P).run(), P.reference(threads=16), xdt, f"4-wave 4-tile slabs M={M} N={N}", P)
 
@@ -633,6 +635,23 @@ def test_xr_slab_pairs_just_past_one_slab_per_cu(cuda, fmt, xdt, M, K, N):
         assert desc.startswith("hq_decode_xr_kernel<") and ",SG=2>" in desc, desc
     P = O.Problem(fmt, M, K, N, 128, xdt, seed=4300 + M)
     check(DeviceProblem(P).run(), P.reference(threads=16), xdt, f"pairs M={M} K={K} N={N}: {desc}", P)
+
+
+@pytest.mark.parametrize("fmt,xdt,M,K,N,sg", [(O.INT4, O.F16, 4, 5120, 34816, 3), (O.TERNARY2, O.BF16, 16, 4096, 40960, 3),
+                                              (O.INT4, O.BF16, 12, 4096, 49280, 4), (O.TERNARY2, O.F16, 1, 5120, 55296, 4),
+                                              (O.INT4, O.F16, 16, 4096, 57344, 4)])
+def test_xr_slab_groups_default_plan(cuda, fmt, xdt, M, K, N, sg):
+    # 513-1024 whole 4-tile slabs: triples and quads of slabs per workgroup (asserted on 256-CU
+    # devices), the last workgroup ragged where the groups do not divide the slabs (544, 640
+    # and 770 slabs); against the oracle.
+    import torch
+
+    desc = hq.describe(fmt, xdt, M, K, N)
+    if torch.cuda.get_device_properties(0).multi_processor_count == 256:
+        slabs = N // 64
+        assert f",T=4,U=2,SG={sg}> workgroups={(slabs + sg - 1) // sg} of {sg} slabs" in desc, desc
+    P = O.Problem(fmt, M, K, N, 128, xdt, seed=4400 + M)
+    check(DeviceProblem(P).run(), P.reference(threads=16), xdt, f"slab groups M={M} K={K} N={N}: {desc}", P)
 
 
 @pytest.mark.parametrize("fmt,xdt,M,N", [(O.TERNARY2, O.F16, 12, 14336), (O.INT4, O.BF16, 16, 14336),
