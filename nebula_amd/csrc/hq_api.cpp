@@ -291,11 +291,13 @@ struct Plan {
 };
 
 // cap: the largest workspace the plan may use (the no-allocation entry point's scratch).
-Plan make_plan(int fmt, const hq::GemmDesc& d, size_t cap = SIZE_MAX) {
+// dtype: the activation type (the prefill tile width depends on it, the workspace does not,
+// so the workspace queries plan without it).
+Plan make_plan(int fmt, const hq::GemmDesc& d, size_t cap = SIZE_MAX, int dtype = HQ_DTYPE_F16) {
   Plan p{};
   if (d.M > decode_max_m()) {
     p.kind = Kind::kPrefill;
-    p.pc = hq::choose_prefill(fmt, d, cap);
+    p.pc = hq::choose_prefill(fmt, d, cap, dtype);
     p.need = hq::prefill_workspace_bytes(d, p.pc);
     return p;
   }
@@ -424,7 +426,7 @@ hq_status run_gemm(const void* X, hq_dtype dtype, int64_t ldx, hq_format fmt, co
   hq_status st = prepare(X, dtype, ldx, fmt, segs, nseg, M, K, group, &d);
   if (st != HQ_OK) return st;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const Plan p = make_plan(fmt, d);
+  const Plan p = make_plan(fmt, d, SIZE_MAX, dtype);
   void* w = nullptr;
   if (p.need > 0) {
     if (ws) {
@@ -522,8 +524,8 @@ std::string describe(int fmt, int dtype, const hq::GemmDesc& d, const Plan& p) {
                           d.gen ? ",general" : "");
     for (int i = 0; i < p.pc.n && n > 0 && (size_t)n < sizeof b; ++i) {
       const hq::PrefillLaunch& l = p.pc.l[i];
-      n += std::snprintf(b + n, sizeof b - n, "%s launch %d: %u-row tiles=%u whole=%u stream-K workgroups=%u%s",
-                         i ? ";" : "", i, 16u * l.RT * l.WM, l.tiles, l.dp, l.psk,
+      n += std::snprintf(b + n, sizeof b - n, "%s launch %d: %u-row%s tiles=%u whole=%u stream-K workgroups=%u%s",
+                         i ? ";" : "", i, 16u * l.RT * l.WM, l.TW == 2 ? " 128-column" : "", l.tiles, l.dp, l.psk,
                          l.KS == 2 ? " k-split in workgroup" : "");
     }
     if (n > 0 && (size_t)n < sizeof b) std::snprintf(b + n, sizeof b - n, " ws=%zu", p.need);
@@ -623,7 +625,7 @@ hq_status hq_describe_gemm(hq_format fmt, hq_dtype dtype, uint32_t M, uint32_t K
   if (st != HQ_OK) return st;
   if (N == 0) return fail(HQ_ERR_SHAPE, "N must be >= 1");
   const hq::GemmDesc d = make_desc(M, K, group, &N, 1, with_bias != 0);
-  const std::string s = describe(fmt, dtype, d, make_plan(fmt, d));
+  const std::string s = describe(fmt, dtype, d, make_plan(fmt, d, SIZE_MAX, dtype));
   std::snprintf(buf, buf_len, "%s", s.c_str());
   return ok();
 }
@@ -904,7 +906,7 @@ hq_status hq_gemm_fused_noalloc(const void* X, hq_dtype dtype, int64_t ldx, hq_f
   hq_status st = prepare(X, dtype, ldx, fmt, segs, nseg, M, K, group, &d);
   if (st != HQ_OK) return st;
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const Plan p = make_plan(fmt, d, kScratchBytes);
+  const Plan p = make_plan(fmt, d, kScratchBytes, dtype);
   if (p.need > kScratchBytes)
     return fail(HQ_ERR_WORKSPACE, "this call needs %zu workspace bytes, more than the %zu-byte static scratch",
                 p.need, kScratchBytes);

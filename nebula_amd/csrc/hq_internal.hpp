@@ -147,6 +147,7 @@ struct PrefillLaunch {
   int RT;
   int WM;
   int KS;  // 2: each tile's k-blocks split between two halves of one workgroup (whole tiles)
+  int TW;  // column tiles per wavefront: 4 (256-column tiles) or 2 (128-column whole tiles)
   GemmDesc d;
   uint32_t tiles;
   uint32_t dp;
@@ -159,7 +160,8 @@ struct PrefillConfig {
   PrefillLaunch l[2];
 };
 // ws_cap: the largest workspace the plan may use (fewer stream-K workgroups, or none, below it).
-PrefillConfig choose_prefill(int fmt, const GemmDesc& d, size_t ws_cap = SIZE_MAX);
+// dtype: the activation type (the tile width depends on it; the workspace does not).
+PrefillConfig choose_prefill(int fmt, const GemmDesc& d, size_t ws_cap = SIZE_MAX, int dtype = HQ_DTYPE_F16);
 // Workspace bytes of a prefill call (0 without stream-K): the counter area, then two fp32
 // partial tiles per stream-K workgroup.
 size_t prefill_workspace_bytes(const GemmDesc& d, const PrefillConfig& c);

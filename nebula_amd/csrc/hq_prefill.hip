@@ -105,7 +105,7 @@ __device__ __forceinline__ u4 dq_scaled(const u4& w, int c, uint32_t s_f16, cons
 // (tile = mt * nb + cb, cb counting segment 0's blocks, then segment 1's, ...; a
 // segment's first block is its blk_begin): its segment, first row and this wavefront's
 // first column tile. Consecutive tiles share their activation rows across segments.
-template <uint32_t BM>
+template <uint32_t BM, int TW = kTilesPerWave>
 __device__ __forceinline__ void tile_geom(const GemmDesc& d, uint32_t nb, uint32_t tile, uint32_t wn, uint32_t& s,
                                           uint32_t& m0, uint32_t& ct0) {
   const uint32_t mt = tile / nb;
@@ -115,7 +115,7 @@ __device__ __forceinline__ void tile_geom(const GemmDesc& d, uint32_t nb, uint32
   for (uint32_t i = 1; i < HQ_MAX_SEGMENTS; ++i)
     if (i < d.nseg && cb >= d.seg[i].blk_begin) s = i;
   m0 = mt * BM;
-  ct0 = (cb - d.seg[s].blk_begin) * 16u + wn * kTilesPerWave;
+  ct0 = (cb - d.seg[s].blk_begin) * (4u * TW) + wn * TW;
 }
 
 // SKP = false: workgroup b computes whole tile b (grid dp). SKP = true: workgroup b
@@ -128,17 +128,21 @@ __device__ __forceinline__ void tile_geom(const GemmDesc& d, uint32_t nb, uint32
 // each computing the tile over half of its k-blocks through its own LDS stages; the halves'
 // sums meet in LDS at the end (half 0 + half 1). A grid of one tile per CU then still keeps
 // two wavefronts on every SIMD, as two workgroups per CU do.
-template <int FMT, int DT, int RT, int WM, bool SKP, bool GEN = false, int KS = 1>
+template <int FMT, int DT, int RT, int WM, bool SKP, bool GEN = false, int KS = 1, int TW = 4>
 __global__ void __launch_bounds__(256 * WM * KS, WM == 1 && RT == 8 && KS == 1 ? 2 : 1)
     hq_prefill_kernel(const GemmDesc d, const PrefillPlan pp) {
   static_assert(KS == 1 || (KS == 2 && !SKP && !GEN && WM == 1), "the K split is for whole fast tiles");
+  static_assert(TW == 4 || (TW == 2 && KS == 1 && !SKP && !GEN && WM == 1 && RT == 8),
+                "128-column tiles are whole 128-row fast tiles");
+  // Column tiles per wavefront: 4 (256-column workgroup tiles) or 2 (128 columns).
+  constexpr int kTilesPerWave = TW;
   constexpr uint32_t BM = 16u * RT * WM;
   constexpr uint32_t kStageBytes = BM * 256u;        // BM rows x 128 fp16
   constexpr uint32_t kPartBytes = BM * 256u * 4u;    // one fp32 partial tile
   constexpr uint32_t kWavePart = RT * kTilesPerWave * 1024u;  // one wavefront's share of it
   // The explicit order holds more values live; the fp16 128-row kernels make room for it with
   // a weight ring of two k-blocks (one ahead: a k-block's MFMAs outlast a load's latency).
-  constexpr bool kOrdered = DT == HQ_DTYPE_F16 && RT == 8 && !GEN;
+  constexpr bool kOrdered = DT == HQ_DTYPE_F16 && RT == 8 && !GEN && TW == 4;
   constexpr int kRing = kOrdered ? 2 : 3;
   // Partial tiles are stored and loaded with the sc1 cache policy: agent-coherent, so a
   // store that has completed is visible to loads from any XCD.
@@ -231,8 +235,10 @@ __global__ void __launch_bounds__(256 * WM * KS, WM == 1 && RT == 8 && KS == 1 ?
     const __amdgpu_buffer_rsrc_t yr =
         make_rsrc(reinterpret_cast<char*>(sg.Y) + (size_t)m0 * (size_t)sg.ldy * 2u, rows * (uint32_t)sg.ldy * 2u);
     const uint32_t align = (uint32_t)reinterpret_cast<uintptr_t>(sg.Y) | ((uint32_t)sg.ldy * 2u);
-    if ((align & 15u) == 0u && ct0 * 16u + 64u <= sg.N) {  // uniform
-      char* const area = smem + wave * (16u * RT * 128u);
+    // RB: bytes of a wavefront's output row (16 TW columns), in 2 TW 16-byte units.
+    constexpr uint32_t RB = 32u * TW, UM = 2u * TW - 1u;
+    if ((align & 15u) == 0u && ct0 * 16u + 16u * TW <= sg.N) {  // uniform
+      char* const area = smem + wave * (16u * RT * RB);
 #pragma unroll
       for (int r = 0; r < RT; ++r) {
         if (r < r0 || r >= r1) continue;
@@ -243,17 +249,18 @@ __global__ void __launch_bounds__(256 * WM * KS, WM == 1 && RT == 8 && KS == 1 ?
           const u2 packed = {(uint32_t)f32_to_out<DT>(v[0]) | ((uint32_t)f32_to_out<DT>(v[1]) << 16),
                              (uint32_t)f32_to_out<DT>(v[2]) | ((uint32_t)f32_to_out<DT>(v[3]) << 16)};
           const uint32_t unit = 2u * t + (g4 >> 1);
-          *reinterpret_cast<u2*>(area + row * 128u + ((unit ^ (row & 7u)) * 16u) + (g4 & 1u) * 8u) = packed;
+          *reinterpret_cast<u2*>(area + row * RB + ((unit ^ (row & UM)) * 16u) + (g4 & 1u) * 8u) = packed;
         }
       }
       // Read back in row order (this wavefront's own area: its LDS operations complete in
-      // order): lane -> row 8 i + lane / 8, columns 8 (lane % 8) .. + 7.
-      const uint32_t j = lane & 7u;
+      // order): lane -> row (32 / TW) i + lane / (2 TW), columns 8 (lane % (2 TW)) .. + 7.
+      const uint32_t j = lane & UM;
+      constexpr int kRowsPer = 32 / TW;  // rows per read instruction
 #pragma unroll
-      for (int i = 0; i < 2 * RT; ++i) {
-        if (i < 2 * r0 || i >= 2 * r1) continue;
-        const uint32_t row = 8u * i + (lane >> 3);
-        const u4 v = *reinterpret_cast<const u4*>(area + row * 128u + ((j ^ (row & 7u)) * 16u));
+      for (int i = 0; i < RT * TW / 2; ++i) {
+        if (i < r0 * TW / 2 || i >= r1 * TW / 2) continue;
+        const uint32_t row = (uint32_t)kRowsPer * i + lane / (2u * TW);
+        const u4 v = *reinterpret_cast<const u4*>(area + row * RB + ((j ^ (row & UM)) * 16u));
         __builtin_amdgcn_raw_buffer_store_b128(v, yr, ((wrow0 + row) * (uint32_t)sg.ldy + ct0 * 16u + 8u * j) * 2u, 0, 0);
       }
       return;
@@ -450,7 +457,7 @@ __global__ void __launch_bounds__(256 * WM * KS, WM == 1 && RT == 8 && KS == 1 ?
       tile = (g * pp.gb + (r - cb * nbg)) * pp.nb + cb;
     }
     uint32_t s, m0, ct0;
-    tile_geom<BM>(d, pp.nb, tile, wn, s, m0, ct0);
+    tile_geom<BM, TW>(d, pp.nb, tile, wn, s, m0, ct0);
     if constexpr (KS == 1) {
       run_piece(s, m0, ct0, 0u, nkb);
       __syncthreads();  // the output goes through the activation stages' LDS
@@ -497,7 +504,7 @@ __global__ void __launch_bounds__(256 * WM * KS, WM == 1 && RT == 8 && KS == 1 ?
     const bool first = u == u0;
     u = tile * nkb + kz;
     uint32_t s, m0, ct0;
-    tile_geom<BM>(d, pp.nb, tile, wn, s, m0, ct0);
+    tile_geom<BM, TW>(d, pp.nb, tile, wn, s, m0, ct0);
     run_piece(s, m0, ct0, ka, kz);
     const uint32_t slot = first ? 0u : 1u;
     if (first) ptile0 = tile;
@@ -542,7 +549,7 @@ __global__ void __launch_bounds__(256 * WM * KS, WM == 1 && RT == 8 && KS == 1 ?
     const uint32_t bf = plan_wg_of_unit(pp.L, pp.rem, rel * nkb);
     const uint32_t bl = plan_wg_of_unit(pp.L, pp.rem, (rel + 1u) * nkb - 1u);
     uint32_t s, m0, ct0;
-    tile_geom<BM>(d, pp.nb, tile, wn, s, m0, ct0);
+    tile_geom<BM, TW>(d, pp.nb, tile, wn, s, m0, ct0);
     // The sum runs over the contributors in workgroup order from zero (this workgroup's
     // own partial is read back too: keeping it in registers across the fix-up would cost
     // the k-loop registers). Four row tiles at a time: all 16 loads of a contributor in
@@ -597,13 +604,13 @@ int prefill_occupancy() {
   return occ;
 }
 
-// Column blocks: blk_begin = first 256-column block of each segment in the global block
-// order. Returns the number of blocks.
-uint32_t assign_blocks(GemmDesc& d) {
+// Column blocks: blk_begin = first column block (64 TW columns: 256, or 128 for TW = 2) of
+// each segment in the global block order. Returns the number of blocks.
+uint32_t assign_blocks(GemmDesc& d, int TW = kTilesPerWave) {
   uint32_t nb = 0;
   for (uint32_t i = 0; i < d.nseg; ++i) {
     d.seg[i].blk_begin = nb;
-    d.seg[i].blk_count = (d.seg[i].ntiles + 15u) / 16u;
+    d.seg[i].blk_count = (d.seg[i].ntiles + 4u * TW - 1u) / (4u * TW);
     nb += d.seg[i].blk_count;
   }
   return nb;
@@ -677,6 +684,27 @@ hipError_t launch_ks2(const PrefillLaunch& c, uint32_t* fault, uint32_t spin, hi
   return hipGetLastError();
 }
 
+// Whole 128-row x 128-column tiles (TW = 2): one workgroup per tile, two per CU.
+template <int FMT, int DT>
+hipError_t launch_tw2(const PrefillLaunch& c, hipStream_t stream) {
+  GemmDesc d = c.d;
+  PrefillPlan pp{};
+  pp.nb = assign_blocks(d, 2);
+  if ((d.M + 127u) / 128u * pp.nb != c.tiles || c.psk != 0 || c.dp != c.tiles) return hipErrorInvalidValue;
+  pp.dp = c.dp;
+  pp.xcd = c.dp % 8u == 0u ? 1u : 0u;
+  pp.bands = (d.M + 127u) / 128u;
+  pp.gb = (uint32_t)std::max(1, env_int("HQ_PREFILL_GB", 4));
+  pp.nkb_m = plan_div_magic(d.nkb);
+  const size_t lds = prefill_lds<FMT, DT, 8, 1>();
+  static const hipError_t attr =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&hq_prefill_kernel<FMT, DT, 8, 1, false, false, 1, 2>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  if (attr != hipSuccess) return attr;
+  hipLaunchKernelGGL((hq_prefill_kernel<FMT, DT, 8, 1, false, false, 1, 2>), dim3(c.dp), dim3(256), lds, stream, d, pp);
+  return hipGetLastError();
+}
+
 int env_int(const char* name, int dflt) {
   const char* v = std::getenv(name);
   return v && *v ? std::atoi(v) : dflt;
@@ -723,6 +751,7 @@ template <int FMT, int DT>
 hipError_t launch_fd(const PrefillLaunch& c, void* ws, uint32_t* fault, uint32_t spin, hipStream_t stream) {
   if (c.d.gen) return c.RT == 4 && c.WM == 1 ? launch_rt<FMT, DT, 4, 1, true>(c, ws, stream) : hipErrorInvalidConfiguration;
   if (c.KS == 2) return c.RT == 8 && c.WM == 1 ? launch_ks2<FMT, DT>(c, fault, spin, stream) : hipErrorInvalidConfiguration;
+  if (c.TW == 2) return c.RT == 8 && c.WM == 1 ? launch_tw2<FMT, DT>(c, stream) : hipErrorInvalidConfiguration;
   if (c.RT == 4) return launch_rt<FMT, DT, 4, 1>(c, ws, stream);
   if (c.WM == 1) return launch_rt<FMT, DT, 8, 1>(c, ws, stream);
   return launch_rt<FMT, DT, 8, 2>(c, ws, stream);
@@ -755,18 +784,19 @@ GemmDesc column_range(int fmt, const GemmDesc& d, uint32_t cb0, uint32_t cb1) {
   return out;
 }
 
-uint32_t count_blocks(const GemmDesc& d) {
+uint32_t count_blocks(const GemmDesc& d, int TW = kTilesPerWave) {
   GemmDesc t = d;
-  return assign_blocks(t);
+  return assign_blocks(t, TW);
 }
 
-PrefillLaunch make_launch(int RT, int WM, const GemmDesc& d) {
+PrefillLaunch make_launch(int RT, int WM, const GemmDesc& d, int TW = kTilesPerWave) {
   PrefillLaunch l{};
   l.RT = RT;
   l.WM = WM;
   l.KS = 1;
+  l.TW = TW;
   l.d = d;
-  l.tiles = (d.M + 16u * RT * WM - 1) / (16u * RT * WM) * count_blocks(d);
+  l.tiles = (d.M + 16u * RT * WM - 1) / (16u * RT * WM) * count_blocks(d, TW);
   l.dp = l.tiles;
   l.psk = 0;
   return l;
@@ -782,7 +812,8 @@ PrefillLaunch make_launch(int RT, int WM, const GemmDesc& d) {
 //    the last k column blocks (just enough to empty that round) run as a second launch of
 //    half-height tiles, if those fit in one round: the tail then takes half a round.
 //  * Otherwise whole tiles.
-PrefillConfig choose_prefill(int fmt, const GemmDesc& d, size_t ws_cap) {
+namespace {
+PrefillConfig choose_prefill_256(int fmt, const GemmDesc& d, size_t ws_cap) {
   PrefillConfig c{};
   int RT = 8, WM = 2;
   prefill_shape(d.M, RT, WM);
@@ -892,6 +923,55 @@ PrefillConfig choose_prefill(int fmt, const GemmDesc& d, size_t ws_cap) {
   c.n = 2;
   c.l[0] = make_launch(RT, WM, column_range(fmt, d, 0, nb - k));
   c.l[1] = tail;
+  return c;
+}
+
+bool env_set(const char* name) {
+  const char* v = std::getenv(name);
+  return v && *v;
+}
+}  // namespace
+
+// The plan over 256-column tiles, then 128-row x 128-column whole tiles (TW = 2, four
+// wavefronts of 32 columns, two workgroups per CU) in place of a one-round whole-tile grid
+// that leaves the CUs one workgroup each or uneven: at the same tile count as 64-row tiles
+// each dequantised weight serves twice the rows, and against a 128-row tile split in two K
+// halves the CU holds two independent tiles. The choice depends on the activation type (the
+// fp16 256-column kernel runs an explicit instruction order, the bf16 one forms its weights
+// in fp32) but not the workspace: every plan it swaps needs none. Measured on MI355X (best of
+// two alternated runs, K = 4096..5120, M = 128..1536):
+//  * in place of 64-row whole tiles (216-344): 10-17% faster for int4 fp16 (5120 x 7168
+//    M = 768 79.6 -> 68.9 us), 12-28% for bf16, 5-7% for ternary fp16 from two bands of 128
+//    rows (5120 x 27648 at M = 128: 4-5% slower);
+//  * in place of the K split (192-256 tiles): fp16 3-6% faster (the fused QKV width at M =
+//    1024, int4: 72.8 -> 68.8 us), bf16 within -4..+2%;
+//  * in place of 272-336 128-row whole tiles (544-672 128-column tiles): bf16 8-11% faster,
+//    fp16 6-13% slower; bf16 at 408 (816) 8% slower.
+// Stream-K plans (short grids, long K) stay: 128-column tiles there were 1-40% slower.
+PrefillConfig choose_prefill(int fmt, const GemmDesc& d, size_t ws_cap, int dtype) {
+  PrefillConfig c = choose_prefill_256(fmt, d, ws_cap);
+  if (d.gen || c.n != 1) return c;
+  PrefillLaunch& l = c.l[0];
+  const int etw = env_int("HQ_PREFILL_TW", 0);  // tuning / test override: 2 forces, 1 forbids
+  if (etw == 2) {
+    if (l.RT == 8 && l.WM == 1) l = make_launch(8, 1, d, 2);
+    return c;
+  }
+  if (etw == 1 || d.M < 128u || l.psk != 0 || l.dp != l.tiles) return c;
+  for (const char* e : {"HQ_PREFILL_RT", "HQ_PREFILL_WM", "HQ_PREFILL_KS", "HQ_PREFILL_PSK", "HQ_PREFILL_SK"})
+    if (env_set(e)) return c;  // a forced 256-column plan stays
+  const uint32_t cus = (uint32_t)cu_count();
+  const PrefillLaunch t2 = make_launch(8, 1, d, 2);
+  const bool f16 = dtype == HQ_DTYPE_F16;
+  const bool one_round = t2.tiles <= 2u * cus;
+  // In place of 64-row tiles only while the 128-row bands add at most a quarter more rows
+  // (M = 136..192 would compute up to a third more).
+  // Ternary fp16 over one band of rows keeps its two bands of 64 (measured 4% faster there).
+  const bool rows_ok = 8u * ((d.M + 127u) / 128u) <= 5u * ((d.M + 63u) / 64u) &&
+                       !(fmt == HQ_FORMAT_TERNARY2 && f16 && d.M <= 128u);
+  const bool use = (l.RT == 4 && l.WM == 1 && one_round && rows_ok) || (l.KS == 2 && f16 && one_round) ||
+                   (!f16 && l.RT == 8 && l.WM == 1 && l.KS == 1 && l.tiles > cus && 4u * t2.tiles <= 11u * cus);
+  if (use) l = t2;
   return c;
 }
 

@@ -868,21 +868,96 @@ def test_prefill_k_split_in_workgroup(cuda, fmt, xdt, M, K, N):
 
 
 def test_prefill_k_split_fused_default_plan(cuda):
-    # Fused QKV shape of the split-fuse step (M = 1024, N = 5120 | 1024 | 1024): 224 tiles take
-    # the K split by default (on a 256-CU part).
+    # Fused QKV shape of the split-fuse step (M = 1024, N = 5120 | 1024 | 1024): 224 256-column
+    # tiles would take the K split; with fp16 activations 448 128-column tiles run by default
+    # (on a 256-CU part), the K split itself forced here.
     Ns, K, M = [5120, 1024, 1024], 5120, 1024
     probs = [O.Problem(O.INT4, M, K, n, 128, O.F16, seed=2760 + i) for i, n in enumerate(Ns)]
     for p in probs[1:]:
         p.X = probs[0].X
     devs = [DeviceProblem(p) for p in probs]
     segs = [(d.Wp, d.S, d.P.N) for d in devs]
-    outs = hq.gemm_fused(O.INT4, devs[0].X, segs)
+    with prefill_env(KS=2, WM=1):
+        outs = hq.gemm_fused(O.INT4, devs[0].X, segs)
     with prefill_env(KS=1, SK=0, TAIL=0):
         ref_outs = hq.gemm_fused(O.INT4, devs[0].X, segs)
     rows = np.sort(np.random.default_rng(5).choice(M, size=12, replace=False))
     for d, y, y1 in zip(devs, outs, ref_outs):
         assert normwise_between(y, y1) <= 2 * 2.0**-11
         assert O.normwise_error(to_host_f32(y)[rows], d.P.reference(rows=rows, threads=16)) <= OUT_TOL[O.F16]
+
+
+# 128-row x 128-column whole tiles (four wavefronts of two column tiles each) against the
+# 256-column tiles: the same values up to fp32 summation order (each output's k order is the
+# same, so in practice equal), bit-reproducible, and the oracle's. Ragged M and N (wavefronts
+# past N, partial last bands), the column tiles of fused segments, every format and dtype.
+@pytest.mark.parametrize("fmt,xdt,M,K,N", [
+    (O.INT4, O.F16, 300, 2048, 1000),
+    (O.INT4, O.BF16, 129, 1024, 4000),
+    (O.TERNARY2, O.F16, 200, 4096, 720),
+    (O.TERNARY2, O.BF16, 1000, 1024, 2600),
+    (O.INT4, O.F16, 1024, 5120, 7168),
+])
+def test_prefill_128_column_tiles(cuda, fmt, xdt, M, K, N):
+    P = O.Problem(fmt, M, K, N, 128, xdt, seed=2790 + M)
+    D = DeviceProblem(P)
+    with prefill_env(TW=2, WM=1, SK=0, TAIL=0):
+        desc = hq.describe(fmt, xdt, M, K, N)
+        assert "128-row 128-column tiles" in desc, desc
+        y = D.run()
+        assert torch_equal(y, D.run())
+    with prefill_env(KS=1, WM=1, SK=0, TAIL=0):
+        y1 = D.run()
+    assert normwise_between(y, y1) <= 2 * (2.0**-11 if xdt == O.F16 else 2.0**-8)
+    if M * K * N <= 4e9:
+        check(y, P.reference(), xdt, f"128-column tiles fmt={fmt} M={M} K={K} N={N}", P)
+    else:
+        rows = np.sort(np.random.default_rng(M).choice(M, size=16, replace=False))
+        assert O.normwise_error(to_host_f32(y)[rows], P.reference(rows=rows, threads=16)) <= OUT_TOL[xdt]
+
+
+def test_prefill_128_column_tiles_fused(cuda):
+    # Fused segments whose widths are not multiples of 128 columns (each segment starts a new
+    # column block).
+    Ns, K, M = [600, 130, 1000], 1024, 300
+    probs = [O.Problem(O.INT4, M, K, n, 128, O.F16, seed=2795 + i) for i, n in enumerate(Ns)]
+    for p in probs[1:]:
+        p.X = probs[0].X
+    devs = [DeviceProblem(p) for p in probs]
+    with prefill_env(TW=2, WM=1, SK=0, TAIL=0):
+        outs = hq.gemm_fused(O.INT4, devs[0].X, [(d.Wp, d.S, d.P.N) for d in devs])
+    for d, y in zip(devs, outs):
+        check(y, d.P.reference(), O.F16, f"128-column tiles fused N={d.P.N}", d.P)
+
+
+# The default plans that take 128-column tiles (asserted on 256-CU devices) and neighbours
+# that keep 256-column tiles; rows at every band boundary against the oracle.
+@pytest.mark.parametrize("fmt,xdt,M,K,N,tw2", [
+    (O.INT4, O.BF16, 768, 5120, 7168, True),       # in place of 336 64-row tiles
+    (O.TERNARY2, O.F16, 384, 4096, 11008, True),    # in place of 258 64-row tiles
+    (O.INT4, O.F16, 704, 5120, 7168, True),         # 128-row bands 64 rows taller than 64-row ones
+    (O.INT4, O.F16, 192, 5120, 36864, False),       # 432 64-row tiles stay (576 128-column tiles)
+    (O.INT4, O.F16, 128, 5120, 27648, True),        # one band of 128 rows in place of two of 64
+    (O.TERNARY2, O.F16, 128, 5120, 27648, False),   # ... except ternary fp16
+    (O.TERNARY2, O.BF16, 512, 5120, 17408, True),   # bf16 in place of 272 128-row tiles
+    (O.INT4, O.F16, 512, 5120, 17408, False),       # fp16 keeps them
+    (O.TERNARY2, O.F16, 1024, 5120, 7168, True),    # fp16 in place of the K split
+    (O.TERNARY2, O.BF16, 1024, 5120, 7168, False),  # bf16 keeps it
+    (O.INT4, O.BF16, 768, 5120, 12288, True),       # bf16 in place of 288 128-row tiles
+    (O.INT4, O.F16, 1024, 27648, 5120, False),      # stream-K over a long K stays
+])
+def test_prefill_128_column_tiles_default_plan(cuda, fmt, xdt, M, K, N, tw2):
+    import torch
+
+    desc = hq.describe(fmt, xdt, M, K, N)
+    if torch.cuda.get_device_properties(0).multi_processor_count == 256:
+        assert ("128-column" in desc) == tw2, desc
+    P = O.Problem(fmt, M, K, N, 128, xdt, seed=4250 + M)
+    y = to_host_f32(DeviceProblem(P).run())
+    rows = np.array(sorted(r for r in {0, 1, 63, 64, 127, 128, 129, M // 2, M - 2, M - 1} if r < M))
+    ref = P.reference(rows=rows, threads=16)
+    assert O.normwise_error(y[rows], ref) <= OUT_TOL[xdt], desc
+    elementwise_bound_check(y[rows], ref, P, rows=rows)
 
 
 # Forced stream-K grids on 15 tiles of 64 rows x 256 columns, K = 1024 (8 k-blocks):
