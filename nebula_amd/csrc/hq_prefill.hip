@@ -142,8 +142,11 @@ __global__ void __launch_bounds__(256 * WM * KS, WM == 1 && RT == 8 && KS == 1 ?
   constexpr uint32_t kWavePart = RT * kTilesPerWave * 1024u;  // one wavefront's share of it
   // The explicit order holds more values live; the fp16 128-row kernels make room for it with
   // a weight ring of two k-blocks (one ahead: a k-block's MFMAs outlast a load's latency).
+  // 128-column tiles keep the compiler's order (the explicit one, scaled to two column tiles,
+  // measured 6-13% slower) with a ring of two k-blocks (three: 1-3.5% slower, int4 fp16 within
+  // 0.5%).
   constexpr bool kOrdered = DT == HQ_DTYPE_F16 && RT == 8 && !GEN && TW == 4;
-  constexpr int kRing = kOrdered ? 2 : 3;
+  constexpr int kRing = kOrdered || TW == 2 ? 2 : 3;
   // Partial tiles are stored and loaded with the sc1 cache policy: agent-coherent, so a
   // store that has completed is visible to loads from any XCD.
   constexpr int kCoherent = 16;
