@@ -942,10 +942,11 @@ bool env_set(const char* name) {
 // halves the CU holds two independent tiles. The choice depends on the activation type (the
 // fp16 256-column kernel runs an explicit instruction order, the bf16 one forms its weights
 // in fp32) but not the workspace: every plan it swaps needs none. Measured on MI355X (best of
-// two alternated runs, K = 4096..5120, M = 128..1536):
-//  * in place of 64-row whole tiles (216-344): 10-17% faster for int4 fp16 (5120 x 7168
-//    M = 768 79.6 -> 68.9 us), 12-28% for bf16, 5-7% for ternary fp16 from two bands of 128
-//    rows (5120 x 27648 at M = 128: 4-5% slower);
+// two alternated runs, K = 4096..5120, M = 81..1536):
+//  * in place of 64-row whole tiles (216-344): 8-18% faster for int4 fp16 (5120 x 7168
+//    M = 768 79.6 -> 68.9 us), 7-30% for bf16 (5120 x 34816 M = 96 104.6 -> 80.5 us), 5-11%
+//    for ternary fp16 where the 64-row tiles outnumber the CUs (216 tiles at 5120 x 27648:
+//    -4..+2%);
 //  * in place of the K split (192-256 tiles): fp16 3-6% faster (the fused QKV width at M =
 //    1024, int4: 72.8 -> 68.8 us), bf16 within -4..+2%;
 //  * in place of 272-336 128-row whole tiles (544-672 128-column tiles): bf16 8-11% faster,
@@ -960,7 +961,7 @@ PrefillConfig choose_prefill(int fmt, const GemmDesc& d, size_t ws_cap, int dtyp
     if (l.RT == 8 && l.WM == 1) l = make_launch(8, 1, d, 2);
     return c;
   }
-  if (etw == 1 || d.M < 128u || l.psk != 0 || l.dp != l.tiles) return c;
+  if (etw == 1 || d.M <= 64u || l.psk != 0 || l.dp != l.tiles) return c;
   for (const char* e : {"HQ_PREFILL_RT", "HQ_PREFILL_WM", "HQ_PREFILL_KS", "HQ_PREFILL_PSK", "HQ_PREFILL_SK"})
     if (env_set(e)) return c;  // a forced 256-column plan stays
   const uint32_t cus = (uint32_t)cu_count();
@@ -969,9 +970,10 @@ PrefillConfig choose_prefill(int fmt, const GemmDesc& d, size_t ws_cap, int dtyp
   const bool one_round = t2.tiles <= 2u * cus;
   // In place of 64-row tiles only while the 128-row bands add at most a quarter more rows
   // (M = 136..192 would compute up to a third more).
-  // Ternary fp16 over one band of rows keeps its two bands of 64 (measured 4% faster there).
+  // Ternary fp16 keeps 64-row tiles that all fit one per CU (5120 x 27648 at M = 81..128, 216
+  // tiles: 4% faster than 128-column tiles at M = 128, within 2% below).
   const bool rows_ok = 8u * ((d.M + 127u) / 128u) <= 5u * ((d.M + 63u) / 64u) &&
-                       !(fmt == HQ_FORMAT_TERNARY2 && f16 && d.M <= 128u);
+                       !(fmt == HQ_FORMAT_TERNARY2 && f16 && l.tiles <= cus);
   const bool use = (l.RT == 4 && l.WM == 1 && one_round && rows_ok) || (l.KS == 2 && f16 && one_round) ||
                    (!f16 && l.RT == 8 && l.WM == 1 && l.KS == 1 && l.tiles > cus && 4u * t2.tiles <= 11u * cus);
   if (use) l = t2;

@@ -938,7 +938,10 @@ def test_prefill_128_column_tiles_fused(cuda):
     (O.INT4, O.F16, 704, 5120, 7168, True),         # 128-row bands 64 rows taller than 64-row ones
     (O.INT4, O.F16, 192, 5120, 36864, False),       # 432 64-row tiles stay (576 128-column tiles)
     (O.INT4, O.F16, 128, 5120, 27648, True),        # one band of 128 rows in place of two of 64
-    (O.TERNARY2, O.F16, 128, 5120, 27648, False),   # ... except ternary fp16
+    (O.TERNARY2, O.F16, 128, 5120, 27648, False),   # ... except ternary fp16 at 216 tiles
+    (O.TERNARY2, O.F16, 112, 5120, 34816, True),    # ... which takes them at 272
+    (O.INT4, O.BF16, 96, 5120, 34816, True),        # M = 81..127: one band of 128 rows
+    (O.INT4, O.F16, 96, 5120, 14336, False),        # stream-K of 64-row tiles stays
     (O.TERNARY2, O.BF16, 512, 5120, 17408, True),   # bf16 in place of 272 128-row tiles
     (O.INT4, O.F16, 512, 5120, 17408, False),       # fp16 keeps them
     (O.TERNARY2, O.F16, 1024, 5120, 7168, True),    # fp16 in place of the K split
