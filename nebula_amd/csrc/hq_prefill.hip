@@ -950,7 +950,9 @@ bool env_set(const char* name) {
 //  * in place of the K split (192-256 tiles): fp16 3-6% faster (the fused QKV width at M =
 //    1024, int4: 72.8 -> 68.8 us), bf16 within -4..+2%;
 //  * in place of 272-336 128-row whole tiles (544-672 128-column tiles): bf16 8-11% faster,
-//    fp16 6-13% slower; bf16 at 408 (816) 8% slower.
+//    also over a long K (27648 x 5120, 17408 x 5120, 16384 x 6144, 8192 x 8192 at M = 1152..
+//    2048: 8-13%), fp16 6-13% slower; bf16 at 408 (816) 8% slower, at 432-1728 (864-3456) up
+//    to 11% slower.
 // Stream-K plans (short grids, long K) stay: 128-column tiles there were 1-40% slower.
 PrefillConfig choose_prefill(int fmt, const GemmDesc& d, size_t ws_cap, int dtype) {
   PrefillConfig c = choose_prefill_256(fmt, d, ws_cap);
