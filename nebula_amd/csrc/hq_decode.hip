@@ -1103,8 +1103,12 @@ XrConfig choose_decode_xr(int fmt, const GemmDesc& d, size_t ws_cap) {
   // one-round grid (at most one workgroup per CU) that keeps the most CUs busy, the fewest
   // pieces among equals. Measured on MI355X (alternated runs), 27648 x 5120: M = 4 16.3 us with
   // 4-tile slabs in three pieces (240 workgroups) against 16.8 in two (160); M = 8 17.1 against
-  // 17.2 for the lockstep kernel.
-  if (!found && !forced && xr_x_bytes(d, 1) > kXrLdsMax && d.M <= 8u) {
+  // 17.2 for the lockstep kernel. Ternary weights over a long K (192 k-blocks or more) take the
+  // pieces also where the rows fit but 2-tile slabs would leave CUs idle: 27648 x 5120 at M = 1,
+  // 2 12.6-12.8 us in three pieces against 13.9-14.2 for 160 whole slabs, 24576 x 5120 at M =
+  // 1..3 8-11% faster (int4 2-3% slower; 17408 x 5120 within 2%, shorter K 4-27% slower).
+  const bool tern_long = fmt == HQ_FORMAT_TERNARY2 && d.nkb >= 192u && tiles > cus && total_slabs(d, 2) < cus;
+  if (!found && !forced && (xr_x_bytes(d, 1) > kXrLdsMax || tern_long) && d.M <= 8u) {
     uint32_t best = 0;
     for (int s = 2; s <= 8; ++s) {
       if ((uint32_t)s > d.nkb || xr_x_bytes(d, s) > kXrLdsMax) continue;

@@ -478,6 +478,10 @@ def test_slab_groups_planned_by_slabs_per_cu(fmt, dt, M, slabs, sg):
     (hq.FORMAT_TERNARY2, hq.DTYPE_BF16, 8, 4096, 11008, "T=4,U=2> workgroups=172 slabs x 1 pieces x 8 wavefronts"),
     # ... while 2-tile slabs one to a CU stay (5120 x 7168: 224 slabs)
     (hq.FORMAT_INT4, hq.DTYPE_F16, 4, 5120, 7168, "T=2,U=3> workgroups=224 slabs x 1 pieces x 8 wavefronts"),
+    # ternary over a long K: K pieces also where the rows fit (int4 and a shorter K keep whole slabs)
+    (hq.FORMAT_TERNARY2, hq.DTYPE_BF16, 1, 27648, 5120, "T=4,U=2> workgroups=80 slabs x 3 pieces x 8 wavefronts"),
+    (hq.FORMAT_INT4, hq.DTYPE_F16, 1, 27648, 5120, "T=2,U=3> workgroups=160 slabs x 1 pieces x 8 wavefronts"),
+    (hq.FORMAT_TERNARY2, hq.DTYPE_F16, 2, 17408, 5120, "T=2,U=3> workgroups=160 slabs x 1 pieces x 8 wavefronts"),
 ])
 def test_decode_plans_by_tile_count(fmt, dt, M, K, N, want):
     # The planner's tile-count rules on a 256-CU device (the count the library assumes without

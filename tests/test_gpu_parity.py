@@ -729,10 +729,13 @@ def test_xr_pieces_default_plans(cuda, M):
     (O.INT4, O.F16, 16, 14336, 1024, "T=1,U=4> workgroups=64 slabs x 3 pieces"),
     (O.INT4, O.F16, 1, 4096, 14336, "T=4,U=2> workgroups=224 slabs x 1 pieces x 8 wavefronts"),
     (O.TERNARY2, O.BF16, 4, 4096, 11008, "T=4,U=2> workgroups=172 slabs x 1 pieces x 8 wavefronts"),
+    (O.TERNARY2, O.BF16, 1, 27648, 5120, "T=4,U=2> workgroups=80 slabs x 3 pieces x 8 wavefronts"),
+    (O.TERNARY2, O.F16, 2, 27648, 5120, "T=4,U=2> workgroups=80 slabs x 3 pieces x 8 wavefronts"),
 ])
 def test_xr_default_plans_by_tile_count(cuda, fmt, xdt, M, K, N, plan):
     # Few tiles (GQA key/value widths): one-tile slabs, whole or in K pieces; 4-tile slabs one
-    # to a CU where 2-tile slabs would take two (plans asserted on 256-CU devices).
+    # to a CU where 2-tile slabs would take two; ternary over a long K in K pieces at one or two
+    # rows (plans asserted on 256-CU devices).
     import torch
 
     desc = hq.describe(fmt, xdt, M, K, N)
