@@ -10,7 +10,7 @@
 // one extra MFMA per chunk whose result seeds every tile's accumulator; the group scale
 // multiplies the fp32 k-block sum once per (column, k-block).
 //   * hq_decode_xr_kernel, the default for M <= 16: one workgroup per (slab of T column
-//     tiles, piece of K), or per pair of whole slabs; the piece's activation rows are copied
+//     tiles, piece of K), or per group of two to four whole slabs; the activation rows are copied
 //     into LDS once, then the wavefronts stream the slab's weights through a barrier-free
 //     register ring and meet once, at the end, in LDS (pieces of a slab: a last-arriver
 //     fix-up in piece order);
